@@ -1,0 +1,122 @@
+"""Host-side mirror of the busfill C-ABI (``include/busfill.h``).
+
+Loads ``bus-fill_amd/lib/libbusfill.so`` with ctypes and exposes the entry
+points on device tensors.  PyTorch is used only to own device memory and to
+name the HIP stream; every kernel that runs is in libbusfill.  There is no
+fallback: if the library is missing, importing the loader raises.
+
+Reference interface mirrored: the kernel symbol ``busfill_q4(A, Wq, Ws, C, Bsz,
+K, N)`` of kernels/busfill_v1a.cu:41-46, launched at :154,169; here
+``busfill_q4(...)`` keeps that argument order and meaning and adds the stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libbusfill.so")
+HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "busfill.h")
+
+# bf_status
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
+# bf_qtype
+Q4_0, Q4_0_PLANES, Q4_K = 0, 1, 2
+# bf_otype
+OUT_F32, OUT_F16 = 0, 1
+# bf_algo
+ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE = 0, 1, 2, 3
+
+EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_dequant_f16",
+           "bf_status_str", "bf_last_error", "bf_version")
+
+
+class BusfillError(RuntimeError):
+    def __init__(self, status: int, where: str, detail: str):
+        self.status = status
+        super().__init__(f"{where}: status {status} ({detail})")
+
+
+class BusfillInvalid(BusfillError, ValueError):
+    pass
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libbusfill.so (raises FileNotFoundError if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(f"{LIB_PATH} is missing: run `python bus-fill_amd/build.py` "
+                                    "(or __graft_entry__.build()) first")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i = ctypes.c_void_p, ctypes.c_int
+        L.bf_busfill_q4.argtypes = [vp, vp, vp, vp, i, i, i, vp]
+        L.bf_gemm.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
+        L.bf_gemm_ex.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, i, vp]
+        L.bf_dequant_f16.argtypes = [i, vp, vp, vp, i, i, vp]
+        for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_dequant_f16"):
+            getattr(L, f).restype = i
+        L.bf_status_str.argtypes = [i]
+        L.bf_status_str.restype = ctypes.c_char_p
+        L.bf_last_error.restype = ctypes.c_char_p
+        L.bf_version.restype = i
+        _lib = L
+    return _lib
+
+
+def _check(status: int, where: str) -> None:
+    if status != OK:
+        detail = lib().bf_last_error().decode() or lib().bf_status_str(status).decode()
+        cls = BusfillInvalid if status == ERR_INVALID else BusfillError
+        raise cls(status, where, detail)
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def gemm(qtype: int, W, W_aux, A, C, M: int, N: int, K: int, *, lda: int | None = None,
+         ldc: int | None = None, otype: int = OUT_F32, algo: int = ALGO_AUTO, stream=None) -> None:
+    """C[M][N] = A[M][K] . dequant(W)^T on the GPU (all arguments device tensors
+    or raw device addresses; C is overwritten)."""
+    st = lib().bf_gemm_ex(qtype, _ptr(W), _ptr(W_aux), _ptr(A), K if lda is None else lda,
+                          _ptr(C), N if ldc is None else ldc, otype, M, N, K, algo, _stream(stream))
+    _check(st, "bf_gemm_ex")
+
+
+def busfill_q4(A, Wq, Ws, C, Bsz: int, K: int, N: int, stream=None) -> None:
+    """Reference-compatible call: Q4_0 planes, fp32 C[Bsz][N]."""
+    _check(lib().bf_busfill_q4(_ptr(A), _ptr(Wq), _ptr(Ws), _ptr(C), Bsz, K, N, _stream(stream)),
+           "bf_busfill_q4")
+
+
+def dequant_f16(qtype: int, W, W_aux, out, N: int, K: int, stream=None) -> None:
+    """out[N][K] (fp16 bits) = bit-exact dequant of W."""
+    _check(lib().bf_dequant_f16(qtype, _ptr(W), _ptr(W_aux), _ptr(out), N, K, _stream(stream)),
+           "bf_dequant_f16")
+
+
+def version() -> int:
+    return int(lib().bf_version())
+
+
+def weight_bytes(N: int, K: int) -> int:
+    """Bytes streamed for one N x K matrix: 4.5 bits/weight in all three formats."""
+    return N * K * 9 // 16

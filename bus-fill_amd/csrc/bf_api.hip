@@ -1,0 +1,162 @@
+// C-ABI front end of libbusfill: validation, dispatch, error reporting.
+// Declarations and the reference interfaces they replace: include/busfill.h.
+#include "busfill.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "bf_device.h"
+#include "bf_launch.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+bf_status fail(bf_status st, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+    va_end(ap);
+    return st;
+}
+
+bf_status from_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return BF_OK;
+    return fail(BF_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+constexpr int kMaxMPerLaunch = 128;   // MFMA kernels cover up to 8 batch tiles of 16
+constexpr int kDot2MaxM = 4;          // crossover dot2 -> MFMA (see the batch sweep)
+
+bf_status check_weights(bf_qtype qt, const void* W, const void* W_aux, int N, int K) {
+    if (qt != BF_Q4_0 && qt != BF_Q4_0_PLANES && qt != BF_Q4_K)
+        return fail(BF_ERR_INVALID, "unknown qtype %d", (int)qt);
+    if (!W) return fail(BF_ERR_INVALID, "W is NULL");
+    if (qt == BF_Q4_0_PLANES) {
+        if (!W_aux) return fail(BF_ERR_INVALID, "W_aux (Ws scale plane) is NULL for BF_Q4_0_PLANES");
+        if (!aligned(W_aux, 2)) return fail(BF_ERR_INVALID, "Ws is not 2-byte aligned");
+    } else if (W_aux) {
+        return fail(BF_ERR_INVALID, "W_aux must be NULL for qtype %d", (int)qt);
+    }
+    if (N < 1 || K < 1) return fail(BF_ERR_INVALID, "N=%d K=%d must be >= 1", N, K);
+    if (qt == BF_Q4_K && K % 256 != 0) return fail(BF_ERR_INVALID, "K=%d is not a multiple of 256 (Q4_K)", K);
+    if (K % 32 != 0) return fail(BF_ERR_INVALID, "K=%d is not a multiple of 32", K);
+    if (qt == BF_Q4_0 && !aligned(W, 2)) return fail(BF_ERR_INVALID, "W is not 2-byte aligned");
+    return BF_OK;
+}
+
+bool fast_eligible(const bf::GemmArgs& g) {
+    if (g.K % 256 != 0) return false;
+    if (!aligned(g.A, 16) || g.lda % 8 != 0) return false;
+    if (!aligned(g.W, 16)) return false;
+    if (g.qtype == bf::QT_PLANES && !aligned(g.Waux, 4)) return false;
+    return true;
+}
+
+bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
+                   int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream) {
+    g_last_error[0] = '\0';
+    bf_status st = check_weights(qtype, W, W_aux, N, K);
+    if (st != BF_OK) return st;
+    if (!A || !C) return fail(BF_ERR_INVALID, "A or C is NULL");
+    if (M < 1) return fail(BF_ERR_INVALID, "M=%d must be >= 1", M);
+    if (lda < K) return fail(BF_ERR_INVALID, "lda=%d < K=%d", lda, K);
+    if (ldc < N) return fail(BF_ERR_INVALID, "ldc=%d < N=%d", ldc, N);
+    if (otype != BF_OUT_F32 && otype != BF_OUT_F16) return fail(BF_ERR_INVALID, "unknown otype %d", (int)otype);
+    if (!aligned(A, 2)) return fail(BF_ERR_INVALID, "A is not 2-byte aligned");
+    if (!aligned(C, otype == BF_OUT_F32 ? 4 : 2)) return fail(BF_ERR_INVALID, "C is not aligned to its element");
+    if (algo < BF_ALGO_AUTO || algo > BF_ALGO_SIMPLE) return fail(BF_ERR_INVALID, "unknown algo %d", (int)algo);
+
+    const size_t csize = otype == BF_OUT_F32 ? 4 : 2;
+    hipStream_t hs = (hipStream_t)stream;
+    for (int m0 = 0; m0 < M; m0 += kMaxMPerLaunch) {
+        bf::GemmArgs g;
+        g.qtype = (int)qtype;
+        g.W = (const uint8_t*)W;
+        g.Waux = (const uint8_t*)W_aux;
+        g.A = A + (int64_t)m0 * lda;
+        g.lda = lda;
+        g.C = (char*)C + (size_t)m0 * ldc * csize;
+        g.ldc = ldc;
+        g.out_f16 = otype == BF_OUT_F16;
+        g.M = M - m0 < kMaxMPerLaunch ? M - m0 : kMaxMPerLaunch;
+        g.N = N;
+        g.K = K;
+
+        bf_algo use = algo;
+        const bool fast = fast_eligible(g);
+        if (use == BF_ALGO_AUTO) {
+            if (!fast) use = BF_ALGO_SIMPLE;
+            else if (g.M <= kDot2MaxM && bf::dot2_supports(g)) use = BF_ALGO_DOT2;
+            else use = BF_ALGO_MFMA;
+        }
+        hipError_t e;
+        switch (use) {
+            case BF_ALGO_MFMA:
+                if (!fast) return fail(BF_ERR_UNSUPPORTED, "MFMA path needs K %% 256 == 0, 16-byte aligned A/W, lda %% 8 == 0");
+                e = bf::gemm_mfma(g, hs);
+                break;
+            case BF_ALGO_DOT2:
+                if (!fast || !bf::dot2_supports(g))
+                    return fail(BF_ERR_UNSUPPORTED, "dot2 path does not serve M=%d K=%d with these alignments", g.M, K);
+                e = bf::gemm_dot2(g, hs);
+                break;
+            default:
+                e = bf::gemm_simple(g, hs);
+                break;
+        }
+        st = from_hip(e, "kernel launch");
+        if (st != BF_OK) return st;
+    }
+    return BF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+bf_status bf_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C, int ldc,
+                  bf_otype otype, int M, int N, int K, void* stream) {
+    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, BF_ALGO_AUTO, stream);
+}
+
+bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
+                     int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream) {
+    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, algo, stream);
+}
+
+bf_status bf_busfill_q4(const uint16_t* A, const uint8_t* Wq, const uint16_t* Ws, float* C, int Bsz, int K, int N,
+                        void* stream) {
+    return run_gemm(BF_Q4_0_PLANES, Wq, Ws, A, K, C, N, BF_OUT_F32, Bsz, N, K, BF_ALGO_AUTO, stream);
+}
+
+bf_status bf_dequant_f16(bf_qtype qtype, const void* W, const void* W_aux, uint16_t* W_f16, int N, int K,
+                         void* stream) {
+    g_last_error[0] = '\0';
+    bf_status st = check_weights(qtype, W, W_aux, N, K);
+    if (st != BF_OK) return st;
+    if (!W_f16) return fail(BF_ERR_INVALID, "W_f16 is NULL");
+    if (!aligned(W_f16, 2)) return fail(BF_ERR_INVALID, "W_f16 is not 2-byte aligned");
+    return from_hip(bf::dequant_f16((int)qtype, (const uint8_t*)W, (const uint8_t*)W_aux, W_f16, N, K,
+                                    (hipStream_t)stream),
+                    "dequant launch");
+}
+
+const char* bf_status_str(bf_status s) {
+    switch (s) {
+        case BF_OK: return "BF_OK";
+        case BF_ERR_INVALID: return "BF_ERR_INVALID";
+        case BF_ERR_UNSUPPORTED: return "BF_ERR_UNSUPPORTED";
+        case BF_ERR_HIP: return "BF_ERR_HIP";
+    }
+    return "BF_UNKNOWN_STATUS";
+}
+
+const char* bf_last_error(void) { return g_last_error; }
+
+int bf_version(void) { return 100; }
+
+}  // extern "C"

@@ -1,0 +1,29 @@
+// Host-side interface between the C-ABI front end (bf_api.hip) and the kernel
+// families.  Arguments are validated by the front end before any of these runs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bf {
+
+struct GemmArgs {
+    int qtype;                 // QT_Q4_0 / QT_PLANES / QT_Q4_K
+    const uint8_t* W;          // block bytes, or the Wq code plane
+    const uint8_t* Waux;       // Ws scale plane (planes layout) or nullptr
+    const uint16_t* A;         // [M][lda] fp16
+    int lda;
+    void* C;                   // [M][ldc] fp32 or fp16
+    int ldc;
+    int out_f16;
+    int M, N, K;               // M <= 128 per launch (the front end slices larger M)
+};
+
+hipError_t gemm_mfma(const GemmArgs& g, hipStream_t st);
+hipError_t gemm_dot2(const GemmArgs& g, hipStream_t st);
+hipError_t gemm_simple(const GemmArgs& g, hipStream_t st);
+bool dot2_supports(const GemmArgs& g);
+hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
+                       int N, int K, hipStream_t st);
+
+}  // namespace bf

@@ -1,0 +1,104 @@
+/*
+ * busfill -- MI355X (gfx950) batched int4-block-weight x fp16-activation GEMM.
+ *
+ * C-ABI drop-in for the reference kernel's call surface
+ *   extern "C" __global__ void busfill_q4(const __half* A, const uint8_t* Wq,
+ *                                        const __half* Ws, float* C,
+ *                                        int Bsz, int K, int N)
+ *   (kernels/busfill_v1a.cu:41-46, launched <<<N/32,128>>> at :151,154,169).
+ * The reference has no library or FFI: its harness main() launches that symbol
+ * directly.  Every entry point below replaces that launch (or, for the Q4_K and
+ * llama.cpp-block formats, the dequantize-then-matmul the reference only
+ * describes in RESULTS.md:84-96) with a host-callable function.
+ *
+ * Conventions
+ *   - All pointers are DEVICE pointers owned by the caller; nothing is allocated.
+ *   - fp16 values travel as uint16_t bit patterns.
+ *   - A is [M][lda] row-major fp16, C is [M][ldc] row-major (fp32 or fp16),
+ *     W is [N][K] in the chosen block format: C = A . dequant(W)^T.
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Calls only enqueue
+ *     work; they are asynchronous with respect to the host.
+ *   - Shapes, alignments and pointers are validated before anything is
+ *     enqueued; a rejected call returns BF_ERR_INVALID and touches nothing.
+ *   - The library holds no global mutable state apart from a thread-local
+ *     text of the last error (bf_last_error).
+ */
+#ifndef BUSFILL_H
+#define BUSFILL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    BF_OK = 0,
+    BF_ERR_INVALID = 1,      /* bad shape, pointer, alignment or enum */
+    BF_ERR_UNSUPPORTED = 2,  /* valid request this build cannot serve */
+    BF_ERR_HIP = 3           /* the HIP runtime reported an error on launch */
+} bf_status;
+
+typedef enum {
+    BF_Q4_0 = 0,         /* llama.cpp block_q4_0: {fp16 d; u8 qs[16]} = 18 B / 32 weights,
+                            elem j = qs[j] & 0xF, elem j+16 = qs[j] >> 4, value (q-8)*d     */
+    BF_Q4_0_PLANES = 1,  /* reference layout (kernels/busfill_v0.cu:42-44,119-123):
+                            Wq[N][K/2] u8, byte j = elems 2j (lo) and 2j+1 (hi);
+                            Ws[N][K/32] fp16 (passed as W_aux); value (q-8)*d              */
+    BF_Q4_K = 2          /* llama.cpp block_q4_K: {fp16 d, dmin; u8 scales[12]; u8 qs[128]}
+                            = 144 B / 256 weights; value (d*sc)*q - dmin*m                 */
+} bf_qtype;
+
+typedef enum { BF_OUT_F32 = 0, BF_OUT_F16 = 1 } bf_otype;
+
+typedef enum {
+    BF_ALGO_AUTO = 0,    /* pick by shape and M                                        */
+    BF_ALGO_MFMA = 1,    /* v_mfma_f32_16x16x32_f16 over 16-row batch tiles            */
+    BF_ALGO_DOT2 = 2,    /* v_dot2_f32_f16 lanes + cross-lane reduction (small M)      */
+    BF_ALGO_SIMPLE = 3   /* one thread per output; any legal shape (slow, for odd K)   */
+} bf_algo;
+
+/* Reference-compatible entry: Q4_0 planes, fp32 output, C[Bsz][N] overwritten.
+ * Replaces the busfill_q4<<<N/32,128>>> launch of kernels/busfill_v1a.cu:154,169
+ * (same argument meaning and order, plus the stream).  Unlike the reference it
+ * checks its preconditions (K % 32 == 0, Bsz >= 1, non-null pointers) and has no
+ * Bsz <= 32 limit (kernels/busfill_v1a.cu:55-56 silently dropped rows >= 32). */
+bf_status bf_busfill_q4(const uint16_t* A, const uint8_t* Wq, const uint16_t* Ws, float* C,
+                        int Bsz, int K, int N, void* stream);
+
+/* General GEMM: C[M][N] (ldc) = A[M][K] (lda) . dequant(W)^T.
+ * W_aux is Ws for BF_Q4_0_PLANES and must be NULL otherwise.
+ * Requirements: M, N >= 1; K % 32 == 0 (K % 256 == 0 for BF_Q4_K); lda >= K;
+ * ldc >= N.  Fast paths additionally use 16-byte aligned A with lda % 8 == 0,
+ * 16-byte aligned W and K % 256 == 0; other legal inputs run BF_ALGO_SIMPLE.
+ * Replaces the reference's fused dequant+mma kernel (kernels/busfill_v1a.cu:41-104)
+ * and, for Q4_K, its described dequantize-then-matmul (RESULTS.md:84-96). */
+bf_status bf_gemm(bf_qtype qtype, const void* W, const void* W_aux,
+                  const uint16_t* A, int lda, void* C, int ldc, bf_otype otype,
+                  int M, int N, int K, void* stream);
+
+/* bf_gemm with an explicit kernel family (for tests and the crossover sweep).
+ * Returns BF_ERR_UNSUPPORTED if that family cannot serve the shape. */
+bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux,
+                     const uint16_t* A, int lda, void* C, int ldc, bf_otype otype,
+                     int M, int N, int K, bf_algo algo, void* stream);
+
+/* Bit-exact fp16 dequant: W_f16[N][K] = RN_fp16(value), value computed in fp32
+ * exactly as kernels/busfill_v0.cu:74,78-81 ((q-8)*fp32(d)) for the Q4_0
+ * formats and as ggml dequantize_row_q4_K ((d*sc)*q - dmin*m) for Q4_K. */
+bf_status bf_dequant_f16(bf_qtype qtype, const void* W, const void* W_aux,
+                         uint16_t* W_f16, int N, int K, void* stream);
+
+/* Static text for a status code. */
+const char* bf_status_str(bf_status status);
+
+/* Detail text for the calling thread's most recent non-OK status ("" if none). */
+const char* bf_last_error(void);
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int bf_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BUSFILL_H */

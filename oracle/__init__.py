@@ -1,0 +1,234 @@
+"""CPU oracle for the batched int4-block-weight x fp16-activation GEMM.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of bench.py, and there only as the checker (or, for the CPU
+baseline, as the host-side thing being timed).  The product path under
+``bus-fill_amd/`` never imports it.
+
+Thin numpy/ctypes front end over ``liboracle.so`` (plain C, ``oracle.c``); each
+C function cites the reference file:line it restates (see ``oracle.h``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+Q4_0 = 0          # llama.cpp block_q4_0, 18 B / 32 weights
+Q4_0_PLANES = 1   # reference planes Wq[N][K/2] u8 + Ws[N][K/32] fp16
+Q4_K = 2          # llama.cpp block_q4_K, 144 B / 256 weights
+
+# value distributions of the benchmark workloads
+Q4_0_SCALE_RANGE = (0.002, 0.02)
+Q4_K_SCALE_RANGE = (0.001, 0.01)
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile (gcc only)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s"] + (["-B"] if force else []) + ["-C", _HERE, "liboracle.so"],
+                       check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        vp, i, u64, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_float
+        L.or_f32_to_f16.argtypes = [f]; L.or_f32_to_f16.restype = ctypes.c_uint16
+        L.or_f16_to_f32.argtypes = [ctypes.c_uint16]; L.or_f16_to_f32.restype = f
+        L.or_f32_to_f16_array.argtypes = [vp, vp, ctypes.c_size_t]
+        L.or_f16_to_f32_array.argtypes = [vp, vp, ctypes.c_size_t]
+        L.or_rand.argtypes = [u64, u64, u64]; L.or_rand.restype = u64
+        L.or_unif_f16.argtypes = [u64, f, f]; L.or_unif_f16.restype = ctypes.c_uint16
+        L.or_gen_q4_0_planes.argtypes = [u64, i, i, f, f, vp, vp]
+        L.or_gen_q4_0_blocks.argtypes = [u64, i, i, f, f, vp]
+        L.or_gen_q4_k.argtypes = [u64, i, i, f, f, vp]
+        L.or_gen_act.argtypes = [u64, i, i, vp]
+        L.or_q4k_get_scale_min.argtypes = [i, vp, vp, vp]
+        L.or_q4k_pack_scales.argtypes = [vp, vp, vp]
+        L.or_q4_0_planes_to_blocks.argtypes = [vp, vp, i, i, vp]
+        L.or_q4_0_blocks_to_planes.argtypes = [vp, i, i, vp, vp]
+        for name in ("or_dequant_f16", "or_dequant_f32"):
+            getattr(L, name).argtypes = [i, vp, vp, i, i, vp]
+            getattr(L, name).restype = i
+        for name in ("or_gemm_f64", "or_gemm_f16w_f64"):
+            getattr(L, name).argtypes = [i, vp, vp, vp, i, i, i, vp, i]
+            getattr(L, name).restype = i
+        L.or_cpu_dequant_matmul.argtypes = [i, vp, vp, vp, i, i, i, vp, vp, i,
+                                            ctypes.POINTER(ctypes.c_double),
+                                            ctypes.POINTER(ctypes.c_double)]
+        L.or_cpu_dequant_matmul.restype = i
+        L.or_max_threads.restype = i
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise ValueError(f"oracle {what} rejected its arguments (rc={rc})")
+
+
+# ---------------------------------------------------------------- fp16
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().or_f32_to_f16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().or_f16_to_f32_array(_p(h), _p(out), h.size)
+    return out
+
+
+# ---------------------------------------------------------------- weights
+class QWeights:
+    """One quantized matrix W[N][K] in one of the three formats (host bytes)."""
+
+    def __init__(self, qtype: int, N: int, K: int, W: np.ndarray, W_aux: np.ndarray | None = None):
+        self.qtype, self.N, self.K, self.W, self.W_aux = qtype, N, K, W, W_aux
+
+    @property
+    def nbytes(self) -> int:
+        return self.W.nbytes + (0 if self.W_aux is None else self.W_aux.nbytes)
+
+
+def weight_bytes(qtype: int, N: int, K: int) -> int:
+    """Bytes of one N x K matrix (4.5 bits per weight for all three formats)."""
+    return N * K * 9 // 16
+
+
+def gen_weights(qtype: int, N: int, K: int, seed: int, scale_range=None) -> QWeights:
+    L = lib()
+    if qtype == Q4_0_PLANES:
+        lo, hi = scale_range or Q4_0_SCALE_RANGE
+        Wq = np.empty((N, K // 2), np.uint8)
+        Ws = np.empty((N, K // 32), np.uint16)
+        L.or_gen_q4_0_planes(seed, N, K, lo, hi, _p(Wq), _p(Ws))
+        return QWeights(qtype, N, K, Wq, Ws)
+    if qtype == Q4_0:
+        lo, hi = scale_range or Q4_0_SCALE_RANGE
+        B = np.empty((N, K // 32 * 18), np.uint8)
+        L.or_gen_q4_0_blocks(seed, N, K, lo, hi, _p(B))
+        return QWeights(qtype, N, K, B)
+    if qtype == Q4_K:
+        lo, hi = scale_range or Q4_K_SCALE_RANGE
+        B = np.empty((N, K // 256 * 144), np.uint8)
+        L.or_gen_q4_k(seed, N, K, lo, hi, _p(B))
+        return QWeights(qtype, N, K, B)
+    raise ValueError(f"unknown qtype {qtype}")
+
+
+def gen_act(M: int, K: int, seed: int) -> np.ndarray:
+    """A[M][K] ~ N(0,1) rounded to fp16 (as uint16 bits)."""
+    A = np.empty((M, K), np.uint16)
+    lib().or_gen_act(seed, M, K, _p(A))
+    return A
+
+
+def planes_to_blocks(w: QWeights) -> QWeights:
+    assert w.qtype == Q4_0_PLANES
+    B = np.empty((w.N, w.K // 32 * 18), np.uint8)
+    lib().or_q4_0_planes_to_blocks(_p(w.W), _p(w.W_aux), w.N, w.K, _p(B))
+    return QWeights(Q4_0, w.N, w.K, B)
+
+
+def blocks_to_planes(w: QWeights) -> QWeights:
+    assert w.qtype == Q4_0
+    Wq = np.empty((w.N, w.K // 2), np.uint8)
+    Ws = np.empty((w.N, w.K // 32), np.uint16)
+    lib().or_q4_0_blocks_to_planes(_p(w.W), w.N, w.K, _p(Wq), _p(Ws))
+    return QWeights(Q4_0_PLANES, w.N, w.K, Wq, Ws)
+
+
+def q4k_get_scale_min(j: int, scales: bytes):
+    s = np.frombuffer(bytes(scales), np.uint8).copy()
+    sc = np.zeros(1, np.uint8); m = np.zeros(1, np.uint8)
+    lib().or_q4k_get_scale_min(j, _p(s), _p(sc), _p(m))
+    return int(sc[0]), int(m[0])
+
+
+def q4k_pack_scales(sc, m) -> bytes:
+    sc = np.ascontiguousarray(sc, np.uint8); m = np.ascontiguousarray(m, np.uint8)
+    out = np.zeros(12, np.uint8)
+    lib().or_q4k_pack_scales(_p(sc), _p(m), _p(out))
+    return out.tobytes()
+
+
+# ---------------------------------------------------------------- dequant / gemm
+def dequant_f16(w: QWeights) -> np.ndarray:
+    """Bit-exact fp16 dequant contract, [N][K] uint16 bits."""
+    out = np.empty((w.N, w.K), np.uint16)
+    _check(lib().or_dequant_f16(w.qtype, _p(w.W), _p(w.W_aux), w.N, w.K, _p(out)), "dequant_f16")
+    return out
+
+
+def dequant_f32(w: QWeights) -> np.ndarray:
+    """Unrounded fp32 dequant (the reference's refW), [N][K]."""
+    out = np.empty((w.N, w.K), np.float32)
+    _check(lib().or_dequant_f32(w.qtype, _p(w.W), _p(w.W_aux), w.N, w.K, _p(out)), "dequant_f32")
+    return out
+
+
+def gemm_f64(w: QWeights, A: np.ndarray, threads: int = 0, round_w: bool = False) -> np.ndarray:
+    """C[M][N] = A . dequant(W)^T accumulated in fp64."""
+    A = np.ascontiguousarray(A, np.uint16)
+    M = A.shape[0]
+    assert A.shape[1] == w.K
+    C = np.empty((M, w.N), np.float64)
+    fn = lib().or_gemm_f16w_f64 if round_w else lib().or_gemm_f64
+    _check(fn(w.qtype, _p(w.W), _p(w.W_aux), _p(A), M, w.N, w.K, _p(C), threads), "gemm_f64")
+    return C
+
+
+def cpu_dequant_matmul(w: QWeights, A: np.ndarray, threads: int = 0, scratch=None):
+    """CPU baseline: full fp32 dequant then fp32-accumulated matmul.
+
+    Returns (C float32 [M][N], t_dequant_s, t_matmul_s)."""
+    A = np.ascontiguousarray(A, np.uint16)
+    M = A.shape[0]
+    if scratch is None or scratch.size < w.N * w.K:
+        scratch = np.empty(w.N * w.K, np.float32)
+    C = np.empty((M, w.N), np.float32)
+    tdq, tmm = ctypes.c_double(), ctypes.c_double()
+    _check(lib().or_cpu_dequant_matmul(w.qtype, _p(w.W), _p(w.W_aux), _p(A), M, w.N, w.K,
+                                       _p(scratch), _p(C), threads,
+                                       ctypes.byref(tdq), ctypes.byref(tmm)), "cpu_dequant_matmul")
+    return C, tdq.value, tmm.value
+
+
+def max_threads() -> int:
+    return int(lib().or_max_threads())
+
+
+def gate(C, C_ref, max_abs: float = 0.6, rel_frob: float = 1e-3):
+    """The GEMM acceptance gate: every value finite, max |C - ref| <= max_abs
+    (kernels/q4k_batched.py:102) and ||C - ref||_F / ||ref||_F <= rel_frob.
+    Returns (ok, max_abs_err, rel_frob_err, n_nonfinite)."""
+    C = np.asarray(C, np.float64)
+    C_ref = np.asarray(C_ref, np.float64)
+    nonfinite = int(np.count_nonzero(~np.isfinite(C)))
+    if nonfinite:
+        return False, float("inf"), float("inf"), nonfinite
+    diff = C - C_ref
+    mae = float(np.max(np.abs(diff))) if diff.size else 0.0
+    denom = float(np.linalg.norm(C_ref))
+    rfe = float(np.linalg.norm(diff)) / denom if denom > 0 else float(np.linalg.norm(diff))
+    return (mae <= max_abs and rfe <= rel_frob), mae, rfe, 0

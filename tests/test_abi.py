@@ -1,0 +1,102 @@
+"""C-ABI checks that need no GPU: the library loads, exports exactly what
+include/busfill.h declares, and rejects bad arguments before enqueuing work
+(validation happens before any HIP call, so no device is touched)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import busfill as bf
+
+HDR = open(bf.HEADER).read()
+
+
+def declared_functions():
+    body = re.sub(r"/\*.*?\*/", "", HDR, flags=re.S)
+    return sorted(set(re.findall(r"\b(bf_[a-z0-9_]+)\s*\(", body)))
+
+
+def test_header_declares_expected_entry_points():
+    assert declared_functions() == sorted(bf.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    L = bf.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    # and the symbols are real dynamic exports
+    out = os.popen(f"nm -D --defined-only {bf.LIB_PATH}").read()
+    for name in declared_functions():
+        assert re.search(rf"\bT {name}\b", out), name
+
+
+def test_status_strings_and_version():
+    L = bf.lib()
+    assert L.bf_status_str(0) == b"BF_OK"
+    assert L.bf_status_str(1) == b"BF_ERR_INVALID"
+    assert L.bf_status_str(2) == b"BF_ERR_UNSUPPORTED"
+    assert L.bf_status_str(3) == b"BF_ERR_HIP"
+    assert bf.version() >= 100
+
+
+FAKE = 0x10000   # never dereferenced: every case below is rejected in validation
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(qtype=7), "qtype"),
+    (dict(W=None), "W is NULL"),
+    (dict(qtype=bf.Q4_0_PLANES, W_aux=None), "W_aux"),
+    (dict(qtype=bf.Q4_K, W_aux=FAKE), "must be NULL"),
+    (dict(K=100), "multiple of 32"),
+    (dict(qtype=bf.Q4_K, K=4096 + 32), "multiple of 256"),
+    (dict(M=0), "M=0"),
+    (dict(N=0), "N=0"),
+    (dict(lda=100), "lda"),
+    (dict(ldc=10), "ldc"),
+    (dict(A=None), "NULL"),
+    (dict(C=None), "NULL"),
+    (dict(otype=5), "otype"),
+    (dict(algo=9), "algo"),
+    (dict(A=FAKE + 1), "aligned"),
+])
+def test_gemm_rejects_invalid_arguments(kw, needle):
+    args = dict(qtype=bf.Q4_0, W=FAKE, W_aux=None, A=FAKE, lda=None, C=FAKE, ldc=None,
+                otype=bf.OUT_F32, M=4, N=64, K=512, algo=bf.ALGO_AUTO)
+    args.update(kw)
+    lda = args["lda"] if args["lda"] is not None else args["K"]
+    ldc = args["ldc"] if args["ldc"] is not None else args["N"]
+    st = bf.lib().bf_gemm_ex(args["qtype"], args["W"], args["W_aux"], args["A"], lda, args["C"], ldc,
+                             args["otype"], args["M"], args["N"], args["K"], args["algo"], None)
+    assert st == bf.ERR_INVALID
+    assert needle in bf.lib().bf_last_error().decode()
+
+
+def test_reference_entry_rejects_bad_shape():
+    st = bf.lib().bf_busfill_q4(FAKE, FAKE, FAKE, FAKE, 1, 33, 64, None)
+    assert st == bf.ERR_INVALID
+    with pytest.raises(bf.BusfillInvalid):
+        bf.busfill_q4(FAKE, FAKE, FAKE, FAKE, 0, 64, 64, stream=0)
+
+
+def test_dequant_rejects_bad_arguments():
+    assert bf.lib().bf_dequant_f16(bf.Q4_K, FAKE, None, None, 4, 256, None) == bf.ERR_INVALID
+    assert bf.lib().bf_dequant_f16(bf.Q4_K, FAKE, None, FAKE, 4, 100, None) == bf.ERR_INVALID
+    assert bf.lib().bf_dequant_f16(bf.Q4_0_PLANES, FAKE, None, FAKE, 4, 256, None) == bf.ERR_INVALID
+
+
+def test_product_path_has_no_fallback(tmp_path, monkeypatch):
+    """The loader raises when libbusfill.so is absent; nothing substitutes for it."""
+    monkeypatch.setattr(bf, "LIB_PATH", str(tmp_path / "missing.so"))
+    monkeypatch.setattr(bf, "_lib", None)
+    with pytest.raises(FileNotFoundError):
+        bf.lib()
+
+
+def test_product_sources_do_not_use_the_oracle():
+    pkg = os.path.dirname(bf.PKG_DIR)
+    for dirpath, _, files in os.walk(os.path.join(pkg, "bus-fill_amd")):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "import oracle" not in text and "liboracle" not in text, f

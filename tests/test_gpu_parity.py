@@ -1,0 +1,246 @@
+"""GPU parity of libbusfill against the CPU oracle (run on an MI355X).
+
+Bar: bit-exact for the fp16 dequant; for the GEMM, every value finite,
+max |C - ref| <= 0.6 (the repo gate, kernels/q4k_batched.py:102) and relative
+Frobenius error <= 1e-3, where ref is the fp64 dequantize-then-matmul of the
+reference check (kernels/busfill_v1a.cu:159-167) over the oracle's weights.
+All calls go through the C-ABI (busfill.* are thin ctypes wrappers).
+"""
+import numpy as np
+import pytest
+import torch
+
+import busfill as bf
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+QTS = [O.Q4_0_PLANES, O.Q4_0, O.Q4_K]
+QT_NAME = {O.Q4_0_PLANES: "planes", O.Q4_0: "q4_0", O.Q4_K: "q4_k"}
+
+
+def to_dev(a, dev):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to(dev)
+
+
+def upload(w, dev):
+    return to_dev(w.W, dev), (to_dev(w.W_aux, dev) if w.W_aux is not None else None)
+
+
+def gpu_gemm(w, A, dev, algo=bf.ALGO_AUTO, otype=bf.OUT_F32, dw=None):
+    M = A.shape[0]
+    Wd, auxd = dw if dw is not None else upload(w, dev)
+    Ad = to_dev(A, dev)
+    C = torch.full((M, w.N), float("nan"), device=dev,
+                   dtype=torch.float32 if otype == bf.OUT_F32 else torch.float16)
+    bf.gemm(w.qtype, Wd, auxd, Ad, C, M, w.N, w.K, otype=otype, algo=algo)
+    torch.cuda.synchronize()
+    return C.float().cpu().numpy().astype(np.float64)
+
+
+def gpu_dequant(w, dev):
+    Wd, auxd = upload(w, dev)
+    out = torch.empty((w.N, w.K), dtype=torch.int16, device=dev)
+    bf.dequant_f16(w.qtype, Wd, auxd, out, w.N, w.K)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().view(np.uint16)
+
+
+def assert_gate(C, ref, what):
+    ok, mae, rfe, nf = O.gate(C, ref)
+    assert ok, f"{what}: max_abs={mae:.4g} rel_frob={rfe:.3g} nonfinite={nf}"
+    return mae, rfe
+
+
+# ------------------------------------------------------------------ dequant
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+@pytest.mark.parametrize("N,K", [(64, 256), (37, 5120), (16, 17408)])
+def test_dequant_bitexact(dev, qt, N, K):
+    w = O.gen_weights(qt, N, K, seed=N * 7 + K)
+    assert (gpu_dequant(w, dev) == O.dequant_f16(w)).all()
+
+
+def test_dequant_bitexact_every_finite_scale(dev):
+    scales = np.arange(65536, dtype=np.uint16)
+    scales = scales[(scales & 0x7C00) != 0x7C00]
+    K = 512
+    N = scales.size // (K // 32)
+    j = np.arange(16, dtype=np.uint8)
+    Wq = np.tile((j | ((15 - j) << 4)).astype(np.uint8), (N, K // 32))
+    w = O.QWeights(O.Q4_0_PLANES, N, K, Wq, scales.reshape(N, K // 32).copy())
+    assert (gpu_dequant(w, dev) == O.dequant_f16(w)).all()
+    b = O.planes_to_blocks(w)
+    assert (gpu_dequant(b, dev) == O.dequant_f16(b)).all()
+
+
+def test_dequant_q4k_extreme_scales(dev):
+    # d and dmin over many binades (incl. subnormal and negative), all 6-bit codes
+    rng = np.random.default_rng(5)
+    w = O.gen_weights(O.Q4_K, 64, 4096, seed=77)
+    blk = w.W.reshape(-1, 144)
+    finite = np.arange(65536, dtype=np.uint16)
+    finite = finite[((finite & 0x7C00) != 0x7C00) & ((finite & 0x7FFF) < 0x5000)]   # |x| < 32
+    hd = rng.choice(finite, blk.shape[0]).astype(np.uint16)
+    hm = rng.choice(finite, blk.shape[0]).astype(np.uint16)
+    blk[:, 0:2] = hd.view(np.uint8).reshape(-1, 2)
+    blk[:, 2:4] = hm.view(np.uint8).reshape(-1, 2)
+    assert (gpu_dequant(w, dev) == O.dequant_f16(w)).all()
+
+
+# ------------------------------------------------------------------ GEMM parity
+M_LIST = [1, 2, 3, 4, 8, 15, 16, 17, 31, 32, 33, 64, 128]
+
+
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+@pytest.mark.parametrize("K", [5120, 17408])
+def test_gemm_parity_batch_sweep(dev, qt, K):
+    N = 200                                   # not a multiple of 16: masked tail tile
+    w = O.gen_weights(qt, N, K, seed=K + qt)
+    dw = upload(w, dev)
+    A_all = O.gen_act(max(M_LIST), K, seed=K * 3 + qt)
+    ref_all = O.gemm_f64(w, A_all)
+    for M in M_LIST:
+        for algo in (bf.ALGO_AUTO, bf.ALGO_MFMA):
+            C = gpu_gemm(w, A_all[:M], dev, algo=algo, dw=dw)
+            assert_gate(C, ref_all[:M], f"{QT_NAME[qt]} K={K} M={M} algo={algo}")
+
+
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_gemm_full_size_5120(dev, qt, M):
+    w = O.gen_weights(qt, 5120, 5120, seed=1000 + qt)
+    A = O.gen_act(M, 5120, seed=2000 + M)
+    assert_gate(gpu_gemm(w, A, dev), O.gemm_f64(w, A), f"{QT_NAME[qt]} 5120^2 M={M}")
+
+
+@pytest.mark.parametrize("N,K", [(7168, 5120), (17408, 5120), (5120, 17408)])
+def test_gemm_layer_shapes_q4k(dev, N, K):
+    w = O.gen_weights(O.Q4_K, N, K, seed=N + K)
+    A = O.gen_act(4, K, seed=N)
+    assert_gate(gpu_gemm(w, A, dev), O.gemm_f64(w, A), f"q4_k {N}x{K} M=4")
+
+
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+def test_gemm_simple_path_matches(dev, qt):
+    w = O.gen_weights(qt, 48, 1024, seed=31)
+    A = O.gen_act(5, 1024, seed=32)
+    assert_gate(gpu_gemm(w, A, dev, algo=bf.ALGO_SIMPLE), O.gemm_f64(w, A), "simple")
+
+
+@pytest.mark.parametrize("qt,K", [(O.Q4_0_PLANES, 32 * 5), (O.Q4_0, 32 * 37), (O.Q4_K, 256 * 3)])
+def test_gemm_odd_shapes(dev, qt, K):
+    # K not a multiple of 256 (Q4_0 formats) and tiny / ragged N, M
+    for N, M in [(1, 1), (17, 3), (100, 9)]:
+        w = O.gen_weights(qt, N, K, seed=N + K)
+        A = O.gen_act(M, K, seed=M + K)
+        assert_gate(gpu_gemm(w, A, dev), O.gemm_f64(w, A), f"{QT_NAME[qt]} N={N} K={K} M={M}")
+
+
+def test_gemm_large_m_is_sliced(dev):
+    w = O.gen_weights(O.Q4_K, 64, 1024, seed=41)
+    A = O.gen_act(300, 1024, seed=42)
+    assert_gate(gpu_gemm(w, A, dev), O.gemm_f64(w, A), "M=300")
+
+
+# ------------------------------------------------------------------ interface behaviour
+def test_reference_entry_beyond_32_rows(dev):
+    """bf_busfill_q4 keeps busfill_q4's arguments; rows >= 32 are computed (the
+    reference dropped them, kernels/busfill_v1a.cu:55-56,98-99)."""
+    N, K, B = 512, 5120, 40
+    w = O.gen_weights(O.Q4_0_PLANES, N, K, seed=51)
+    A = O.gen_act(B, K, seed=52)
+    Wq, Ws = upload(w, dev)
+    Ad = to_dev(A, dev)
+    C = torch.full((B, N), float("nan"), device=dev)
+    bf.busfill_q4(Ad, Wq, Ws, C, B, K, N)
+    torch.cuda.synchronize()
+    assert_gate(C.cpu().numpy(), O.gemm_f64(w, A), "busfill_q4 B=40")
+
+
+def test_strided_operands_and_untouched_rows(dev):
+    N, K, M = 96, 2048, 5
+    lda, ldc = K + 24, N + 40
+    w = O.gen_weights(O.Q4_K, N, K, seed=61)
+    A = O.gen_act(M, K, seed=62)
+    Apad = np.zeros((M, lda), np.uint16)
+    Apad[:, :K] = A
+    Wd, _ = upload(w, dev)
+    Ad = to_dev(Apad, dev)
+    C = torch.full((M + 2, ldc), 12345.0, device=dev)
+    bf.gemm(O.Q4_K, Wd, None, Ad, C, M, N, K, lda=lda, ldc=ldc)
+    torch.cuda.synchronize()
+    Ch = C.cpu().numpy()
+    assert_gate(Ch[:M, :N], O.gemm_f64(w, A), "strided")
+    assert (Ch[:M, N:] == 12345.0).all() and (Ch[M:] == 12345.0).all()
+
+
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+def test_output_f16(dev, qt):
+    w = O.gen_weights(qt, 256, 5120, seed=71)
+    A = O.gen_act(16, 5120, seed=72)
+    dw = upload(w, dev)
+    C16 = gpu_gemm(w, A, dev, otype=bf.OUT_F16, dw=dw)
+    C32 = gpu_gemm(w, A, dev, otype=bf.OUT_F32, dw=dw)
+    assert_gate(C16, O.gemm_f64(w, A), "f16 out")
+    assert (C32.astype(np.float32).astype(np.float16).astype(np.float64) == C16).all()
+
+
+def test_nan_injection_fails_the_gate(dev):
+    w = O.gen_weights(O.Q4_K, 128, 1024, seed=81)
+    A = O.gen_act(4, 1024, seed=82)
+    A[1, 7] = 0x7E00                       # fp16 NaN
+    C = gpu_gemm(w, A, dev)
+    ref = O.gemm_f64(w, O.gen_act(4, 1024, seed=82))
+    assert not np.isfinite(C[1]).any()
+    assert np.isfinite(C[[0, 2, 3]]).all()
+    assert not O.gate(C, ref)[0]
+    assert O.gate(C[[0, 2, 3]], ref[[0, 2, 3]])[0]
+
+
+def test_one_hot_probe_of_output_scatter(dev):
+    """frag_probe-style known answers: one nonzero weight and one nonzero
+    activation must land on exactly one output element."""
+    N, K, M = 48, 512, 128
+    Ws = np.full((N, K // 32), np.float16(1.0).view(np.uint16), np.uint16)
+    for (m, n, k) in [(0, 0, 0), (5, 15, 7), (17, 16, 8), (127, 33, 31), (64, 47, 32), (9, 3, 255), (33, 20, 333)]:
+        Wq = np.full((N, K // 2), 0x88, np.uint8)                # every weight 0
+        byte = Wq[n, k // 2]
+        Wq[n, k // 2] = (byte & 0xF0) | 0x9 if k % 2 == 0 else (byte & 0x0F) | 0x90   # weight 1 at (n, k)
+        A = np.zeros((M, K), np.uint16)
+        A[m, k] = np.float16(2.0).view(np.uint16)
+        w = O.QWeights(O.Q4_0_PLANES, N, K, Wq, Ws)
+        for algo in (bf.ALGO_AUTO, bf.ALGO_MFMA, bf.ALGO_SIMPLE):
+            C = gpu_gemm(w, A, dev, algo=algo)
+            expect = np.zeros((M, N))
+            expect[m, n] = 2.0
+            assert (C == expect).all(), (m, n, k, algo)
+
+
+def test_formats_agree_bitwise_and_runs_are_deterministic(dev):
+    w = O.gen_weights(O.Q4_0_PLANES, 1024, 5120, seed=91)
+    b = O.planes_to_blocks(w)
+    for M in (1, 8, 32):
+        A = O.gen_act(M, 5120, seed=92)
+        Cp = gpu_gemm(w, A, dev)
+        Cb = gpu_gemm(b, A, dev)
+        assert (Cp == Cb).all()
+        assert (gpu_gemm(w, A, dev) == Cp).all()
+
+
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+def test_full_size_exact_properties(dev, qt):
+    """Size-independent checks at the benchmark shape: scaling A by 2 is exact
+    in fp16 and fp32, so C(2A) == 2 C(A) bit for bit; permuting batch rows
+    permutes output rows bit for bit."""
+    w = O.gen_weights(qt, 5120, 5120, seed=101)
+    dw = upload(w, dev)
+    A = O.gen_act(32, 5120, seed=102)
+    C = gpu_gemm(w, A, dev, dw=dw)
+    A2 = (A.view(np.float16) * np.float16(2)).view(np.uint16)
+    assert (gpu_gemm(w, A2, dev, dw=dw) == 2 * C).all()
+    perm = np.random.default_rng(3).permutation(32)
+    assert (gpu_gemm(w, A[perm], dev, dw=dw) == C[perm]).all()
+    assert np.isfinite(C).all()
