@@ -1,0 +1,390 @@
+#!/usr/bin/env python3
+"""Benchmark of the batched int4-block GEMM on one MI355X.
+
+Default run (the headline metric): Q4_K weights, N = K = 5120, batch M = 1, 8
+and 32, one GEMM per step, cycling through >= 1 GB of distinct weight matrices
+already resident in HBM (so the 256 MB Infinity Cache cannot serve them).
+Timing is hipEvents recorded on the launch stream around exactly --steps GEMMs
+(after --warmup untimed ones), issued back to back by the C++ bench host
+(bus-fill_amd/host/bench_host.hip) through the libbusfill C-ABI.
+
+Prints ONE JSON line.  `value` is the weight-stream GB/s at M = 1
+(N*K*9/16 bytes / time per GEMM); `per_batch` carries M = 8 and 32; `roofline`
+prices the algorithmic bytes (weights + A + C) per launch against the 8 TB/s
+HBM peak; `cpu_baseline` is the oracle's CPU dequantize-then-matmul timed on
+this host on a bounded sample of the same workload.
+
+Other workloads (--workload): q4_0 (18-byte blocks), planes (the reference
+layout), layer (one 27B-class decoder layer's Q4_K linears at M = 32) and sweep
+(M = 1..128 on 5120x17408 and 17408x5120).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "bus-fill_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "weight-stream HBM GB/s + tok/s, Q4_K 5120x5120 GEMM at batch 1/8/32"
+HBM_PEAK_GBPS = 8000.0           # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
+ROTATION_BYTES = 1_050_000_000   # >= 1 GB of distinct weights per timing loop
+
+QT = {"q4_k": 2, "q4_0": 0, "planes": 1}
+QT_DESC = {"q4_k": "llama.cpp block_q4_K (144 B / 256 weights)",
+           "q4_0": "llama.cpp block_q4_0 (18 B / 32 weights)",
+           "planes": "reference planes Wq[N][K/2] u8 + Ws[N][K/32] fp16"}
+SCALE_RANGE = {"q4_k": (0.001, 0.01), "q4_0": (0.002, 0.02), "planes": (0.002, 0.02)}
+
+LAYER = [("qkv", 7168, 5120), ("o", 5120, 5120), ("gate", 17408, 5120), ("up", 17408, 5120), ("down", 5120, 17408)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ device data
+class Rotation:
+    """`count` distinct N x K matrices of one format in one device allocation."""
+
+    def __init__(self, fmt, N, K, min_bytes, seed, dev):
+        import torch
+        self.fmt, self.N, self.K = fmt, N, K
+        self.wbytes = N * K * 9 // 16
+        self.count = max(1, math.ceil(min_bytes / self.wbytes))
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        lo, hi = SCALE_RANGE[fmt]
+        if fmt == "planes":
+            self.W = torch.randint(0, 256, (self.count, N * K // 2), dtype=torch.uint8, device=dev, generator=g)
+            d = torch.rand((self.count, N * K // 32), device=dev, generator=g) * (hi - lo) + lo
+            self.aux = d.half().contiguous()
+        else:
+            blk = 144 if fmt == "q4_k" else 18
+            nblk = N * K // (256 if fmt == "q4_k" else 32)
+            self.W = torch.randint(0, 256, (self.count, nblk * blk), dtype=torch.uint8, device=dev, generator=g)
+            v = self.W.view(self.count * nblk, blk)
+            nd = 2 if fmt == "q4_k" else 1          # d (and dmin for Q4_K)
+            d = (torch.rand((self.count * nblk, nd), device=dev, generator=g) * (hi - lo) + lo).half()
+            v[:, 0:2 * nd] = d.view(torch.uint8).view(self.count * nblk, 2 * nd)
+            self.aux = None
+        torch.cuda.synchronize()
+
+    @property
+    def total_bytes(self):
+        return self.count * self.wbytes
+
+    def ptr_arrays(self):
+        W = (ctypes.c_void_p * self.count)(*[self.W[i].data_ptr() for i in range(self.count)])
+        aux = None
+        if self.aux is not None:
+            aux = (ctypes.c_void_p * self.count)(*[self.aux[i].data_ptr() for i in range(self.count)])
+        return W, aux
+
+
+def bench_lib():
+    import busfill
+    busfill.lib()                                  # the product library first (fails loudly)
+    path = os.path.join(os.path.dirname(busfill.LIB_PATH), "libbusfill_bench.so")
+    L = ctypes.CDLL(path)
+    vp, i, d = ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_double)
+    L.bfb_time_gemms.argtypes = [i, vp, vp, i, vp, i, vp, i, i, i, i, i, i, i, i, i, vp, d]
+    L.bfb_time_sequence.argtypes = [i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, d]
+    L.bfb_read_peak.argtypes = [vp, ctypes.c_size_t, i, vp, vp, d]
+    L.bfb_copy.argtypes = [vp, vp, ctypes.c_size_t, i, vp, d]
+    L.bfb_last_error.restype = ctypes.c_char_p
+    for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_read_peak", "bfb_copy"):
+        getattr(L, f).restype = i
+    return L
+
+
+def P(arr):
+    """A ctypes array (or None) as a plain pointer argument."""
+    return None if arr is None else ctypes.cast(arr, ctypes.c_void_p)
+
+
+_STREAM = None
+
+
+def stream_handle():
+    """A dedicated (default-priority) stream: the legacy null stream cannot be
+    captured into a HIP graph."""
+    global _STREAM
+    import torch
+    if _STREAM is None:
+        _STREAM = torch.cuda.Stream()
+    return _STREAM.cuda_stream
+
+
+def time_gemm(L, rot, M, steps, warmup, graph, algo, dev, seed=7):
+    import torch
+    torch.manual_seed(seed)
+    A = torch.randn((M, rot.K), device=dev).half()
+    C = torch.empty((M, rot.N), device=dev, dtype=torch.float32)
+    W, aux = rot.ptr_arrays()
+    ms = ctypes.c_double()
+    torch.cuda.synchronize()
+    rc = L.bfb_time_gemms(QT[rot.fmt], P(W), P(aux), rot.count, A.data_ptr(), rot.K, C.data_ptr(), rot.N, 0,
+                          M, rot.N, rot.K, algo, warmup, steps, int(graph), stream_handle(), ctypes.byref(ms))
+    torch.cuda.synchronize()
+    if rc != 0:
+        raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+    if not torch.isfinite(C).all():
+        raise RuntimeError("non-finite GEMM output during timing")
+    return ms.value
+
+
+def gemm_record(rot, M, ms, steps, graph):
+    t = ms / 1e3 / steps
+    alg = rot.wbytes + M * rot.K * 2 + M * rot.N * 4
+    flops = 2.0 * M * rot.N * rot.K
+    return {
+        "M": M, "us_per_gemm": round(t * 1e6, 4),
+        "weight_GBps": round(rot.wbytes / t / 1e9, 2),
+        "tok_s": round(M / t, 1),
+        "alg_GBps": round(alg / t / 1e9, 2),
+        "hbm_frac": round(alg / t / 1e9 / HBM_PEAK_GBPS, 4),
+        "mfma_frac": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 5),
+        "launch": "graph" if graph else "stream",
+    }
+
+
+def read_peak(L, rot):
+    import torch
+    sink = torch.zeros(1, dtype=torch.int32, device=rot.W.device)
+    ms = ctypes.c_double()
+    nbytes = rot.W.numel()
+    rc = L.bfb_read_peak(rot.W.data_ptr(), nbytes, 5, sink.data_ptr(), stream_handle(), ctypes.byref(ms))
+    if rc != 0:
+        raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+    return 5 * nbytes / (ms.value / 1e3) / 1e9
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_threads():
+    n = os.cpu_count() or 1
+    cap = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(n, cap))
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(fmt, N, K, M, seconds):
+    """The oracle's CPU dequantize-then-matmul (full fp32 dequant of W, then an
+    fp32-accumulated matmul), timed on this host.  Only this leg of bench.py
+    touches the oracle."""
+    import numpy as np
+    import oracle as O
+    qt = {"q4_k": O.Q4_K, "q4_0": O.Q4_0, "planes": O.Q4_0_PLANES}[fmt]
+    w = O.gen_weights(qt, N, K, seed=2024)
+    A = O.gen_act(M, K, seed=2025)
+    scratch = np.empty(N * K, np.float32)
+    out = {}
+    for label, threads, budget in (("all", cpu_threads(), seconds), ("one", 1, max(2.0, seconds / 3))):
+        O.cpu_dequant_matmul(w, A, threads=threads, scratch=scratch)          # warm
+        n, tdq, tmm = 0, 0.0, 0.0
+        t0 = time.perf_counter()
+        while True:
+            _, a, b = O.cpu_dequant_matmul(w, A, threads=threads, scratch=scratch)
+            n, tdq, tmm = n + 1, tdq + a, tmm + b
+            el = time.perf_counter() - t0
+            if el >= budget:
+                break
+        t = el / n
+        out[label] = {"threads": threads, "calls": n, "seconds": round(el, 2), "ms_per_call": round(t * 1e3, 3),
+                      "ms_dequant": round(tdq / n * 1e3, 3), "ms_matmul": round(tmm / n * 1e3, 3),
+                      "weight_GBps": round(N * K * 9 / 16 / t / 1e9, 4), "tok_s": round(M / t, 2)}
+    a = out["all"]
+    return {"value": a["weight_GBps"], "unit": "GB/s", "cores": a["threads"], "kind": "port",
+            "sample": (f"{fmt} N={N} K={K} M={M}: {a['calls']} dequantize-then-matmul calls in "
+                       f"{a['seconds']} s on {a['threads']} threads ({cpu_model()})"),
+            "tok_s": a["tok_s"], "ms_per_call": a["ms_per_call"], "ms_dequant": a["ms_dequant"],
+            "ms_matmul": a["ms_matmul"], "one_thread": out["one"]}
+
+
+def traffic_from_profiles(key):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        return json.load(open(path)).get(key)
+    except (OSError, ValueError):
+        return None
+
+
+# ------------------------------------------------------------------ workloads
+def run_gemm_workload(L, fmt, N, K, batches, args, dev):
+    rot = Rotation(fmt, N, K, ROTATION_BYTES, seed=11, dev=dev)
+    log(f"[bench] {fmt} N={N} K={K}: {rot.count} matrices, {rot.total_bytes / 1e9:.3f} GB rotation")
+    recs = []
+    for M in batches:
+        for graph in ((0, 1) if args.graph == "both" else (int(args.graph),)):
+            ms = time_gemm(L, rot, M, args.steps, args.warmup, graph, args.algo_id, dev)
+            r = gemm_record(rot, M, ms, args.steps, graph)
+            log(f"[bench] {fmt} M={M:3d} {r['launch']:6s}: {r['us_per_gemm']:8.3f} us  "
+                f"{r['weight_GBps']:8.1f} GB/s  {r['tok_s']:10.0f} tok/s  hbm {r['hbm_frac']:.3f}")
+            recs.append(r)
+    peak = read_peak(L, rot)
+    log(f"[bench] streaming-read over the rotation buffer: {peak:.1f} GB/s")
+    return rot, recs, peak
+
+
+def best(recs, M):
+    c = [r for r in recs if r["M"] == M]
+    return min(c, key=lambda r: r["us_per_gemm"])
+
+
+def run_layer(L, args, dev):
+    import torch
+    M = 32
+    layer_bytes = sum(n * k * 9 // 16 for _, n, k in LAYER)
+    nl = max(1, math.ceil(ROTATION_BYTES / layer_bytes))
+    log(f"[bench] layer: {nl} distinct layers x {layer_bytes / 1e6:.1f} MB")
+    keep, seq = [], []
+    for li in range(nl):
+        for name, n, k in LAYER:
+            rot = Rotation("q4_k", n, k, 1, seed=100 + 10 * li + len(seq), dev=dev)
+            A = torch.randn((M, k), device=dev).half()
+            C = torch.empty((M, n), device=dev)
+            keep += [rot, A, C]
+            seq.append((rot.W[0].data_ptr(), A.data_ptr(), C.data_ptr(), n, k))
+    cnt = len(seq)
+    arr = lambda t, xs: P((t * cnt)(*xs))
+    ms = ctypes.c_double()
+    steps = (args.steps // len(LAYER)) * len(LAYER) or len(LAYER)
+    out = []
+    for graph in ((0, 1) if args.graph == "both" else (int(args.graph),)):
+        torch.cuda.synchronize()
+        rc = L.bfb_time_sequence(cnt, arr(ctypes.c_int, [2] * cnt), arr(ctypes.c_void_p, [s[0] for s in seq]), None,
+                                 arr(ctypes.c_void_p, [s[1] for s in seq]), arr(ctypes.c_int, [s[4] for s in seq]),
+                                 arr(ctypes.c_void_p, [s[2] for s in seq]), arr(ctypes.c_int, [s[3] for s in seq]),
+                                 arr(ctypes.c_int, [M] * cnt), arr(ctypes.c_int, [s[3] for s in seq]),
+                                 arr(ctypes.c_int, [s[4] for s in seq]), 0, args.algo_id,
+                                 args.warmup, steps, graph, stream_handle(), ctypes.byref(ms))
+        torch.cuda.synchronize()
+        if rc != 0:
+            raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+        t_layer = ms.value / 1e3 / (steps / len(LAYER))
+        rec = {"M": M, "us_per_layer": round(t_layer * 1e6, 3), "layer_tok_s": round(M / t_layer, 1),
+               "weight_GBps": round(layer_bytes / t_layer / 1e9, 2),
+               "hbm_frac": round(layer_bytes / t_layer / 1e9 / HBM_PEAK_GBPS, 4),
+               "launch": "graph" if graph else "stream", "layers_rotated": nl}
+        log(f"[bench] layer M=32 {rec['launch']}: {rec['us_per_layer']:.2f} us/layer "
+            f"{rec['weight_GBps']:.1f} GB/s {rec['layer_tok_s']:.0f} tok/s")
+        out.append(rec)
+    return out
+
+
+def run_sweep(L, args, dev):
+    res = []
+    for (N, K) in ((17408, 5120), (5120, 17408)):
+        rot = Rotation("q4_k", N, K, ROTATION_BYTES, seed=N, dev=dev)
+        for M in (1, 2, 4, 8, 16, 32, 64, 128):
+            ms = time_gemm(L, rot, M, args.steps, args.warmup, int(args.graph == "1"), args.algo_id, dev)
+            r = gemm_record(rot, M, ms, args.steps, args.graph == "1")
+            r.update({"N": N, "K": K})
+            log(f"[bench] sweep N={N} K={K} M={M:3d}: {r['us_per_gemm']:8.2f} us {r['weight_GBps']:8.1f} GB/s "
+                f"mfma {r['mfma_frac']:.4f}")
+            res.append(r)
+        del rot
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000, help="timed GEMMs per configuration")
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", default="q4_k", choices=["q4_k", "q4_0", "planes", "layer", "sweep"])
+    ap.add_argument("--batches", default="1,8,32")
+    ap.add_argument("--graph", default="both", choices=["0", "1", "both"],
+                    help="issue launches on the stream (0), replay a HIP graph (1), or time both")
+    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "dot2", "simple"])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--out", default=None, help="also write the full record to this JSON file")
+    args = ap.parse_args()
+    args.algo_id = {"auto": 0, "mfma": 1, "dot2": 2, "simple": 3}[args.algo]
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build runs the GEMM on a single MI355X and has no "
+              "multi-GPU path (see the sharding note in DESIGN.md); run it with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    dev = torch.device("cuda:0")
+    L = bench_lib()
+    batches = [int(x) for x in args.batches.split(",")]
+
+    if args.workload in ("q4_k", "q4_0", "planes"):
+        fmt = args.workload
+        rot, recs, peak = run_gemm_workload(L, fmt, 5120, 5120, batches, args, dev)
+        head = best(recs, batches[0])
+        t = head["us_per_gemm"] / 1e6
+        alg_bytes = rot.wbytes + head["M"] * rot.K * 2 + head["M"] * rot.N * 4
+        record = {
+            "metric": METRIC if fmt == "q4_k" else METRIC.replace("Q4_K", fmt.upper()),
+            "value": head["weight_GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(head["us_per_gemm"] / 1e3, 6),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+            "data": "synthetic",
+            "config": {"workload": f"{fmt} GEMM N=K=5120, batch M={head['M']} (per_batch: M={batches})",
+                       "format": QT_DESC[fmt], "N": 5120, "K": 5120, "batches": batches,
+                       "rotation_matrices": rot.count, "rotation_bytes": rot.total_bytes,
+                       "launch": head["launch"], "accumulate": "fp32", "algo": args.algo},
+            "tok_s": head["tok_s"],
+            "per_batch": [best(recs, M) for M in batches],
+            "all_runs": recs,
+            "hbm_read_measured_GBps": round(peak, 1),
+            "roofline": {"bound": "hbm", "achieved": round(alg_bytes / t / 1e9, 2), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(alg_bytes / t / 1e9 / HBM_PEAK_GBPS, 4),
+                         "traffic": traffic_from_profiles(f"{fmt}_5120_m{head['M']}"),
+                         "algorithmic_bytes_per_launch": alg_bytes},
+        }
+        del rot
+        torch.cuda.empty_cache()
+        if not args.no_cpu:
+            log("[bench] CPU baseline ...")
+            record["cpu_baseline"] = cpu_baseline(fmt, 5120, 5120, batches[0], args.cpu_seconds)
+    elif args.workload == "layer":
+        recs = run_layer(L, args, dev)
+        b = min(recs, key=lambda r: r["us_per_layer"])
+        record = {"metric": "layer-sum weight-stream GB/s + tok/s, 27B-class decoder layer Q4_K linears at batch 32",
+                  "value": b["weight_GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+                  "warmup": args.warmup, "ms_per_step": round(b["us_per_layer"] / 1e3 / len(LAYER), 6),
+                  "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+                  "data": "synthetic",
+                  "config": {"workload": "q4_k qkv 5120->7168, o 5120->5120, gate/up 5120->17408, down 17408->5120",
+                             "M": 32, "launch": b["launch"]},
+                  "layer_tok_s": b["layer_tok_s"], "runs": recs}
+    else:
+        recs = run_sweep(L, args, dev)
+        record = {"metric": "Q4_K GEMM batch sweep: weight-stream GB/s and MFMA utilisation",
+                  "value": max(r["weight_GBps"] for r in recs), "unit": "GB/s", "n_gpus": 1,
+                  "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
+                  "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+                  "config": {"workload": "q4_k M in 1..128 on 17408x5120 and 5120x17408", "algo": args.algo},
+                  "sweep": recs}
+    line = json.dumps(record)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(line + "\n")
+    print(line, flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -13,6 +13,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libbusfill.so")
+BENCH_LIB = os.path.join(LIBDIR, "libbusfill_bench.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["bf_api.hip", "bf_gemm_mfma.hip", "bf_gemm_dot2.hip", "bf_simple.hip"]
@@ -26,10 +27,9 @@ HIP_FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(LIBDIR, exist_ok=True)
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, *[os.path.join(CSRC, s) for s in SOURCES], "-o", tmp]
+def _hipcc(sources, out, extra=(), verbose=False):
+    tmp = out + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, *sources, *extra, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -39,7 +39,16 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
     if verbose and err:
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    """Builds libbusfill.so (the product) and libbusfill_bench.so (the bench
+    host's timed loops, linked against the product through its C-ABI)."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    _hipcc([os.path.join(CSRC, s) for s in SOURCES], LIB, verbose=verbose)
+    _hipcc([os.path.join(HERE, "host", "bench_host.hip")], BENCH_LIB,
+           extra=["-L", LIBDIR, "-lbusfill", "-Wl,-rpath,$ORIGIN"], verbose=verbose)
     return LIB
 
 

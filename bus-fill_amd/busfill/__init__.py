@@ -16,7 +16,8 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.dirname(_HERE)
-LIB_PATH = os.path.join(PKG_DIR, "lib", "libbusfill.so")
+# BUSFILL_LIBDIR points the loader at another build of the same library
+LIB_PATH = os.path.join(os.environ.get("BUSFILL_LIBDIR") or os.path.join(PKG_DIR, "lib"), "libbusfill.so")
 HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "busfill.h")
 
 # bf_status

@@ -1,0 +1,151 @@
+// Per-format register image of one lane's 64-weight run of a 256-weight
+// super-group, and its decode into pre-scaled fp16 MFMA operands.  Shared by
+// the register-streaming and the LDS-staged MFMA kernels.
+//
+// Lane (r = l%16, kg = l/16) owns, for super-group s of row r, the 64 weights
+// k = 256s + 64kg + 8i + j (i = 0..7 selects the MFMA, j the element):
+//   Q4_K  : chunk kg of qs[128] (32 B, sub-blocks 2kg and 2kg+1) + the header
+//   planes: code bytes 32kg..32kg+31 of the row + the two fp16 block scales
+//   Q4_0  : 18-byte blocks 2kg and 2kg+1 (36 B)
+#pragma once
+
+#include "bf_device.h"
+
+namespace bf {
+
+struct __attribute__((aligned(4))) U4a4 { uint32_t x, y, z, w; };
+
+__device__ __forceinline__ u4 ld16(const uint8_t* p) { return *(const u4*)p; }
+__device__ __forceinline__ u4 ld16_a4(const uint8_t* p) {
+    U4a4 v = *(const U4a4*)p;
+    return u4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ h8 ld_act(const uint16_t* p) { return *(const h8*)p; }
+
+// Raw bytes one lane holds for one super-group of one row.
+template <int QT> struct Raw;
+template <> struct Raw<QT_Q4_K> { u4 hdr, q0, q1; };
+template <> struct Raw<QT_PLANES> { u4 q0, q1; uint32_t sc; };
+template <> struct Raw<QT_Q4_0> { u4 a, b; uint32_t c; };
+
+template <int QT>
+__device__ __forceinline__ void load_raw(Raw<QT>& raw, const uint8_t* W, const uint8_t* Waux,
+                                         int64_t n, int s, int kg, int K);
+
+template <>
+__device__ __forceinline__ void load_raw<QT_Q4_K>(Raw<QT_Q4_K>& raw, const uint8_t* W, const uint8_t*,
+                                                  int64_t n, int s, int kg, int K) {
+    const uint8_t* base = W + n * ((int64_t)(K >> 8) * 144) + (int64_t)s * 144;
+    raw.hdr = ld16(base);
+    raw.q0 = ld16(base + 16 + 32 * kg);
+    raw.q1 = ld16(base + 32 + 32 * kg);
+}
+
+template <>
+__device__ __forceinline__ void load_raw<QT_PLANES>(Raw<QT_PLANES>& raw, const uint8_t* W, const uint8_t* Waux,
+                                                    int64_t n, int s, int kg, int K) {
+    const uint8_t* base = W + n * (int64_t)(K >> 1) + (int64_t)s * 128 + 32 * kg;
+    raw.q0 = ld16(base);
+    raw.q1 = ld16(base + 16);
+    raw.sc = *(const uint32_t*)(Waux + 2 * (n * (int64_t)(K >> 5) + 8 * s + 2 * kg));
+}
+
+template <>
+__device__ __forceinline__ void load_raw<QT_Q4_0>(Raw<QT_Q4_0>& raw, const uint8_t* W, const uint8_t*,
+                                                  int64_t n, int s, int kg, int K) {
+    const uint8_t* base = W + n * ((int64_t)(K >> 8) * 144) + (int64_t)s * 144 + 36 * kg;
+    raw.a = ld16_a4(base);
+    raw.b = ld16_a4(base + 16);
+    raw.c = *(const uint32_t*)(base + 32);
+}
+
+// Per-lane scale state derived once per super-group.
+template <int QT> struct Scl;
+template <> struct Scl<QT_Q4_K> { h2 sa, ma, sb, mb; };   // scale / -min of sub-blocks 2kg, 2kg+1
+template <> struct Scl<QT_PLANES> { h2 da, db; };
+template <> struct Scl<QT_Q4_0> { h2 da, db; uint32_t qa[4]; };
+
+__device__ __forceinline__ h2 splat(uint32_t hbits) {
+    _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)hbits);
+    return h2{v, v};
+}
+
+__device__ __forceinline__ Scl<QT_Q4_K> scales(const Raw<QT_Q4_K>& raw, int kg) {
+    // (scale, min) codes of sub-blocks 2kg and 2kg+1, two bytes at a time and
+    // without branches: for kg < 2 they are the low six bits of scale bytes
+    // 2kg, 2kg+1 and 2kg+4, 2kg+5; for kg >= 2 they are assembled from the
+    // nibbles of bytes 8..11 and the top two bits of bytes 0..7.
+    const uint32_t s0 = raw.hdr.y, s1 = raw.hdr.z, s2 = raw.hdr.w;
+    const uint32_t sh = 16u * (uint32_t)(kg & 1);
+    const uint32_t sc_lo = (s0 >> sh) & 0x3F3Fu, mn_lo = (s1 >> sh) & 0x3F3Fu;
+    const uint32_t sc_hi = ((s2 >> sh) & 0x0F0Fu) | ((s0 >> (sh + 2)) & 0x3030u);
+    const uint32_t mn_hi = ((s2 >> (sh + 4)) & 0x0F0Fu) | ((s1 >> (sh + 2)) & 0x3030u);
+    const uint32_t sc = kg < 2 ? sc_lo : sc_hi, mn = kg < 2 ? mn_lo : mn_hi;
+    const float d = half_bits_to_float(raw.hdr.x & 0xFFFFu);
+    const float dmin = half_bits_to_float(raw.hdr.x >> 16);
+    Scl<QT_Q4_K> o;
+    _Float16 xa = (_Float16)(d * (float)(sc & 0xFFu)), ya = (_Float16)(-(dmin * (float)(mn & 0xFFu)));
+    _Float16 xb = (_Float16)(d * (float)(sc >> 8)), yb = (_Float16)(-(dmin * (float)(mn >> 8)));
+    o.sa = h2{xa, xa}; o.ma = h2{ya, ya};
+    o.sb = h2{xb, xb}; o.mb = h2{yb, yb};
+    return o;
+}
+
+__device__ __forceinline__ Scl<QT_PLANES> scales(const Raw<QT_PLANES>& raw, int) {
+    Scl<QT_PLANES> o;
+    o.da = splat(raw.sc & 0xFFFFu);
+    o.db = splat(raw.sc >> 16);
+    return o;
+}
+
+__device__ __forceinline__ Scl<QT_Q4_0> scales(const Raw<QT_Q4_0>& raw, int) {
+    Scl<QT_Q4_0> o;
+    // block 2kg = bytes 0..17: d at 0, qs at 2..17 (realigned by 2 bytes)
+    o.da = splat(raw.a.x & 0xFFFFu);
+    o.qa[0] = __builtin_amdgcn_alignbit(raw.a.y, raw.a.x, 16);
+    o.qa[1] = __builtin_amdgcn_alignbit(raw.a.z, raw.a.y, 16);
+    o.qa[2] = __builtin_amdgcn_alignbit(raw.a.w, raw.a.z, 16);
+    o.qa[3] = __builtin_amdgcn_alignbit(raw.b.x, raw.a.w, 16);
+    // block 2kg+1 = bytes 18..35: d at 18, qs at 20..35 = words 5..8
+    o.db = splat(raw.b.x >> 16);
+    return o;
+}
+
+// Weights of MFMA i (elements 64kg + 8i .. +7 of the lane's run).
+__device__ __forceinline__ h8 weights(const Magic& mg, const Raw<QT_Q4_K>& raw, const Scl<QT_Q4_K>& sc, int i) {
+    const uint32_t w[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
+    const int t = i & 3;
+    if (i < 4) return decode8_fma<false>(mg, w[2 * t], w[2 * t + 1], sc.sa, sc.ma);
+    return decode8_fma<true>(mg, w[2 * t], w[2 * t + 1], sc.sb, sc.mb);
+}
+
+__device__ __forceinline__ h8 weights(const Magic& mg, const Raw<QT_PLANES>& raw, const Scl<QT_PLANES>& sc, int i) {
+    const uint32_t w[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
+    return decode8_planes(mg, w[i], i < 4 ? sc.da : sc.db);
+}
+
+__device__ __forceinline__ h8 weights(const Magic& mg, const Raw<QT_Q4_0>& raw, const Scl<QT_Q4_0>& sc, int i) {
+    const int t = i & 3;
+    if (i < 4) {
+        const uint32_t* q = sc.qa;
+        return t < 2 ? decode8_q4_0<false>(mg, q[2 * t], q[2 * t + 1], sc.da)
+                     : decode8_q4_0<true>(mg, q[2 * (t - 2)], q[2 * (t - 2) + 1], sc.da);
+    }
+    const uint32_t q[4] = {raw.b.y, raw.b.z, raw.b.w, raw.c};
+    return t < 2 ? decode8_q4_0<false>(mg, q[2 * t], q[2 * t + 1], sc.db)
+                 : decode8_q4_0<true>(mg, q[2 * (t - 2)], q[2 * (t - 2) + 1], sc.db);
+}
+
+// One wave's share of the K loop: SPW super-groups s = wave, wave + KW, ...
+// held in a register ring that is filled before any of it is consumed.
+// ALDS: the workgroup first copies A[0:M][0:K] into LDS (rows padded by 16 B so
+// the 16 lanes r of one kg group hit different banks) and every wave reads its
+// fragments from there; used when M*K is small.  Otherwise fragments come from
+// global memory (L2-resident: A is at most 128 x K fp16), one super-group ahead
+// when registers allow.
+//
+// Every load is unconditional with clamped, in-bounds addresses (padding lanes
+// read row 0, slots past the end reread the last super-group) and only stores
+// and MFMAs are predicated: the compiler's wait counters then stay exact, so a
+// slot is consumed as soon as ITS bytes have arrived.
+}  // namespace bf

@@ -1,0 +1,201 @@
+// Bench host: the timed loops that drive libbusfill through its C-ABI.
+//
+// Restates the reference harness's timing (kernels/busfill_v1a.cu:168-175:
+// cudaEvent around back-to-back launches, tok/s = B/t) with two changes the
+// MI355X needs: the loop cycles through a caller-provided set of DISTINCT
+// weight matrices (>= 1 GB, so the 256 MB Infinity Cache cannot serve them),
+// and it can replay the same launch sequence as a captured HIP graph.
+// Events are recorded on the stream the kernels run on.
+//
+// Also holds two plain memory kernels used as yardsticks: a 128-bit streaming
+// read (the achievable HBM read rate) and a 128-bit copy (the calibration
+// kernel for FETCH_SIZE / WRITE_SIZE counters).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <vector>
+
+#include "busfill.h"
+
+namespace {
+
+thread_local hipError_t g_err = hipSuccess;
+thread_local bf_status g_bf = BF_OK;
+
+#define HCK(x)                                  \
+    do {                                        \
+        hipError_t e_ = (x);                    \
+        if (e_ != hipSuccess) {                 \
+            g_err = e_;                         \
+            return -1;                          \
+        }                                       \
+    } while (0)
+
+struct Launch {
+    int qtype;
+    const void* W;
+    const void* W_aux;
+    const uint16_t* A;
+    int lda;
+    void* C;
+    int ldc;
+    int M, N, K;
+};
+
+int issue(const Launch& l, int otype, int algo, hipStream_t st) {
+    bf_status s = bf_gemm_ex((bf_qtype)l.qtype, l.W, l.W_aux, l.A, l.lda, l.C, l.ldc, (bf_otype)otype, l.M, l.N,
+                             l.K, (bf_algo)algo, st);
+    if (s != BF_OK) {
+        g_bf = s;
+        return -1;
+    }
+    return 0;
+}
+
+// Runs `warmup` then `steps` launches taken cyclically from seq; returns ms.
+int time_seq(const std::vector<Launch>& seq, int otype, int algo, int warmup, int steps, int use_graph,
+             hipStream_t st, double* ms_out) {
+    const size_t n = seq.size();
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    float ms = 0.f;
+    if (!use_graph) {
+        for (int i = 0; i < warmup; i++)
+            if (issue(seq[i % n], otype, algo, st)) return -1;
+        HCK(hipStreamSynchronize(st));
+        HCK(hipEventRecord(e0, st));
+        for (int i = 0; i < steps; i++)
+            if (issue(seq[i % n], otype, algo, st)) return -1;
+        HCK(hipEventRecord(e1, st));
+        HCK(hipEventSynchronize(e1));
+        HCK(hipEventElapsedTime(&ms, e0, e1));
+    } else {
+        auto capture = [&](int count, hipGraphExec_t* exec) -> int {
+            hipGraph_t g;
+            HCK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            for (int i = 0; i < count; i++)
+                if (issue(seq[i % n], otype, algo, st)) {
+                    hipGraph_t dead;
+                    (void)hipStreamEndCapture(st, &dead);
+                    return -1;
+                }
+            HCK(hipStreamEndCapture(st, &g));
+            HCK(hipGraphInstantiate(exec, g, nullptr, nullptr, 0));
+            HCK(hipGraphDestroy(g));
+            return 0;
+        };
+        hipGraphExec_t gw = nullptr, gs = nullptr;
+        if (warmup > 0 && capture(warmup, &gw)) return -1;
+        if (capture(steps, &gs)) return -1;
+        if (gw) HCK(hipGraphLaunch(gw, st));
+        HCK(hipStreamSynchronize(st));
+        HCK(hipEventRecord(e0, st));
+        HCK(hipGraphLaunch(gs, st));
+        HCK(hipEventRecord(e1, st));
+        HCK(hipEventSynchronize(e1));
+        HCK(hipEventElapsedTime(&ms, e0, e1));
+        if (gw) HCK(hipGraphExecDestroy(gw));
+        HCK(hipGraphExecDestroy(gs));
+    }
+    HCK(hipEventDestroy(e0));
+    HCK(hipEventDestroy(e1));
+    *ms_out = ms;
+    return 0;
+}
+
+__global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ src, size_t n16,
+                                                     unsigned* __restrict__ sink) {
+    unsigned acc = 0;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x) {
+        uint4 v = src[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;   // keeps the loads live; practically never taken
+}
+
+__global__ __launch_bounds__(256) void k_stream_copy(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                     size_t n16) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+}  // namespace
+
+extern "C" {
+
+// Times `steps` GEMMs (after `warmup` untimed ones) cycling through `count`
+// weight matrices W[i] (W_aux[i] for the planes layout), same A and C.
+int bfb_time_gemms(int qtype, const void* const* W, const void* const* W_aux, int count, const uint16_t* A,
+                   int lda, void* C, int ldc, int otype, int M, int N, int K, int algo, int warmup, int steps,
+                   int use_graph, void* stream, double* ms_out) {
+    std::vector<Launch> seq;
+    for (int i = 0; i < count; i++) seq.push_back(Launch{qtype, W[i], W_aux ? W_aux[i] : nullptr, A, lda, C, ldc, M, N, K});
+    return time_seq(seq, otype, algo, warmup, steps, use_graph, (hipStream_t)stream, ms_out);
+}
+
+// Times `steps` launches cycling through a heterogeneous list of n GEMMs
+// (e.g. the linears of decoder layers).
+int bfb_time_sequence(int n, const int* qtype, const void* const* W, const void* const* W_aux,
+                      const uint16_t* const* A, const int* lda, void* const* C, const int* ldc, const int* M,
+                      const int* N, const int* K, int otype, int algo, int warmup, int steps, int use_graph,
+                      void* stream, double* ms_out) {
+    std::vector<Launch> seq;
+    for (int i = 0; i < n; i++)
+        seq.push_back(Launch{qtype[i], W[i], W_aux ? W_aux[i] : nullptr, A[i], lda[i], C[i], ldc[i], M[i], N[i], K[i]});
+    return time_seq(seq, otype, algo, warmup, steps, use_graph, (hipStream_t)stream, ms_out);
+}
+
+// Streaming 128-bit read of `bytes` at `src`, `reps` times; returns ms.
+int bfb_read_peak(const void* src, size_t bytes, int reps, void* sink, void* stream, double* ms_out) {
+    hipStream_t st = (hipStream_t)stream;
+    const size_t n16 = bytes / 16;
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    hipLaunchKernelGGL(k_stream_read, dim3(2048), dim3(256), 0, st, (const uint4*)src, n16, (unsigned*)sink);
+    HCK(hipGetLastError());
+    HCK(hipEventRecord(e0, st));
+    for (int r = 0; r < reps; r++)
+        hipLaunchKernelGGL(k_stream_read, dim3(2048), dim3(256), 0, st, (const uint4*)src, n16, (unsigned*)sink);
+    HCK(hipGetLastError());
+    HCK(hipEventRecord(e1, st));
+    HCK(hipEventSynchronize(e1));
+    float ms;
+    HCK(hipEventElapsedTime(&ms, e0, e1));
+    *ms_out = ms;
+    HCK(hipEventDestroy(e0));
+    HCK(hipEventDestroy(e1));
+    return 0;
+}
+
+// 128-bit copy of `bytes` (the known-size calibration kernel for HBM counters).
+int bfb_copy(const void* src, void* dst, size_t bytes, int reps, void* stream, double* ms_out) {
+    hipStream_t st = (hipStream_t)stream;
+    const size_t n16 = bytes / 16;
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    HCK(hipEventRecord(e0, st));
+    for (int r = 0; r < reps; r++)
+        hipLaunchKernelGGL(k_stream_copy, dim3(2048), dim3(256), 0, st, (const uint4*)src, (uint4*)dst, n16);
+    HCK(hipGetLastError());
+    HCK(hipEventRecord(e1, st));
+    HCK(hipEventSynchronize(e1));
+    float ms;
+    HCK(hipEventElapsedTime(&ms, e0, e1));
+    *ms_out = ms;
+    HCK(hipEventDestroy(e0));
+    HCK(hipEventDestroy(e1));
+    return 0;
+}
+
+const char* bfb_last_error(void) {
+    static thread_local char buf[512];
+    if (g_bf != BF_OK) snprintf(buf, sizeof buf, "%s: %s", bf_status_str(g_bf), bf_last_error());
+    else snprintf(buf, sizeof buf, "%s", hipGetErrorString(g_err));
+    return buf;
+}
+
+}  // extern "C"

@@ -244,3 +244,22 @@ def test_full_size_exact_properties(dev, qt):
     perm = np.random.default_rng(3).permutation(32)
     assert (gpu_gemm(w, A[perm], dev, dw=dw) == C[perm]).all()
     assert np.isfinite(C).all()
+
+
+@pytest.mark.parametrize("K", [256, 1792, 2048, 5120, 7168, 17408])
+@pytest.mark.parametrize("N", [1, 3, 200])
+def test_dot2_small_batch_parity(dev, K, N):
+    """The row-streaming v_dot2 kernel (Q4_K, M <= 2): super-block groups of
+    seven per load, ragged tails, every N."""
+    w = O.gen_weights(O.Q4_K, N, K, seed=K * 3 + N)
+    dw = upload(w, dev)
+    A = O.gen_act(2, K, seed=K + 5)
+    ref = O.gemm_f64(w, A)
+    for M in (1, 2):
+        if M * K * 2 > 48 * 1024:          # staged activations beyond the kernel's LDS budget
+            with pytest.raises(bf.BusfillError):
+                gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DOT2, dw=dw)
+            continue
+        C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DOT2, dw=dw)
+        assert_gate(C, ref[:M], f"dot2 N={N} K={K} M={M}")
+        assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_AUTO, dw=dw) == C).all()
