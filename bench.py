@@ -289,6 +289,32 @@ def run_layer(L, args, dev):
     return out
 
 
+COPY_BYTES = 256 << 20
+
+
+def run_copy(L, args, dev):
+    """The calibration kernel for the HBM byte counters: a 128-bit copy of
+    exactly COPY_BYTES (read COPY_BYTES, write COPY_BYTES per launch)."""
+    import torch
+    src = torch.randint(0, 256, (COPY_BYTES,), dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    reps = max(1, min(args.steps, 50))
+    ms = ctypes.c_double()
+    torch.cuda.synchronize()
+    rc = L.bfb_copy(src.data_ptr(), dst.data_ptr(), COPY_BYTES, reps, stream_handle(), ctypes.byref(ms))
+    torch.cuda.synchronize()
+    if rc != 0:
+        raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+    if not torch.equal(src, dst):
+        raise RuntimeError("copy kernel produced a wrong copy")
+    t = ms.value / 1e3 / reps
+    return {"metric": "HBM copy GB/s (read + write), calibration kernel", "value": round(2 * COPY_BYTES / t / 1e9, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": reps, "warmup": 0, "ms_per_step": round(t * 1e3, 6),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+            "config": {"workload": f"k_stream_copy of {COPY_BYTES} bytes", "bytes_read": COPY_BYTES,
+                       "bytes_written": COPY_BYTES}}
+
+
 def run_sweep(L, args, dev):
     res = []
     for (N, K) in ((17408, 5120), (5120, 17408)):
@@ -309,16 +335,16 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000, help="timed GEMMs per configuration")
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", default="q4_k", choices=["q4_k", "q4_0", "planes", "layer", "sweep"])
+    ap.add_argument("--workload", default="q4_k", choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy"])
     ap.add_argument("--batches", default="1,8,32")
     ap.add_argument("--graph", default="both", choices=["0", "1", "both"],
                     help="issue launches on the stream (0), replay a HIP graph (1), or time both")
-    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "dot2", "simple"])
+    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "dot2", "simple", "lds"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--out", default=None, help="also write the full record to this JSON file")
     args = ap.parse_args()
-    args.algo_id = {"auto": 0, "mfma": 1, "dot2": 2, "simple": 3}[args.algo]
+    args.algo_id = {"auto": 0, "mfma": 1, "dot2": 2, "simple": 3, "lds": 4}[args.algo]
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the GEMM on a single MI355X and has no "
@@ -371,6 +397,8 @@ def main():
                   "config": {"workload": "q4_k qkv 5120->7168, o 5120->5120, gate/up 5120->17408, down 17408->5120",
                              "M": 32, "launch": b["launch"]},
                   "layer_tok_s": b["layer_tok_s"], "runs": recs}
+    elif args.workload == "copy":
+        record = run_copy(L, args, dev)
     else:
         recs = run_sweep(L, args, dev)
         record = {"metric": "Q4_K GEMM batch sweep: weight-stream GB/s and MFMA utilisation",

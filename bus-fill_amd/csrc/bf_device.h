@@ -92,24 +92,28 @@ __device__ __forceinline__ void q4k_scale_min(const uint32_t s[3], int j, uint32
 }
 
 // Eight fp16 weights from eight code bytes (w0 = bytes 0-3, w1 = bytes 4-7),
-// one nibble per byte (low nibbles when HI == false), in natural byte order,
-// pre-scaled: out = RN(RN(q - bias_off) * scale + shift) per element.
-// Q4_K: bias_off subtracts the magic bias only, scale = d*sc, shift = -dmin*m.
+// one nibble per byte (low nibbles when HI == false), in natural byte order.
+// Q4_K: out = RN16(fma32(bias + q, s, c)) with s = d*sc and c = -dmin*m - bias*s
+// in fp32 (v_fma_mix: fp16 operand, fp32 arithmetic, one rounding to fp16).
+// (bias + q) is exact in fp16 and (bias + q)*s is exact in the fused multiply-add,
+// so each weight is q*s - dmin*m rounded once, up to c's own fp32 rounding
+// (at most 2^-24 * bias * s).
 template <bool HI>
-__device__ __forceinline__ h8 decode8_fma(const Magic& mg, uint32_t w0, uint32_t w1, h2 scale, h2 shift) {
+__device__ __forceinline__ h8 decode8_mix(const Magic& mg, uint32_t w0, uint32_t w1, float s, float c) {
     const uint32_t mask = HI ? mg.hi_mask : mg.lo_mask, bits = HI ? mg.hi_bits : mg.lo_bits;
-    const h2 unbias = HI ? h2{(_Float16)-64.0f, (_Float16)-64.0f} : h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
     uint32_t p[4] = {perm_b32(w0, w0, SEL_B01), perm_b32(w0, w0, SEL_B23),
                      perm_b32(w1, w1, SEL_B01), perm_b32(w1, w1, SEL_B23)};
-    h8 out;
+    uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        h2 q = as_h2(and_or(p[i], mask, bits)) + unbias;        // exact integer q
-        h2 v = q * scale + shift;                               // v_pk_fma_f16
-        out[2 * i] = v[0];
-        out[2 * i + 1] = v[1];
+        const uint32_t x = and_or(p[i], mask, bits);              // {bias + q, bias + q'}
+        // v_fma_mix{lo,hi}_f16: op_sel_hi marks src0 as fp16 (op_sel picks its half),
+        // s and c are fp32; mixhi keeps the low half written by mixlo
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(o[i]) : "v"(x), "v"(s), "v"(c));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "+v"(o[i]) : "v"(x), "v"(s), "v"(c));
     }
-    return out;
+    return __builtin_bit_cast(h8, u4{o[0], o[1], o[2], o[3]});
 }
 
 // Same for the Q4_0 formats: out = RN((q - 8) * d); (q - 8) is exact, so each

@@ -61,7 +61,7 @@ __device__ __forceinline__ void load_raw<QT_Q4_0>(Raw<QT_Q4_0>& raw, const uint8
 
 // Per-lane scale state derived once per super-group.
 template <int QT> struct Scl;
-template <> struct Scl<QT_Q4_K> { h2 sa, ma, sb, mb; };   // scale / -min of sub-blocks 2kg, 2kg+1
+template <> struct Scl<QT_Q4_K> { float sa, ca, sb, cb; };   // scale, offset of sub-blocks 2kg, 2kg+1
 template <> struct Scl<QT_PLANES> { h2 da, db; };
 template <> struct Scl<QT_Q4_0> { h2 da, db; uint32_t qa[4]; };
 
@@ -84,10 +84,11 @@ __device__ __forceinline__ Scl<QT_Q4_K> scales(const Raw<QT_Q4_K>& raw, int kg) 
     const float d = half_bits_to_float(raw.hdr.x & 0xFFFFu);
     const float dmin = half_bits_to_float(raw.hdr.x >> 16);
     Scl<QT_Q4_K> o;
-    _Float16 xa = (_Float16)(d * (float)(sc & 0xFFu)), ya = (_Float16)(-(dmin * (float)(mn & 0xFFu)));
-    _Float16 xb = (_Float16)(d * (float)(sc >> 8)), yb = (_Float16)(-(dmin * (float)(mn >> 8)));
-    o.sa = h2{xa, xa}; o.ma = h2{ya, ya};
-    o.sb = h2{xb, xb}; o.mb = h2{yb, yb};
+    // sub-block 2kg uses the low nibbles (magic bias 1024), 2kg+1 the high ones (bias 64)
+    o.sa = d * (float)(sc & 0xFFu);
+    o.ca = __builtin_fmaf(-1024.0f, o.sa, -(dmin * (float)(mn & 0xFFu)));
+    o.sb = d * (float)(sc >> 8);
+    o.cb = __builtin_fmaf(-64.0f, o.sb, -(dmin * (float)(mn >> 8)));
     return o;
 }
 
@@ -115,8 +116,8 @@ __device__ __forceinline__ Scl<QT_Q4_0> scales(const Raw<QT_Q4_0>& raw, int) {
 __device__ __forceinline__ h8 weights(const Magic& mg, const Raw<QT_Q4_K>& raw, const Scl<QT_Q4_K>& sc, int i) {
     const uint32_t w[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
     const int t = i & 3;
-    if (i < 4) return decode8_fma<false>(mg, w[2 * t], w[2 * t + 1], sc.sa, sc.ma);
-    return decode8_fma<true>(mg, w[2 * t], w[2 * t + 1], sc.sb, sc.mb);
+    if (i < 4) return decode8_mix<false>(mg, w[2 * t], w[2 * t + 1], sc.sa, sc.ca);
+    return decode8_mix<true>(mg, w[2 * t], w[2 * t + 1], sc.sb, sc.cb);
 }
 
 __device__ __forceinline__ h8 weights(const Magic& mg, const Raw<QT_PLANES>& raw, const Scl<QT_PLANES>& sc, int i) {
@@ -136,16 +137,4 @@ __device__ __forceinline__ h8 weights(const Magic& mg, const Raw<QT_Q4_0>& raw, 
                  : decode8_q4_0<true>(mg, q[2 * (t - 2)], q[2 * (t - 2) + 1], sc.db);
 }
 
-// One wave's share of the K loop: SPW super-groups s = wave, wave + KW, ...
-// held in a register ring that is filled before any of it is consumed.
-// ALDS: the workgroup first copies A[0:M][0:K] into LDS (rows padded by 16 B so
-// the 16 lanes r of one kg group hit different banks) and every wave reads its
-// fragments from there; used when M*K is small.  Otherwise fragments come from
-// global memory (L2-resident: A is at most 128 x K fp16), one super-group ahead
-// when registers allow.
-//
-// Every load is unconditional with clamped, in-bounds addresses (padding lanes
-// read row 0, slots past the end reread the last super-group) and only stores
-// and MFMAs are predicated: the compiler's wait counters then stay exact, so a
-// slot is consumed as soon as ITS bytes have arrived.
 }  // namespace bf

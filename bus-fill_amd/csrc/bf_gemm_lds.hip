@@ -1,0 +1,456 @@
+// LDS-staged MFMA GEMM for small batches (the decode shapes, M <= 16 when the
+// activations fit in LDS).
+//
+//   C[m][n] = sum_k A[m][k] * dequant(W)[n][k]      (fp32 accumulation)
+//
+// Replaces the hot loop of the reference kernel (kernels/busfill_v1a.cu:41-104:
+// one thread block per group of weight rows, weights read once from HBM,
+// dequantised in registers, fp32 accumulation) with a layout built for CDNA4.
+//
+// * One workgroup per CU-sized slice of rows: `nsub` sub-tiles of R = 16/G
+//   consecutive rows (N = 5120, G = 4: 256 workgroups of 20 rows, one per CU).
+// * K segments on the MFMA's idle rows: with a batch of M <= 16/G rows per
+//   segment, the 16x16x32 MFMA's 16 columns hold R weight rows times G
+//   K-segments (column n = G*row + g) and its 16 rows hold 16/G batch rows
+//   times the same G segments (row m = G*m' + g).  Only the entries with equal
+//   segments are used; they are summed across the G lanes (DPP).  A work unit
+//   ("step") is always 16 (row, super-group) pairs = 2304 bytes, whatever G is.
+// * Loader waves (kNL per workgroup) move every weight byte HBM -> LDS with
+//   direct-to-LDS loads (global_load_lds_dwordx4: one 64-lane instruction moves
+//   1 KB without touching VGPRs), steps in order, as runs of G*144 contiguous
+//   bytes per row.  They never wait: after the last load of each step a loader
+//   issues a one-dword "marker" load of a nonzero word into that step's flag.
+//   A wave's loads return in issue order, so a visible marker means the step has
+//   landed.  Loaders run at the highest issue priority (s_setprio) and use a
+//   precomputed address pattern, so the compute waves' VALU work never delays
+//   the next load.  The activations A[0:M][0:K] are loaded the same way first.
+// * Compute waves (kNC per workgroup) never touch VMEM except for the final
+//   stores: they spin on the markers (ds_read + s_sleep) and take steps c,
+//   c + kNC, ... (the order in which steps land), decode each step from LDS
+//   into pre-scaled fp16 MFMA operands and run 8 MFMAs per m-tile.  The folded
+//   partial sums of each step are parked in LDS; a per-sub-tile counter
+//   (ds_add_rtn) tells the wave that finishes a sub-tile's last step to add the
+//   sub-tile's partials in step order (a fixed order: results are
+//   deterministic) and store them.  There is no workgroup barrier after the
+//   start.
+//
+// Weight layout in LDS: the workgroup's steps in order, 2304 bytes each; inside
+// a step, the 144-byte super-group image of column n = 0..15 at n*144 (Q4_K and
+// Q4_0 copy their 144 bytes verbatim; the planes layout stores the 16 bytes of
+// the eight block scales followed by the 128 code bytes).  Lane (r, kg) reads
+// column r at a 36-dword stride: the 16 lanes of a k-group fall on 16 distinct
+// 4-bank groups.
+#include <atomic>
+
+#include "bf_formats.h"
+#include "bf_launch.h"
+
+namespace bf {
+namespace {
+
+constexpr int kStep = 16 * 144;          // bytes of one step
+constexpr int kASg = 528;                // LDS bytes of one super-group of one activation row (512 + 16)
+constexpr int kMaxLds = 160 * 1024;      // LDS per workgroup on gfx950
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
+// Lane l copies the 16 bytes at `src` to LDS byte address m0 + 16*l.
+// (One wait state is required between the M0 write and the LDS-DMA.)
+__device__ __forceinline__ void dma16(const void* src, uint32_t m0) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(src), "{m0}"(m0) : "memory");
+}
+
+// Completion marker: lane 0 copies the nonzero word at `src` to LDS byte address
+// m0 (a one-dword direct-to-LDS load; the other lanes are masked off).  A wave's
+// loads return in issue order, so once the marker is visible in LDS every load
+// this wave issued before it has landed as well.
+__device__ __forceinline__ void dma_marker(const void* src, uint32_t m0, int lane) {
+    if (lane == 0)
+        asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" :: "v"(src), "{m0}"(m0) : "memory");
+}
+
+__device__ const uint32_t g_marker_src[64] = {
+    1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u,
+    1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u,
+    1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u};
+
+// Barrier that waits for this wave's LDS traffic only (the LDS-DMA loads of
+// later steps stay in flight across it).
+__device__ __forceinline__ void barrier_lds() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One column's image of one super-group, read from LDS.
+template <int QT>
+__device__ __forceinline__ void lds_raw(Raw<QT>& raw, const uint8_t* u, int kg);
+
+template <>
+__device__ __forceinline__ void lds_raw<QT_Q4_K>(Raw<QT_Q4_K>& raw, const uint8_t* u, int kg) {
+    raw.hdr = *(const u4*)u;
+    raw.q0 = *(const u4*)(u + 16 + 32 * kg);
+    raw.q1 = *(const u4*)(u + 32 + 32 * kg);
+}
+
+template <>
+__device__ __forceinline__ void lds_raw<QT_PLANES>(Raw<QT_PLANES>& raw, const uint8_t* u, int kg) {
+    raw.q0 = *(const u4*)(u + 16 + 32 * kg);
+    raw.q1 = *(const u4*)(u + 32 + 32 * kg);
+    raw.sc = *(const uint32_t*)(u + 4 * kg);
+}
+
+template <>
+__device__ __forceinline__ void lds_raw<QT_Q4_0>(Raw<QT_Q4_0>& raw, const uint8_t* u, int kg) {
+    raw.a = ld16_a4(u + 36 * kg);
+    raw.b = ld16_a4(u + 36 * kg + 16);
+    raw.c = *(const uint32_t*)(u + 36 * kg + 32);
+}
+
+// Global address of 16-byte piece c (0..8) of the super-group image of (row, sg).
+template <int QT>
+__device__ __forceinline__ const uint8_t* w_piece(const uint8_t* W, const uint8_t* Waux, int64_t row, int sg,
+                                                  int c, int K) {
+    if constexpr (QT == QT_PLANES) {
+        if (c == 0) return Waux + 2 * (row * (int64_t)(K >> 5) + 8 * sg);
+        return W + row * (int64_t)(K >> 1) + 128 * sg + 16 * (c - 1);
+    } else {
+        return W + row * ((int64_t)(K >> 8) * 144) + 144 * sg + 16 * c;
+    }
+}
+
+// Spin (with s_sleep) until the LDS word at `flag` is nonzero.  The bound only
+// guards against a hang if a producer were ever missing: no launch comes close.
+__device__ __forceinline__ void wait_flag(const int* flag) {
+    const uint32_t a = lds_addr(flag);
+    for (int it = 0; it < (1 << 20); it++) {
+        int v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+        if (__builtin_amdgcn_readfirstlane(v) != 0) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+__device__ __forceinline__ float dpp_xor(float v, int ctrl_sel) {
+    // quad_perm [1,0,3,2] (xor 1) or [2,3,0,1] (xor 2)
+    const int x = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, ctrl_sel == 1 ? __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false)
+                                                   : __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+}
+
+// Loader address pattern: the offset of piece c of column (rowl, g) inside one
+// step image, relative to the step's base (bit 28 set: the piece comes from
+// the planes layout's scale array), and the scalar bases of a step.
+template <int QT>
+__device__ __forceinline__ uint32_t step_piece_offset(int rowl, int g, int c, int K) {
+    if constexpr (QT == QT_PLANES) {
+        if (c == 0) return (uint32_t)(rowl * (K >> 4) + 16 * g) | (1u << 28);
+        return (uint32_t)(rowl * (K >> 1) + 128 * g + 16 * (c - 1));
+    } else {
+        return (uint32_t)(rowl * ((K >> 8) * 144) + 144 * g + 16 * c);
+    }
+}
+
+template <int QT> struct StepBase { int64_t w; };
+template <> struct StepBase<QT_PLANES> { int64_t w, aux; };
+
+template <int QT>
+__device__ __forceinline__ StepBase<QT> step_base(int64_t row0, int sg0, int K) {
+    if constexpr (QT == QT_PLANES) {
+        return StepBase<QT>{row0 * (K >> 1) + 128 * sg0, row0 * (K >> 4) + 16 * sg0};
+    } else {
+        return StepBase<QT>{row0 * ((K >> 8) * 144) + 144 * sg0};
+    }
+}
+
+template <int QT>
+__device__ __forceinline__ const uint8_t* piece_addr(const uint8_t* W, const uint8_t* Waux, const StepBase<QT>& b,
+                                                     uint32_t off) {
+    if constexpr (QT == QT_PLANES) {
+        const uint32_t o = off & 0x0FFFFFFFu;
+        return (off >> 28) & 1u ? Waux + b.aux + o : W + b.w + o;
+    } else {
+        return W + b.w + off;
+    }
+}
+
+// LDS layout (bytes): [0, 2048) flags: activation markers of loader j at 4j,
+// step markers at 64 + 4e, finished-step counters of sub-tile t at 1024 + 4t;
+// [2048, 2048 + a_bytes) activations, row m at m * a_rs; then the W steps of the
+// workgroup in order (2304 bytes each); then one parked partial per step.
+constexpr int kFlagBytes = 2048;
+constexpr int kMaxSteps = (1024 - 64) / 4;
+constexpr int kMaxSub = (kFlagBytes - 1024) / 4;
+
+template <int QT, int G, int MT, int NC, int NL>
+__global__ __launch_bounds__(64 * (NC + NL))
+void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
+                const uint16_t* __restrict__ A, int lda, void* __restrict__ C, int ldc, int out_f16,
+                int M, int N, int K, int nsub, int a_rs, int a_bytes) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
+    constexpr int SLOT = MT * R * R;                   // floats of one parked partial
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nsg = K >> 8, nsteps = nsg / G;
+    const int S = nsub * nsteps;                       // steps of the workgroup
+    const int tile0 = blockIdx.x * nsub;
+    int* const flags = (int*)lds;
+    uint8_t* const a_lds = lds + kFlagBytes;
+    uint8_t* const w_lds = a_lds + a_bytes;
+    float* const parts = (float*)(w_lds + S * kStep);
+    const uint32_t lds0 = lds_addr(lds);
+
+    if (wave == 0) {
+        for (int i = lane; i < kFlagBytes / 4; i += 64) flags[i] = 0;
+    }
+    barrier_lds();
+
+    if (wave >= NC) {
+        // ------------------------------------------------------------ loader wave
+        // Issues its loads in order and never waits for them: a marker load after
+        // each group tells the compute waves that the group has landed.  Runs at
+        // the highest issue priority so that the compute waves' VALU work never
+        // delays the next load.
+        __builtin_amdgcn_s_setprio(3);
+        const int j = wave - NC;
+        // activations: row m of A is nIr 1 KB instructions at m * a_rs (lanes past
+        // the row's 33 * nsg pieces are masked); instructions i = j, j + NL, ...
+        const int nIr = (nsg * 33 + 63) >> 6;
+        for (int i = j; i < M * nIr; i += NL) {
+            const int m = i / nIr, jj = i - m * nIr;
+            const int P = 64 * jj + lane;
+            const int sg = min(P / 33, nsg - 1), c = min(P - 33 * (P / 33), 31);
+            if (P < nsg * 33)
+                dma16(A + (int64_t)m * lda + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + m * a_rs + 1024 * jj));
+        }
+        dma_marker(g_marker_src + lane, lds0 + 4 * j, lane);
+        // weights: steps [s0, s1) into their place in the step array
+        const int s0 = S * j / NL, s1 = S * (j + 1) / NL, n = s1 - s0;
+        const int nI = (n * kStep + 1023) >> 10, pmax = n * 144 - 1;
+        const uint32_t m0 = lds0 + (uint32_t)(kFlagBytes + a_bytes + s0 * kStep);
+        // Instruction i = 9a + b covers pieces 576a + 64b + lane of this loader's
+        // region: the lane's step is 4a + d_b and its piece (column n, part c) is
+        // fixed per (b, lane), so its offset inside the step image is too.
+        uint32_t pat[9];
+#pragma unroll
+        for (int b = 0; b < 9; b++) {
+            const int P = 64 * b + lane, d = P / 144, q = P - 144 * d, nn = q / 9, c = q - 9 * nn;
+            pat[b] = step_piece_offset<QT>(nn / G, nn % G, c, K) | ((uint32_t)d << 29);
+        }
+        const bool clamp = (int64_t)(tile0 + nsub) * R > N;   // last workgroup: rows past N reread row N-1
+        int t = s0 / nsteps, s = s0 - t * nsteps;       // position of step s0 + 4a
+        for (int a4 = 0; 9 * a4 < nI; a4++) {
+            // scalar image bases of the steps 4a .. 4a+4 (t, s advance in step order)
+            StepBase<QT> base[5];
+            int tt = t, ss = s;
+#pragma unroll
+            for (int d = 0; d < 5; d++) {
+                base[d] = step_base<QT>((int64_t)(tile0 + tt) * R, G * ss, K);
+                if (++ss == nsteps) { ss = 0; ++tt; }
+            }
+#pragma unroll
+            for (int b = 0; b < 9; b++) {
+                const int i = 9 * a4 + b;
+                if (i >= nI) break;
+                const int d0 = (64 * b) / 144;             // the instruction spans steps d0 and d0 + 1
+                const int P = 64 * i + lane;
+                const uint32_t pb = pat[b];
+                const bool hi = (pb >> 29) != (uint32_t)d0;
+                const uint8_t* src;
+                if (!clamp) {
+                    src = piece_addr<QT>(W, Waux, hi ? base[d0 + 1] : base[d0], pb & 0x1FFFFFFFu);
+                } else {
+                    const int e = min(P, pmax) / 144;
+                    const int q = min(P, pmax) - 144 * e, nn = q / 9, c = q - 9 * nn;
+                    const int ea = s0 + e;
+                    const int te = ea / nsteps, se = ea - te * nsteps;
+                    const int64_t row = min((int64_t)(tile0 + te) * R + nn / G, (int64_t)N - 1);
+                    src = w_piece<QT>(W, Waux, row, G * se + nn % G, c, K);
+                }
+                if (P <= pmax) dma16(src, m0 + (uint32_t)(i << 10));
+                // marker for the step (if any) whose last byte this instruction loads
+                const int k = min((64 * i + 63) / 144, n - 1);
+                if ((((k + 1) * kStep - 1) >> 10) == i)
+                    dma_marker(g_marker_src + lane, lds0 + 64 + 4 * (s0 + k), lane);
+                else if (k >= 1 && ((k * kStep - 1) >> 10) == i)
+                    dma_marker(g_marker_src + lane, lds0 + 64 + 4 * (s0 + k - 1), lane);
+            }
+            for (int d = 0; d < 4; d++)
+                if (++s == nsteps) { s = 0; ++t; }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
+
+    // ---------------------------------------------------------------- compute wave
+    // Steps c, c + NC, ... (roughly the order in which they land).  Each step's
+    // G-folded partial sums go to the step's own slot; the wave that finishes
+    // the last step of a sub-tile adds the sub-tile's slots in step order (a
+    // fixed order: results do not depend on timing) and stores them.
+    const int c = wave;
+    for (int j = 0; j < NL; j++) wait_flag(&flags[j]);
+
+    const Magic mg = make_magic();
+    const int r = lane & 15, kg = lane >> 4;
+    const int g = r % G, rowl = r / G;
+    const uint8_t* arow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int m = min(mt * R + r / G, M - 1);      // padding batch rows reread row M-1
+        arow[mt] = a_lds + m * a_rs + g * kASg + 128 * kg;
+    }
+
+    int s_in = c % nsteps, t_in = c / nsteps;
+    for (int e = c; e < S; e += NC) {
+        wait_flag(&flags[16 + e]);
+        Raw<QT> raw;
+        lds_raw<QT>(raw, w_lds + e * kStep + r * 144, kg);
+        const auto sc = scales(raw, kg);
+        const int aoff = G * s_in * kASg;
+        f4 acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const h8 b = weights(mg, raw, sc, i);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                acc[mt] = mfma16x16x32(*(const h8*)(arow[mt] + aoff + 16 * i), b, acc[mt]);
+        }
+        // fold the G segments (lanes r = G*rowl + g) and park the partial sums
+        float* slot = parts + e * SLOT;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+            for (int jj = 0; jj < 4 / G; jj++) {
+                // register G*jj + g holds batch row (4kg)/G + jj of segment g
+                float y = acc[mt][G * jj];
+#pragma unroll
+                for (int gg = 1; gg < G; gg++)
+                    if (g == gg) y = acc[mt][G * jj + gg];
+                if constexpr (G >= 2) y += dpp_xor(y, 1);
+                if constexpr (G >= 4) y += dpp_xor(y, 2);
+                if (g == 0) slot[(mt * R + (4 * kg) / G + jj) * R + rowl] = y;
+            }
+        }
+        // count the finished step; the last of the sub-tile reduces and stores it
+        int old = 0;
+        if (lane == 0)
+            asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+                         : "=v"(old) : "v"(lds_addr(&flags[256 + t_in])), "v"(1) : "memory");
+        if (__builtin_amdgcn_readfirstlane(old) == nsteps - 1) {
+            const int64_t row0 = (int64_t)(tile0 + t_in) * R;
+            for (int v = lane; v < SLOT; v += 64) {
+                const float* pp = parts + t_in * nsteps * SLOT + v;
+                float sum = 0.f;
+                for (int s2 = 0; s2 < nsteps; s2++) sum += pp[s2 * SLOT];
+                const int m = v / R, rl = v - m * R;   // m = mt * R + m_loc
+                const int64_t row = row0 + rl;
+                if (m < M && row < N) {
+                    if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + row] = (_Float16)sum;
+                    else ((float*)C)[(int64_t)m * ldc + row] = sum;
+                }
+            }
+        }
+        s_in += NC;
+        while (s_in >= nsteps) { s_in -= nsteps; ++t_in; }
+    }
+}
+
+// LDS row stride for activations: whole kilobytes for the 528-byte super-group
+// images of one row, plus 16*G bytes, so that the rows m' of one k-group sit on
+// distinct bank groups (stride = 16*G mod 256 bytes).
+inline int a_row_stride(int nsg, int G) {
+    return (nsg * kASg + 1023) / 1024 * 1024 + 16 * G;
+}
+
+constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
+
+struct LdsPlan {
+    int G, MT, nsub, grid, a_rs, a_bytes, lds;
+};
+
+// Sub-tiles per workgroup: about one workgroup per CU when the LDS holds all of
+// its steps, otherwise the fewest rounds of 256 workgroups that fit.
+bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p) {
+    const int nsg = g.K / 256;
+    if (nsg % G) return false;
+    const int nsteps = nsg / G, R = 16 / G;
+    if (g.M > MT * R) return false;
+    const int T = (g.N + R - 1) / R;
+    p.G = G;
+    p.MT = MT;
+    p.a_rs = a_row_stride(nsg, G);
+    if ((int64_t)g.M * p.a_rs > kMaxLds) return false;
+    p.a_bytes = (int)(((int64_t)g.M * p.a_rs + 15) / 16 * 16);
+    for (int rounds = 1; rounds <= 64; rounds++) {
+        const int nsub = (T + 256 * rounds - 1) / (256 * rounds);
+        const int S = nsub * nsteps;
+        if (S > kMaxSteps || nsub > kMaxSub) continue;
+        const int64_t lds = kFlagBytes + (int64_t)p.a_bytes + (int64_t)S * kStep + (int64_t)S * MT * R * R * 4;
+        if (lds > kMaxLds) {
+            if (nsub == 1) return false;
+            continue;
+        }
+        p.nsub = nsub;
+        p.grid = (T + nsub - 1) / nsub;
+        p.lds = (int)lds;
+        return true;
+    }
+    return false;
+}
+
+template <int QT, int G, int MT>
+hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
+    auto k = k_gemm_lds<QT, G, MT, kNC, kNL>;
+    static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(attr_set.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        if (e != hipSuccess) return e;
+        attr_set.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kNC + kNL)), p.lds, st, g.W, g.Waux, g.A, g.lda, g.C, g.ldc,
+                       g.out_f16, g.M, g.N, g.K, p.nsub, p.a_rs, p.a_bytes);
+    return hipGetLastError();
+}
+
+template <int QT>
+hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
+    if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1>(g, p, st);
+    if (p.G == 4 && p.MT == 2) return launch_lds<QT, 4, 2>(g, p, st);
+    if (p.G == 2 && p.MT == 1) return launch_lds<QT, 2, 1>(g, p, st);
+    return launch_lds<QT, 1, 1>(g, p, st);
+}
+
+bool choose_lds(const GemmArgs& g, LdsPlan& p) {
+    if (g.M <= 4 && plan_lds(g, 4, 1, p)) return true;
+    if (g.M <= 8 && plan_lds(g, 4, 2, p)) return true;
+    if (g.M <= 8 && plan_lds(g, 2, 1, p)) return true;
+    if (g.M <= 16 && plan_lds(g, 1, 1, p)) return true;
+    return false;
+}
+
+}  // namespace
+
+bool lds_supports(const GemmArgs& g) {
+    LdsPlan p;
+    if (g.qtype == QT_PLANES && ((uintptr_t)g.Waux & 15)) return false;
+    return choose_lds(g, p);
+}
+
+hipError_t gemm_lds(const GemmArgs& g, hipStream_t st) {
+    LdsPlan p;
+    if (!choose_lds(g, p)) return hipErrorInvalidValue;
+    switch (g.qtype) {
+        case QT_Q4_K: return dispatch_lds<QT_Q4_K>(g, p, st);
+        case QT_PLANES: return dispatch_lds<QT_PLANES>(g, p, st);
+        default: return dispatch_lds<QT_Q4_0>(g, p, st);
+    }
+}
+
+}  // namespace bf

@@ -27,6 +27,18 @@
 
 namespace bf {
 
+// One wave's share of the K loop: SPW super-groups s = wave, wave + KW, ...
+// held in a register ring that is filled before any of it is consumed.
+// ALDS: the workgroup first copies A[0:M][0:K] into LDS (rows padded by 16 B so
+// the 16 lanes r of one kg group hit different banks) and every wave reads its
+// fragments from there; used when M*K is small.  Otherwise fragments come from
+// global memory (L2-resident: A is at most 128 x K fp16), one super-group ahead
+// when registers allow.
+//
+// Every load is unconditional with clamped, in-bounds addresses (padding lanes
+// read row 0, slots past the end reread the last super-group) and only stores
+// and MFMAs are predicated: the compiler's wait counters then stay exact, so a
+// slot is consumed as soon as ITS bytes have arrived.
 template <int QT, int NT, int KW, int SPW>
 __device__ __forceinline__ void ring_load(Raw<QT> (&ring)[SPW][NT], const uint8_t* W, const uint8_t* Waux,
                                           const int64_t (&rows)[NT], int kg, int s_first, int nsg, int K) {

@@ -1,9 +1,15 @@
 """GPU parity of libbusfill against the CPU oracle (run on an MI355X).
 
-Bar: bit-exact for the fp16 dequant; for the GEMM, every value finite,
-max |C - ref| <= 0.6 (the repo gate, kernels/q4k_batched.py:102) and relative
-Frobenius error <= 1e-3, where ref is the fp64 dequantize-then-matmul of the
-reference check (kernels/busfill_v1a.cu:159-167) over the oracle's weights.
+Bar: bit-exact for the fp16 dequant.  For the GEMM, every value finite, and
+  * max |C - ref| <= 0.6 (the repo gate, kernels/q4k_batched.py:102) and
+    relative Frobenius error <= 1e-3, where ref is the fp64 dequantize-then-
+    matmul of the reference check (kernels/busfill_v1a.cu:159-167) over the
+    oracle's weights -- applied when the output has >= 64 elements (on one or
+    two outputs the relative error of fp16 weights alone can exceed 1e-3);
+  * elementwise |C - ref16| <= 1e-4 * (|A| . |W16|^T) + 1e-6, where ref16 is
+    the fp64 matmul over the bit-exact fp16 dequant W16: a forward-error bound
+    for fp16 weights with fp32 accumulation, which any wrong index, scale or
+    dropped term exceeds by orders of magnitude.
 All calls go through the C-ABI (busfill.* are thin ctypes wrappers).
 """
 import numpy as np
@@ -55,6 +61,31 @@ def assert_gate(C, ref, what):
     return mae, rfe
 
 
+class Ref:
+    """Oracle references for weights w and activations A (rows sliceable)."""
+
+    def __init__(self, w, A):
+        self.exact = O.gemm_f64(w, A)
+        self.f16w = O.gemm_f64(w, A, round_w=True)
+        W16 = np.abs(O.dequant_f16(w).view(np.float16).astype(np.float32))
+        Aabs = np.abs(A.view(np.float16).astype(np.float32))
+        self.bound = 1e-4 * (Aabs @ W16.T).astype(np.float64) + 1e-6
+
+    def check(self, C, what, rows=None):
+        sl = slice(None) if rows is None else slice(0, rows)
+        assert np.isfinite(C).all(), f"{what}: non-finite output"
+        err = np.abs(C - self.f16w[sl])
+        bad = err > self.bound[sl]
+        assert not bad.any(), (f"{what}: {int(bad.sum())} elements beyond the fp16-weight bound, "
+                               f"worst excess {float((err / self.bound[sl]).max()):.3g}x")
+        if C.size >= 64:
+            assert_gate(C, self.exact[sl], what)
+
+
+def check_gemm(C, w, A, what):
+    Ref(w, A).check(C, what)
+
+
 # ------------------------------------------------------------------ dequant
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
 @pytest.mark.parametrize("N,K", [(64, 256), (37, 5120), (16, 17408)])
@@ -101,11 +132,11 @@ def test_gemm_parity_batch_sweep(dev, qt, K):
     w = O.gen_weights(qt, N, K, seed=K + qt)
     dw = upload(w, dev)
     A_all = O.gen_act(max(M_LIST), K, seed=K * 3 + qt)
-    ref_all = O.gemm_f64(w, A_all)
+    ref = Ref(w, A_all)
     for M in M_LIST:
         for algo in (bf.ALGO_AUTO, bf.ALGO_MFMA):
             C = gpu_gemm(w, A_all[:M], dev, algo=algo, dw=dw)
-            assert_gate(C, ref_all[:M], f"{QT_NAME[qt]} K={K} M={M} algo={algo}")
+            ref.check(C, f"{QT_NAME[qt]} K={K} M={M} algo={algo}", rows=M)
 
 
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
@@ -113,21 +144,21 @@ def test_gemm_parity_batch_sweep(dev, qt, K):
 def test_gemm_full_size_5120(dev, qt, M):
     w = O.gen_weights(qt, 5120, 5120, seed=1000 + qt)
     A = O.gen_act(M, 5120, seed=2000 + M)
-    assert_gate(gpu_gemm(w, A, dev), O.gemm_f64(w, A), f"{QT_NAME[qt]} 5120^2 M={M}")
+    check_gemm(gpu_gemm(w, A, dev), w, A, f"{QT_NAME[qt]} 5120^2 M={M}")
 
 
 @pytest.mark.parametrize("N,K", [(7168, 5120), (17408, 5120), (5120, 17408)])
 def test_gemm_layer_shapes_q4k(dev, N, K):
     w = O.gen_weights(O.Q4_K, N, K, seed=N + K)
     A = O.gen_act(4, K, seed=N)
-    assert_gate(gpu_gemm(w, A, dev), O.gemm_f64(w, A), f"q4_k {N}x{K} M=4")
+    check_gemm(gpu_gemm(w, A, dev), w, A, f"q4_k {N}x{K} M=4")
 
 
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
 def test_gemm_simple_path_matches(dev, qt):
     w = O.gen_weights(qt, 48, 1024, seed=31)
     A = O.gen_act(5, 1024, seed=32)
-    assert_gate(gpu_gemm(w, A, dev, algo=bf.ALGO_SIMPLE), O.gemm_f64(w, A), "simple")
+    check_gemm(gpu_gemm(w, A, dev, algo=bf.ALGO_SIMPLE), w, A, "simple")
 
 
 @pytest.mark.parametrize("qt,K", [(O.Q4_0_PLANES, 32 * 5), (O.Q4_0, 32 * 37), (O.Q4_K, 256 * 3)])
@@ -136,13 +167,13 @@ def test_gemm_odd_shapes(dev, qt, K):
     for N, M in [(1, 1), (17, 3), (100, 9)]:
         w = O.gen_weights(qt, N, K, seed=N + K)
         A = O.gen_act(M, K, seed=M + K)
-        assert_gate(gpu_gemm(w, A, dev), O.gemm_f64(w, A), f"{QT_NAME[qt]} N={N} K={K} M={M}")
+        check_gemm(gpu_gemm(w, A, dev), w, A, f"{QT_NAME[qt]} N={N} K={K} M={M}")
 
 
 def test_gemm_large_m_is_sliced(dev):
     w = O.gen_weights(O.Q4_K, 64, 1024, seed=41)
     A = O.gen_act(300, 1024, seed=42)
-    assert_gate(gpu_gemm(w, A, dev), O.gemm_f64(w, A), "M=300")
+    check_gemm(gpu_gemm(w, A, dev), w, A, "M=300")
 
 
 # ------------------------------------------------------------------ interface behaviour
@@ -157,7 +188,7 @@ def test_reference_entry_beyond_32_rows(dev):
     C = torch.full((B, N), float("nan"), device=dev)
     bf.busfill_q4(Ad, Wq, Ws, C, B, K, N)
     torch.cuda.synchronize()
-    assert_gate(C.cpu().numpy(), O.gemm_f64(w, A), "busfill_q4 B=40")
+    check_gemm(C.cpu().numpy().astype(np.float64), w, A, "busfill_q4 B=40")
 
 
 def test_strided_operands_and_untouched_rows(dev):
@@ -173,7 +204,7 @@ def test_strided_operands_and_untouched_rows(dev):
     bf.gemm(O.Q4_K, Wd, None, Ad, C, M, N, K, lda=lda, ldc=ldc)
     torch.cuda.synchronize()
     Ch = C.cpu().numpy()
-    assert_gate(Ch[:M, :N], O.gemm_f64(w, A), "strided")
+    check_gemm(Ch[:M, :N].astype(np.float64), w, A, "strided")
     assert (Ch[:M, N:] == 12345.0).all() and (Ch[M:] == 12345.0).all()
 
 
@@ -219,6 +250,31 @@ def test_one_hot_probe_of_output_scatter(dev):
             assert (C == expect).all(), (m, n, k, algo)
 
 
+def test_one_hot_probe_lds_segments(dev):
+    """Known answers for the K-segment mapping of the LDS-staged kernel: one
+    weight (n, k) and one activation (m, k) set, everything else zero, for k in
+    every segment and sub-block and m across the batch rows of each segment."""
+    N, K, M = 24, 2048, 8
+    Ws = np.full((N, K // 32), np.float16(1.0).view(np.uint16), np.uint16)
+    cases = [(0, 0, 0), (7, 23, 2047), (3, 5, 256), (4, 6, 511), (1, 17, 1024 + 33), (6, 8, 1536 + 255),
+             (2, 3, 768 + 64), (5, 12, 300)]
+    for (m, n, k) in cases:
+        Wq = np.full((N, K // 2), 0x88, np.uint8)
+        byte = Wq[n, k // 2]
+        Wq[n, k // 2] = (byte & 0xF0) | 0x9 if k % 2 == 0 else (byte & 0x0F) | 0x90
+        w = O.QWeights(O.Q4_0_PLANES, N, K, Wq, Ws)
+        for Mb in (1, 4, 8):
+            if m >= Mb:
+                continue
+            A = np.zeros((Mb, K), np.uint16)
+            A[m, k] = np.float16(-3.0).view(np.uint16)
+            expect = np.zeros((Mb, N))
+            expect[m, n] = -3.0
+            for ww in (w, O.planes_to_blocks(w)):
+                C = gpu_gemm(ww, A, dev, algo=bf.ALGO_LDS)
+                assert (C == expect).all(), (m, n, k, Mb, ww.qtype)
+
+
 def test_formats_agree_bitwise_and_runs_are_deterministic(dev):
     w = O.gen_weights(O.Q4_0_PLANES, 1024, 5120, seed=91)
     b = O.planes_to_blocks(w)
@@ -254,12 +310,33 @@ def test_dot2_small_batch_parity(dev, K, N):
     w = O.gen_weights(O.Q4_K, N, K, seed=K * 3 + N)
     dw = upload(w, dev)
     A = O.gen_act(2, K, seed=K + 5)
-    ref = O.gemm_f64(w, A)
+    ref = Ref(w, A)
     for M in (1, 2):
         if M * K * 2 > 48 * 1024:          # staged activations beyond the kernel's LDS budget
             with pytest.raises(bf.BusfillError):
                 gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DOT2, dw=dw)
             continue
         C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DOT2, dw=dw)
-        assert_gate(C, ref[:M], f"dot2 N={N} K={K} M={M}")
-        assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_AUTO, dw=dw) == C).all()
+        ref.check(C, f"dot2 N={N} K={K} M={M}", rows=M)
+        assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DOT2, dw=dw) == C).all()
+
+
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+@pytest.mark.parametrize("K", [256, 1024, 5120, 7168, 17408])
+@pytest.mark.parametrize("N", [1, 3, 200, 1000])
+def test_lds_small_batch_parity(dev, qt, K, N):
+    """The LDS-staged kernel: K segments on the MFMA rows (G = 4, 2, 1), steps
+    split across waves and sub-tiles, ragged N, every batch size it serves."""
+    w = O.gen_weights(qt, N, K, seed=K * 5 + N + qt)
+    dw = upload(w, dev)
+    A = O.gen_act(16, K, seed=K + 9)
+    ref = Ref(w, A)
+    for M in (1, 2, 3, 4, 5, 8, 9, 16):
+        must = (M <= 4 and M * K <= 4 * 5120) or (M <= 8 and K <= 5120)
+        try:
+            C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_LDS, dw=dw)
+        except bf.BusfillError as e:
+            assert not must, f"LDS path refused N={N} K={K} M={M}: {e}"
+            continue
+        ref.check(C, f"lds {QT_NAME[qt]} N={N} K={K} M={M}", rows=M)
+        assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_LDS, dw=dw) == C).all()
