@@ -42,137 +42,11 @@
 // 4-bank groups.
 #include <atomic>
 
-#include "bf_formats.h"
 #include "bf_launch.h"
+#include "bf_lds.h"
 
 namespace bf {
 namespace {
-
-constexpr int kStep = 16 * 144;          // bytes of one step
-constexpr int kASg = 528;                // LDS bytes of one super-group of one activation row (512 + 16)
-constexpr int kMaxLds = 160 * 1024;      // LDS per workgroup on gfx950
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
-}
-
-// Lane l copies the 16 bytes at `src` to LDS byte address m0 + 16*l.
-// (One wait state is required between the M0 write and the LDS-DMA.)
-__device__ __forceinline__ void dma16(const void* src, uint32_t m0) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(src), "{m0}"(m0) : "memory");
-}
-
-// Completion marker: lane 0 copies the nonzero word at `src` to LDS byte address
-// m0 (a one-dword direct-to-LDS load; the other lanes are masked off).  A wave's
-// loads return in issue order, so once the marker is visible in LDS every load
-// this wave issued before it has landed as well.
-__device__ __forceinline__ void dma_marker(const void* src, uint32_t m0, int lane) {
-    if (lane == 0)
-        asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" :: "v"(src), "{m0}"(m0) : "memory");
-}
-
-__device__ const uint32_t g_marker_src[64] = {
-    1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u,
-    1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u,
-    1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u, 1u};
-
-// Barrier that waits for this wave's LDS traffic only (the LDS-DMA loads of
-// later steps stay in flight across it).
-__device__ __forceinline__ void barrier_lds() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// One column's image of one super-group, read from LDS.
-template <int QT>
-__device__ __forceinline__ void lds_raw(Raw<QT>& raw, const uint8_t* u, int kg);
-
-template <>
-__device__ __forceinline__ void lds_raw<QT_Q4_K>(Raw<QT_Q4_K>& raw, const uint8_t* u, int kg) {
-    raw.hdr = *(const u4*)u;
-    raw.q0 = *(const u4*)(u + 16 + 32 * kg);
-    raw.q1 = *(const u4*)(u + 32 + 32 * kg);
-}
-
-template <>
-__device__ __forceinline__ void lds_raw<QT_PLANES>(Raw<QT_PLANES>& raw, const uint8_t* u, int kg) {
-    raw.q0 = *(const u4*)(u + 16 + 32 * kg);
-    raw.q1 = *(const u4*)(u + 32 + 32 * kg);
-    raw.sc = *(const uint32_t*)(u + 4 * kg);
-}
-
-template <>
-__device__ __forceinline__ void lds_raw<QT_Q4_0>(Raw<QT_Q4_0>& raw, const uint8_t* u, int kg) {
-    raw.a = ld16_a4(u + 36 * kg);
-    raw.b = ld16_a4(u + 36 * kg + 16);
-    raw.c = *(const uint32_t*)(u + 36 * kg + 32);
-}
-
-// Global address of 16-byte piece c (0..8) of the super-group image of (row, sg).
-template <int QT>
-__device__ __forceinline__ const uint8_t* w_piece(const uint8_t* W, const uint8_t* Waux, int64_t row, int sg,
-                                                  int c, int K) {
-    if constexpr (QT == QT_PLANES) {
-        if (c == 0) return Waux + 2 * (row * (int64_t)(K >> 5) + 8 * sg);
-        return W + row * (int64_t)(K >> 1) + 128 * sg + 16 * (c - 1);
-    } else {
-        return W + row * ((int64_t)(K >> 8) * 144) + 144 * sg + 16 * c;
-    }
-}
-
-// Spin (with s_sleep) until the LDS word at `flag` is nonzero.  The bound only
-// guards against a hang if a producer were ever missing: no launch comes close.
-__device__ __forceinline__ void wait_flag(const int* flag) {
-    const uint32_t a = lds_addr(flag);
-    for (int it = 0; it < (1 << 20); it++) {
-        int v;
-        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
-        if (__builtin_amdgcn_readfirstlane(v) != 0) return;
-        __builtin_amdgcn_s_sleep(1);
-    }
-}
-
-__device__ __forceinline__ float dpp_xor(float v, int ctrl_sel) {
-    // quad_perm [1,0,3,2] (xor 1) or [2,3,0,1] (xor 2)
-    const int x = __builtin_bit_cast(int, v);
-    return __builtin_bit_cast(float, ctrl_sel == 1 ? __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false)
-                                                   : __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
-}
-
-// Loader address pattern: the offset of piece c of column (rowl, g) inside one
-// step image, relative to the step's base (bit 28 set: the piece comes from
-// the planes layout's scale array), and the scalar bases of a step.
-template <int QT>
-__device__ __forceinline__ uint32_t step_piece_offset(int rowl, int g, int c, int K) {
-    if constexpr (QT == QT_PLANES) {
-        if (c == 0) return (uint32_t)(rowl * (K >> 4) + 16 * g) | (1u << 28);
-        return (uint32_t)(rowl * (K >> 1) + 128 * g + 16 * (c - 1));
-    } else {
-        return (uint32_t)(rowl * ((K >> 8) * 144) + 144 * g + 16 * c);
-    }
-}
-
-template <int QT> struct StepBase { int64_t w; };
-template <> struct StepBase<QT_PLANES> { int64_t w, aux; };
-
-template <int QT>
-__device__ __forceinline__ StepBase<QT> step_base(int64_t row0, int sg0, int K) {
-    if constexpr (QT == QT_PLANES) {
-        return StepBase<QT>{row0 * (K >> 1) + 128 * sg0, row0 * (K >> 4) + 16 * sg0};
-    } else {
-        return StepBase<QT>{row0 * ((K >> 8) * 144) + 144 * sg0};
-    }
-}
-
-template <int QT>
-__device__ __forceinline__ const uint8_t* piece_addr(const uint8_t* W, const uint8_t* Waux, const StepBase<QT>& b,
-                                                     uint32_t off) {
-    if constexpr (QT == QT_PLANES) {
-        const uint32_t o = off & 0x0FFFFFFFu;
-        return (off >> 28) & 1u ? Waux + b.aux + o : W + b.w + o;
-    } else {
-        return W + b.w + off;
-    }
-}
 
 // LDS layout (bytes): [0, 2048) flags: activation markers of loader j at 4j,
 // step markers at 64 + 4e, finished-step counters of sub-tile t at 1024 + 4t;

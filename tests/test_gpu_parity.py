@@ -250,6 +250,24 @@ def test_one_hot_probe_of_output_scatter(dev):
             assert (C == expect).all(), (m, n, k, algo)
 
 
+@pytest.mark.parametrize("qt", [O.Q4_0, O.Q4_K], ids=lambda q: QT_NAME[q])
+@pytest.mark.parametrize("N,K", [(1, 256), (77, 2048), (200, 5120), (5120, 5120), (600, 17408)])
+def test_slab_batch_parity(dev, qt, N, K):
+    """The slab-streamed kernel (weights + activation slabs through an LDS ring):
+    one or two row tiles per workgroup, ragged N, ring wrap-around (K = 17408 has
+    68 steps over 5 slots), every batch size it serves."""
+    w = O.gen_weights(qt, N, K, seed=K * 7 + N + qt)
+    dw = upload(w, dev)
+    A = O.gen_act(32, K, seed=K + 13)
+    ref = Ref(w, A)
+    for M in (1, 5, 9, 16, 17, 31, 32):
+        C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_SLAB, dw=dw)
+        ref.check(C, f"slab {QT_NAME[qt]} N={N} K={K} M={M}", rows=M)
+        assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_SLAB, dw=dw) == C).all()
+    with pytest.raises(bf.BusfillError):                  # M > 32 is not served
+        gpu_gemm(w, O.gen_act(33, K, seed=1), dev, algo=bf.ALGO_SLAB, dw=dw)
+
+
 def test_one_hot_probe_lds_segments(dev):
     """Known answers for the K-segment mapping of the LDS-staged kernel: one
     weight (n, k) and one activation (m, k) set, everything else zero, for k in
