@@ -49,8 +49,9 @@ namespace bf {
 namespace {
 
 // LDS layout (bytes): [0, 2048) flags: activation markers of loader j at 4j,
-// step markers at 64 + 4e, finished-step counters of sub-tile t at 1024 + 4t;
-// [2048, 2048 + a_bytes) activations, row m at m * a_rs; then the W steps of the
+// the compute waves' next-step counter at 60, step markers at 64 + 4e,
+// finished-step counters of sub-tile t at 1024 + 4t; [2048, 2048 + a_bytes)
+// activations, row m at m * a_rs; then the W steps of the
 // workgroup in order (2304 bytes each); then one parked partial per step.
 constexpr int kFlagBytes = 2048;
 constexpr int kMaxSteps = (1024 - 64) / 4;
@@ -83,15 +84,19 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
     if (wave >= NC) {
         // ------------------------------------------------------------ loader wave
         // Issues its loads in order and never waits for them: a marker load after
-        // each group tells the compute waves that the group has landed.  Runs at
+        // each step tells the compute waves that the step has landed.  Runs at
         // the highest issue priority so that the compute waves' VALU work never
         // delays the next load.
         __builtin_amdgcn_s_setprio(3);
         const int j = wave - NC;
         // activations: row m of A is nIr 1 KB instructions at m * a_rs (lanes past
-        // the row's 33 * nsg pieces are masked); instructions i = j, j + NL, ...
-        const int nIr = (nsg * 33 + 63) >> 6;
-        for (int i = j; i < M * nIr; i += NL) {
+        // the row's 33 * nsg pieces are masked); instructions i = j, j + NL, ...,
+        // started at a per-workgroup offset so that the workgroups, which all read
+        // the same activations, do not all ask for the same lines at once
+        const int nIr = (nsg * 33 + 63) >> 6, nA = M * nIr;
+        const int rot = (int)((blockIdx.x * 7u) % (unsigned)nA);
+        for (int i0 = j; i0 < nA; i0 += NL) {
+            const int i = i0 + rot < nA ? i0 + rot : i0 + rot - nA;
             const int m = i / nIr, jj = i - m * nIr;
             const int P = 64 * jj + lane;
             const int sg = min(P / 33, nsg - 1), c = min(P - 33 * (P / 33), 31);
@@ -99,70 +104,61 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
                 dma16(A + (int64_t)m * lda + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + m * a_rs + 1024 * jj));
         }
         dma_marker(g_marker_src + lane, lds0 + 4 * j, lane);
-        // weights: steps [s0, s1) into their place in the step array
-        const int s0 = S * j / NL, s1 = S * (j + 1) / NL, n = s1 - s0;
-        const int nI = (n * kStep + 1023) >> 10, pmax = n * 144 - 1;
-        const uint32_t m0 = lds0 + (uint32_t)(kFlagBytes + a_bytes + s0 * kStep);
-        // Instruction i = 9a + b covers pieces 576a + 64b + lane of this loader's
-        // region: the lane's step is 4a + d_b and its piece (column n, part c) is
-        // fixed per (b, lane), so its offset inside the step image is too.
-        uint32_t pat[9];
+        // weights: four steps (9,216 bytes) form a group of 9 instructions whose
+        // per-lane address pattern repeats from group to group: instruction b of a
+        // group covers pieces 64b + lane, i.e. step d_b = (64b + lane) / 144 of the
+        // group and a fixed piece (column n, part c) of that step.  Loader j loads
+        // step j of every group (steps j, j + 4, ...): instructions
+        // b = 9j/4 .. (9j+8)/4 with only the lanes of its step enabled; the
+        // instructions that straddle two steps are issued by both of their
+        // loaders with complementary lanes.  Each step then has one loader, which
+        // issues the step's marker after the step's last load.
+        static_assert(NL == 4, "one step of each group per loader");
+        const int pmax = S * 144 - 1;
+        const uint32_t m0 = lds0 + (uint32_t)(kFlagBytes + a_bytes);
+        const int b_lo = (9 * j) / 4, b_hi = (9 * j + 8) / 4;   // this loader's instructions in a group
+        uint32_t pat[3];
 #pragma unroll
-        for (int b = 0; b < 9; b++) {
-            const int P = 64 * b + lane, d = P / 144, q = P - 144 * d, nn = q / 9, c = q - 9 * nn;
-            pat[b] = step_piece_offset<QT>(nn / G, nn % G, c, K) | ((uint32_t)d << 29);
+        for (int q = 0; q < 3; q++) {
+            const int b = b_lo + q;
+            const int P = 64 * b + lane, d = P / 144, r9 = P - 144 * d, nn = r9 / 9, c = r9 - 9 * nn;
+            pat[q] = step_piece_offset<QT>(nn / G, nn % G, c, K) | ((uint32_t)d << 29);
         }
         const bool clamp = (int64_t)(tile0 + nsub) * R > N;   // last workgroup: rows past N reread row N-1
-        int t = s0 / nsteps, s = s0 - t * nsteps;       // position of step s0 + 4a
-        for (int a4 = 0; 9 * a4 < nI; a4++) {
-            // scalar image bases of the steps 4a .. 4a+4 (t, s advance in step order)
-            StepBase<QT> base[5];
-            int tt = t, ss = s;
+        for (int g4 = 0; 4 * g4 + j < S; g4++) {
+            const int e = 4 * g4 + j;                  // the step this loader owns in group g4
+            const int te = e / nsteps, se = e - te * nsteps;
+            const StepBase<QT> base = step_base<QT>((int64_t)(tile0 + te) * R, G * se, K);
 #pragma unroll
-            for (int d = 0; d < 5; d++) {
-                base[d] = step_base<QT>((int64_t)(tile0 + tt) * R, G * ss, K);
-                if (++ss == nsteps) { ss = 0; ++tt; }
-            }
-#pragma unroll
-            for (int b = 0; b < 9; b++) {
-                const int i = 9 * a4 + b;
-                if (i >= nI) break;
-                const int d0 = (64 * b) / 144;             // the instruction spans steps d0 and d0 + 1
+            for (int q = 0; q < 3; q++) {
+                const int b = b_lo + q;
+                if (b > b_hi) break;
+                const int i = 9 * g4 + b;
                 const int P = 64 * i + lane;
-                const uint32_t pb = pat[b];
-                const bool hi = (pb >> 29) != (uint32_t)d0;
+                const uint32_t pb = pat[q];
                 const uint8_t* src;
                 if (!clamp) {
-                    src = piece_addr<QT>(W, Waux, hi ? base[d0 + 1] : base[d0], pb & 0x1FFFFFFFu);
+                    src = piece_addr<QT>(W, Waux, base, pb & 0x1FFFFFFFu);
                 } else {
-                    const int e = min(P, pmax) / 144;
-                    const int q = min(P, pmax) - 144 * e, nn = q / 9, c = q - 9 * nn;
-                    const int ea = s0 + e;
-                    const int te = ea / nsteps, se = ea - te * nsteps;
+                    const int Pc = min(P, pmax);
+                    const int q9 = Pc - 144 * (Pc / 144), nn = q9 / 9, c = q9 - 9 * nn;
                     const int64_t row = min((int64_t)(tile0 + te) * R + nn / G, (int64_t)N - 1);
                     src = w_piece<QT>(W, Waux, row, G * se + nn % G, c, K);
                 }
-                if (P <= pmax) dma16(src, m0 + (uint32_t)(i << 10));
-                // marker for the step (if any) whose last byte this instruction loads
-                const int k = min((64 * i + 63) / 144, n - 1);
-                if ((((k + 1) * kStep - 1) >> 10) == i)
-                    dma_marker(g_marker_src + lane, lds0 + 64 + 4 * (s0 + k), lane);
-                else if (k >= 1 && ((k * kStep - 1) >> 10) == i)
-                    dma_marker(g_marker_src + lane, lds0 + 64 + 4 * (s0 + k - 1), lane);
+                if ((pb >> 29) == (uint32_t)j && P <= pmax) dma16(src, m0 + (uint32_t)(i << 10));
             }
-            for (int d = 0; d < 4; d++)
-                if (++s == nsteps) { s = 0; ++t; }
+            dma_marker(g_marker_src + lane, lds0 + 64 + 4 * e, lane);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         return;
     }
 
     // ---------------------------------------------------------------- compute wave
-    // Steps c, c + NC, ... (roughly the order in which they land).  Each step's
-    // G-folded partial sums go to the step's own slot; the wave that finishes
-    // the last step of a sub-tile adds the sub-tile's slots in step order (a
-    // fixed order: results do not depend on timing) and stores them.
-    const int c = wave;
+    // Steps are taken from a shared counter in step order, which is roughly the
+    // order in which they land.  Each step's G-folded partial sums go to the
+    // step's own slot; the wave that finishes the last step of a sub-tile adds
+    // the sub-tile's slots in step order (a fixed order: results do not depend
+    // on timing) and stores them.
     for (int j = 0; j < NL; j++) wait_flag(&flags[j]);
 
     const Magic mg = make_magic();
@@ -175,8 +171,15 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
         arow[mt] = a_lds + m * a_rs + g * kASg + 128 * kg;
     }
 
-    int s_in = c % nsteps, t_in = c / nsteps;
-    for (int e = c; e < S; e += NC) {
+    for (;;) {
+        // take the next step (steps land roughly in order; a free wave takes the next one)
+        int e = 0;
+        if (lane == 0)
+            asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+                         : "=v"(e) : "v"(lds_addr(&flags[15])), "v"(1) : "memory");
+        e = __builtin_amdgcn_readfirstlane(e);
+        if (e >= S) break;
+        const int t_in = e / nsteps, s_in = e - t_in * nsteps;
         wait_flag(&flags[16 + e]);
         Raw<QT> raw;
         lds_raw<QT>(raw, w_lds + e * kStep + r * 144, kg);
@@ -227,8 +230,6 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
                 }
             }
         }
-        s_in += NC;
-        while (s_in >= nsteps) { s_in -= nsteps; ++t_in; }
     }
 }
 
