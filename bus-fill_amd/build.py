@@ -23,6 +23,9 @@ HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Wall", "-Wextra", "-Werror", "-Wno-unused-parameter",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the first kernel arguments arrive in SGPRs at wave launch instead of through
+    # a load from the kernarg segment (saves one memory round trip per launch)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I", os.path.join(ROOT, "include"), "-I", CSRC,
 ]
 

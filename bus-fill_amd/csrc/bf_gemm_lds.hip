@@ -17,22 +17,23 @@
 //   ("step") is always 16 (row, super-group) pairs = 2304 bytes, whatever G is.
 // * Loader waves (kNL per workgroup) move every weight byte HBM -> LDS with
 //   direct-to-LDS loads (global_load_lds_dwordx4: one 64-lane instruction moves
-//   1 KB without touching VGPRs), steps in order, as runs of G*144 contiguous
-//   bytes per row.  They never wait: after the last load of each step a loader
-//   issues a one-dword "marker" load of a nonzero word into that step's flag.
-//   A wave's loads return in issue order, so a visible marker means the step has
-//   landed.  Loaders run at the highest issue priority (s_setprio) and use a
-//   precomputed address pattern, so the compute waves' VALU work never delays
-//   the next load.  The activations A[0:M][0:K] are loaded the same way first.
-// * Compute waves (kNC per workgroup) never touch VMEM except for the final
-//   stores: they spin on the markers (ds_read + s_sleep) and take steps c,
-//   c + kNC, ... (the order in which steps land), decode each step from LDS
-//   into pre-scaled fp16 MFMA operands and run 8 MFMAs per m-tile.  The folded
-//   partial sums of each step are parked in LDS; a per-sub-tile counter
-//   (ds_add_rtn) tells the wave that finishes a sub-tile's last step to add the
-//   sub-tile's partials in step order (a fixed order: results are
-//   deterministic) and store them.  There is no workgroup barrier after the
-//   start.
+//   1 KB without touching VGPRs), as runs of G*144 contiguous bytes per row;
+//   loader j owns steps j, j + 4, ...  They never wait: after the last load of
+//   each step the loader issues a one-dword "marker" load of a nonzero word into
+//   that step's flag.  A wave's loads return in issue order, so a visible marker
+//   means the step has landed.  Loaders run at the highest issue priority
+//   (s_setprio) and use a precomputed address pattern, so the compute waves'
+//   VALU work never delays the next load.  The first step's loads are issued
+//   before the workgroup's only barrier (the flags are cleared before it).
+// * Compute waves (kNC per workgroup) load the activations A[0:M][0:K] the same
+//   way at the start (each raises a flag once its own loads are complete), then
+//   spin on the markers (ds_read + s_sleep) and take steps from a shared LDS
+//   counter (the order in which steps
+//   land), decode each step from LDS into pre-scaled fp16 MFMA operands and run
+//   8 MFMAs per m-tile.  The folded partial sums of each step are parked in LDS;
+//   a per-sub-tile counter (ds_add_rtn) tells the wave that finishes a
+//   sub-tile's last step to add the sub-tile's partials in step order (a fixed
+//   order: results are deterministic) and store them.
 //
 // Weight layout in LDS: the workgroup's steps in order, 2304 bytes each; inside
 // a step, the 144-byte super-group image of column n = 0..15 at n*144 (Q4_K and
@@ -48,7 +49,7 @@
 namespace bf {
 namespace {
 
-// LDS layout (bytes): [0, 2048) flags: activation markers of loader j at 4j,
+// LDS layout (bytes): [0, 2048) flags: activation flag of compute wave c at 4c,
 // the compute waves' next-step counter at 60, step markers at 64 + 4e,
 // finished-step counters of sub-tile t at 1024 + 4t; [2048, 2048 + a_bytes)
 // activations, row m at m * a_rs; then the W steps of the
@@ -56,13 +57,15 @@ namespace {
 constexpr int kFlagBytes = 2048;
 constexpr int kMaxSteps = (1024 - 64) / 4;
 constexpr int kMaxSub = (kFlagBytes - 1024) / 4;
+constexpr int kStepCounter = 15;                  // flags[15]: next step to take
 
 template <int QT, int G, int MT, int NC, int NL>
 __global__ __launch_bounds__(64 * (NC + NL))
-void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
-                const uint16_t* __restrict__ A, int lda, void* __restrict__ C, int ldc, int out_f16,
-                int M, int N, int K, int nsub, int a_rs, int a_bytes) {
+void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
+                int nsub, int a_rs, int a_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc,
+                int out_f16) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    static_assert(NC <= kStepCounter, "activation flags sit below the step counter");
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     constexpr int SLOT = MT * R * R;                   // floats of one parked partial
     const int lane = threadIdx.x & 63;
@@ -76,10 +79,14 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
     float* const parts = (float*)(w_lds + S * kStep);
     const uint32_t lds0 = lds_addr(lds);
 
-    if (wave == 0) {
-        for (int i = lane; i < kFlagBytes / 4; i += 64) flags[i] = 0;
-    }
-    barrier_lds();
+    // Every wave clears 128 bytes of the flags, then meets the others at the
+    // one barrier of the kernel.  Loads that write no flag (weights,
+    // activations) are issued before it; every marker after it.
+    auto clear_flags_and_meet = [&]() {
+        static_assert((NC + NL) * 128 == kFlagBytes, "each wave clears 32 flags");
+        if (lane < 32) flags[32 * wave + lane] = 0;
+        barrier_lds();
+    };
 
     if (wave >= NC) {
         // ------------------------------------------------------------ loader wave
@@ -87,33 +94,19 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
         // each step tells the compute waves that the step has landed.  Runs at
         // the highest issue priority so that the compute waves' VALU work never
         // delays the next load.
-        __builtin_amdgcn_s_setprio(3);
-        const int j = wave - NC;
-        // activations: row m of A is nIr 1 KB instructions at m * a_rs (lanes past
-        // the row's 33 * nsg pieces are masked); instructions i = j, j + NL, ...,
-        // started at a per-workgroup offset so that the workgroups, which all read
-        // the same activations, do not all ask for the same lines at once
-        const int nIr = (nsg * 33 + 63) >> 6, nA = M * nIr;
-        const int rot = (int)((blockIdx.x * 7u) % (unsigned)nA);
-        for (int i0 = j; i0 < nA; i0 += NL) {
-            const int i = i0 + rot < nA ? i0 + rot : i0 + rot - nA;
-            const int m = i / nIr, jj = i - m * nIr;
-            const int P = 64 * jj + lane;
-            const int sg = min(P / 33, nsg - 1), c = min(P - 33 * (P / 33), 31);
-            if (P < nsg * 33)
-                dma16(A + (int64_t)m * lda + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + m * a_rs + 1024 * jj));
-        }
-        dma_marker(g_marker_src + lane, lds0 + 4 * j, lane);
-        // weights: four steps (9,216 bytes) form a group of 9 instructions whose
-        // per-lane address pattern repeats from group to group: instruction b of a
-        // group covers pieces 64b + lane, i.e. step d_b = (64b + lane) / 144 of the
+        //
+        // Four steps (9,216 bytes) form a group of 9 instructions whose per-lane
+        // address pattern repeats from group to group: instruction b of a group
+        // covers pieces 64b + lane, i.e. step d_b = (64b + lane) / 144 of the
         // group and a fixed piece (column n, part c) of that step.  Loader j loads
         // step j of every group (steps j, j + 4, ...): instructions
         // b = 9j/4 .. (9j+8)/4 with only the lanes of its step enabled; the
         // instructions that straddle two steps are issued by both of their
         // loaders with complementary lanes.  Each step then has one loader, which
         // issues the step's marker after the step's last load.
+        __builtin_amdgcn_s_setprio(3);
         static_assert(NL == 4, "one step of each group per loader");
+        const int j = wave - NC;
         const int pmax = S * 144 - 1;
         const uint32_t m0 = lds0 + (uint32_t)(kFlagBytes + a_bytes);
         const int b_lo = (9 * j) / 4, b_hi = (9 * j + 8) / 4;   // this loader's instructions in a group
@@ -125,9 +118,9 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
             pat[q] = step_piece_offset<QT>(nn / G, nn % G, c, K) | ((uint32_t)d << 29);
         }
         const bool clamp = (int64_t)(tile0 + nsub) * R > N;   // last workgroup: rows past N reread row N-1
-        for (int g4 = 0; 4 * g4 + j < S; g4++) {
-            const int e = 4 * g4 + j;                  // the step this loader owns in group g4
-            const int te = e / nsteps, se = e - te * nsteps;
+        int te = 0, se = j;                            // step e = te * nsteps + se
+        while (se >= nsteps) { se -= nsteps; te++; }
+        for (int g4 = 0, e = j; e < S; g4++, e += 4) {
             const StepBase<QT> base = step_base<QT>((int64_t)(tile0 + te) * R, G * se, K);
 #pragma unroll
             for (int q = 0; q < 3; q++) {
@@ -147,19 +140,43 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
                 }
                 if ((pb >> 29) == (uint32_t)j && P <= pmax) dma16(src, m0 + (uint32_t)(i << 10));
             }
+            if (g4 == 0) clear_flags_and_meet();
             dma_marker(g_marker_src + lane, lds0 + 64 + 4 * e, lane);
+            se += 4;
+            while (se >= nsteps) { se -= nsteps; te++; }
         }
+        if (j >= S) clear_flags_and_meet();
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         return;
     }
 
     // ---------------------------------------------------------------- compute wave
+    // Activations first: row m of A is nIr 1 KB instructions at m * a_rs (lanes
+    // past the row's 33 * nsg pieces are masked); compute wave c issues
+    // instructions c, c + NC, ..., counted from a per-workgroup offset so that
+    // the workgroups, which all read the same activations, do not all ask for the
+    // same lines at once.
+    {
+        const int nIr = (nsg * 33 + 63) >> 6, nA = M * nIr;
+        const int rot = (int)((blockIdx.x * 7u) % (unsigned)nA);
+        for (int i0 = wave; i0 < nA; i0 += NC) {
+            const int i = i0 + rot < nA ? i0 + rot : i0 + rot - nA;
+            const int m = i / nIr, jj = i - m * nIr;
+            const int P = 64 * jj + lane;
+            const int sg = min(P / 33, nsg - 1), c = min(P - 33 * (P / 33), 31);
+            if (P < nsg * 33)
+                dma16(A + (int64_t)m * lda + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + m * a_rs + 1024 * jj));
+        }
+    }
+    clear_flags_and_meet();
+    signal_own_loads(&flags[wave], lane);
+
     // Steps are taken from a shared counter in step order, which is roughly the
     // order in which they land.  Each step's G-folded partial sums go to the
     // step's own slot; the wave that finishes the last step of a sub-tile adds
     // the sub-tile's slots in step order (a fixed order: results do not depend
     // on timing) and stores them.
-    for (int j = 0; j < NL; j++) wait_flag(&flags[j]);
+    wait_flags(flags, NC, lane);
 
     const Magic mg = make_magic();
     const int r = lane & 15, kg = lane >> 4;
@@ -176,7 +193,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux,
         int e = 0;
         if (lane == 0)
             asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
-                         : "=v"(e) : "v"(lds_addr(&flags[15])), "v"(1) : "memory");
+                         : "=v"(e) : "v"(lds_addr(&flags[kStepCounter])), "v"(1) : "memory");
         e = __builtin_amdgcn_readfirstlane(e);
         if (e >= S) break;
         const int t_in = e / nsteps, s_in = e - t_in * nsteps;
@@ -289,8 +306,8 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
         if (e != hipSuccess) return e;
         attr_set.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kNC + kNL)), p.lds, st, g.W, g.Waux, g.A, g.lda, g.C, g.ldc,
-                       g.out_f16, g.M, g.N, g.K, p.nsub, p.a_rs, p.a_bytes);
+    hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kNC + kNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K, p.nsub,
+                       p.a_rs, p.a_bytes, g.Waux, g.C, g.ldc, g.out_f16);
     return hipGetLastError();
 }
 

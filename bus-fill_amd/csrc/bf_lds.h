@@ -91,6 +91,25 @@ __device__ __forceinline__ void wait_flag(const int* flag) {
     }
 }
 
+// Spin until the n <= 64 consecutive LDS words from `flags` are all nonzero:
+// lane l polls word l, so one LDS read per round covers all of them.
+__device__ __forceinline__ void wait_flags(const int* flags, int n, int lane) {
+    const uint32_t a = lds_addr(flags + (lane < n ? lane : 0));
+    for (int it = 0; it < (1 << 20); it++) {
+        int v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+        if (__builtin_amdgcn_ballot_w64(v == 0) == 0) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Sets the LDS word at `flag` to 1 once every load this wave has issued has
+// completed; for direct-to-LDS loads completion includes the LDS write.
+__device__ __forceinline__ void signal_own_loads(int* flag, int lane) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(flag)), "v"(1) : "memory");
+}
+
 __device__ __forceinline__ float dpp_xor(float v, int ctrl_sel) {
     // quad_perm [1,0,3,2] (xor 1) or [2,3,0,1] (xor 2)
     const int x = __builtin_bit_cast(int, v);
