@@ -116,6 +116,26 @@ __device__ __forceinline__ h8 decode8_mix(const Magic& mg, uint32_t w0, uint32_t
     return __builtin_bit_cast(h8, u4{o[0], o[1], o[2], o[3]});
 }
 
+// Q4_K weights as exact small integers, for the factored product
+//   sum_k a_k w_k = d * sum_k a_k (sc_j q_k) - dmin * sum_j m_j (sum_{k in j} a_k):
+// (bias + q) * sc - bias * sc = sc * q <= 945 is exact in fp16 (s = {sc, sc},
+// c = {-bias * sc, ...} are exact too), so one v_pk_fma_f16 yields two
+// weights with no rounding at all.
+template <bool HI>
+__device__ __forceinline__ h8 decode8_int(const Magic& mg, uint32_t w0, uint32_t w1, h2 s, h2 c) {
+    const uint32_t mask = HI ? mg.hi_mask : mg.lo_mask, bits = HI ? mg.hi_bits : mg.lo_bits;
+    uint32_t p[4] = {perm_b32(w0, w0, SEL_B01), perm_b32(w0, w0, SEL_B23),
+                     perm_b32(w1, w1, SEL_B01), perm_b32(w1, w1, SEL_B23)};
+    h8 out;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const h2 v = __builtin_elementwise_fma(as_h2(and_or(p[i], mask, bits)), s, c);   // v_pk_fma_f16
+        out[2 * i] = v[0];
+        out[2 * i + 1] = v[1];
+    }
+    return out;
+}
+
 // Same for the Q4_0 formats: out = RN((q - 8) * d); (q - 8) is exact, so each
 // element is bit-identical to the reference dequant RN_fp16((q-8)*d).
 template <bool HI>

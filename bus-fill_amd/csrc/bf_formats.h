@@ -92,6 +92,52 @@ __device__ __forceinline__ Scl<QT_Q4_K> scales(const Raw<QT_Q4_K>& raw, int kg) 
     return o;
 }
 
+// Per-lane state of the factored Q4_K product (integer weights sc * q, the
+// scales and mins applied per super-group outside the MFMA):
+//   s_lo/c_lo, s_hi/c_hi: fp16 {sc, sc} and {-bias*sc, ...} of sub-blocks 2kg
+//     (low nibbles, bias 1024) and 2kg+1 (high nibbles, bias 64);
+//   min_hi, min_lo: fp16 {32 m, 32 m'} and {m / 64, m' / 64} of the same two
+//     sub-blocks, the MFMA operand that meets the activation block sums;
+//   d, dmin: the super-block's fp32 scales.
+struct SclK {
+    h2 s_lo, c_lo, s_hi, c_hi;
+    uint32_t min_hi, min_lo;
+    float d, dmin;
+};
+
+__device__ __forceinline__ SclK scales_int(const Raw<QT_Q4_K>& raw, int kg) {
+    const uint32_t s0 = raw.hdr.y, s1 = raw.hdr.z, s2 = raw.hdr.w;
+    const uint32_t sh = 16u * (uint32_t)(kg & 1);
+    const uint32_t sc_lo = (s0 >> sh) & 0x3F3Fu, mn_lo = (s1 >> sh) & 0x3F3Fu;
+    const uint32_t sc_hi = ((s2 >> sh) & 0x0F0Fu) | ((s0 >> (sh + 2)) & 0x3030u);
+    const uint32_t mn_hi = ((s2 >> (sh + 4)) & 0x0F0Fu) | ((s1 >> (sh + 2)) & 0x3030u);
+    const uint32_t sc = kg < 2 ? sc_lo : sc_hi, mn = kg < 2 ? mn_lo : mn_hi;
+    // six-bit codes v to fp16 through the exponent of 1024: bits 0x6400 | v are 1024 + v
+    const uint32_t e1024 = 0x64646464u;
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    SclK o;
+    o.s_lo = as_h2(perm_b32(e1024, sc, 0x04000400u)) - k1024;        // {sc, sc} of sub-block 2kg
+    o.s_hi = as_h2(perm_b32(e1024, sc, 0x04010401u)) - k1024;        // of sub-block 2kg+1
+    o.c_lo = o.s_lo * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+    o.c_hi = o.s_hi * h2{(_Float16)-64.0f, (_Float16)-64.0f};
+    const h2 mb = as_h2(perm_b32(e1024, mn, 0x04010400u));            // {1024 + m, 1024 + m'}
+    o.min_hi = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+        mb, h2{(_Float16)32.0f, (_Float16)32.0f}, h2{(_Float16)-32768.0f, (_Float16)-32768.0f}));
+    o.min_lo = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+        mb, h2{(_Float16)0.015625f, (_Float16)0.015625f}, h2{(_Float16)-16.0f, (_Float16)-16.0f}));
+    o.d = half_bits_to_float(raw.hdr.x & 0xFFFFu);
+    o.dmin = half_bits_to_float(raw.hdr.x >> 16);
+    return o;
+}
+
+// Integer weights sc * q of MFMA i (the same elements as weights() below).
+__device__ __forceinline__ h8 weights_int(const Magic& mg, const Raw<QT_Q4_K>& raw, const SclK& sc, int i) {
+    const uint32_t w[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
+    const int t = i & 3;
+    if (i < 4) return decode8_int<false>(mg, w[2 * t], w[2 * t + 1], sc.s_lo, sc.c_lo);
+    return decode8_int<true>(mg, w[2 * t], w[2 * t + 1], sc.s_hi, sc.c_hi);
+}
+
 __device__ __forceinline__ Scl<QT_PLANES> scales(const Raw<QT_PLANES>& raw, int) {
     Scl<QT_PLANES> o;
     o.da = splat(raw.sc & 0xFFFFu);

@@ -53,7 +53,8 @@ namespace {
 // the compute waves' next-step counter at 60, step markers at 64 + 4e,
 // finished-step counters of sub-tile t at 1024 + 4t; [2048, 2048 + a_bytes)
 // activations, row m at m * a_rs; then the W steps of the
-// workgroup in order (2304 bytes each); then one parked partial per step.
+// workgroup in order (2304 bytes each); then one parked partial per step; then
+// (Q4_K) the activation block sums, 32 bytes per batch row and super-group.
 constexpr int kFlagBytes = 2048;
 constexpr int kMaxSteps = (1024 - 64) / 4;
 constexpr int kMaxSub = (kFlagBytes - 1024) / 4;
@@ -178,14 +179,56 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     // on timing) and stores them.
     wait_flags(flags, NC, lane);
 
+    // Q4_K runs in the factored form sum_k a_k w_k = d * sum_k a_k (sc q_k)
+    // - dmin * sum_j m_j S_j over the sub-blocks j of a super-block, where
+    // S_j = sum_{k in j} a_k.  The block sums are tabulated once: entry
+    // (m, sg, kg) holds fp16 {hi_0, hi_1, lo_0, lo_1} for sub-blocks 2kg, 2kg+1
+    // of super-group sg of batch row m, with S / 32 = hi + lo / 2048 (hi is S / 32
+    // rounded to fp16, lo the rounded remainder: S to about 2^-22).
+    const uint8_t* const tab = (const uint8_t*)(parts + S * SLOT);
+    if constexpr (QT == QT_Q4_K) {
+        const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        for (int u = wave * 64 + lane; u < M * nsg * 4; u += NC * 64) {
+            const int kq = u & 3, rest = u >> 2;
+            const int m = rest / nsg, sg = rest - m * nsg;
+            const uint8_t* src = a_lds + m * a_rs + sg * kASg + 128 * kq;
+            uint32_t hi[2], lo[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float sum = 0.f;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const u4 v = *(const u4*)(src + 64 * h + 16 * q);
+                    sum = __builtin_amdgcn_fdot2(as_h2(v.x), one, sum, false);
+                    sum = __builtin_amdgcn_fdot2(as_h2(v.y), one, sum, false);
+                    sum = __builtin_amdgcn_fdot2(as_h2(v.z), one, sum, false);
+                    sum = __builtin_amdgcn_fdot2(as_h2(v.w), one, sum, false);
+                }
+                const float mean = sum * 0.03125f;
+                const _Float16 mh = (_Float16)mean;
+                const _Float16 ml = (_Float16)((mean - (float)mh) * 2048.0f);
+                hi[h] = __builtin_bit_cast(uint16_t, mh);
+                lo[h] = __builtin_bit_cast(uint16_t, ml);
+            }
+            uint32_t* dst = (uint32_t*)(tab + 8 * u);
+            dst[0] = hi[0] | (hi[1] << 16);
+            dst[1] = lo[0] | (lo[1] << 16);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[wave])), "v"(2) : "memory");
+        wait_flags(flags, NC, lane, 2);
+    }
+
     const Magic mg = make_magic();
     const int r = lane & 15, kg = lane >> 4;
     const int g = r % G, rowl = r / G;
     const uint8_t* arow[MT];
+    const uint8_t* trow[MT];                           // this lane's block-sum entries (Q4_K)
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const int m = min(mt * R + r / G, M - 1);      // padding batch rows reread row M-1
         arow[mt] = a_lds + m * a_rs + g * kASg + 128 * kg;
+        trow[mt] = tab + ((m * nsg + g) * 4 + kg) * 8;
     }
 
     for (;;) {
@@ -200,17 +243,40 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         wait_flag(&flags[16 + e]);
         Raw<QT> raw;
         lds_raw<QT>(raw, w_lds + e * kStep + r * 144, kg);
-        const auto sc = scales(raw, kg);
         const int aoff = G * s_in * kASg;
-        f4 acc[MT];
+        f4 acc[MT], accm[MT];
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < MT; mt++) acc[mt] = accm[mt] = f4{0.f, 0.f, 0.f, 0.f};
+        float d = 1.f, dmin = 0.f;
+        if constexpr (QT == QT_Q4_K) {
+            const SclK sk = scales_int(raw, kg);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const h8 b = weights(mg, raw, sc, i);
+            for (int i = 0; i < 8; i++) {
+                const h8 b = weights_int(mg, raw, sk, i);
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                acc[mt] = mfma16x16x32(*(const h8*)(arow[mt] + aoff + 16 * i), b, acc[mt]);
+                for (int mt = 0; mt < MT; mt++)
+                    acc[mt] = mfma16x16x32(*(const h8*)(arow[mt] + aoff + 16 * i), b, acc[mt]);
+            }
+            // sum_j m_j S_j: the mins {32m, m/64} of sub-blocks 2kg, 2kg+1 meet the
+            // block sums {hi, lo} of the same sub-blocks (k slots 8kg .. 8kg+3)
+            const h8 bm = __builtin_bit_cast(h8, u4{sk.min_hi, sk.min_lo, 0u, 0u});
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const uint32_t* t = (const uint32_t*)(trow[mt] + G * s_in * 32);
+                const h8 am = __builtin_bit_cast(h8, u4{t[0], t[1], 0u, 0u});
+                accm[mt] = mfma16x16x32(am, bm, accm[mt]);
+            }
+            d = sk.d;
+            dmin = sk.dmin;
+        } else {
+            const auto sc = scales(raw, kg);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const h8 b = weights(mg, raw, sc, i);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    acc[mt] = mfma16x16x32(*(const h8*)(arow[mt] + aoff + 16 * i), b, acc[mt]);
+            }
         }
         // fold the G segments (lanes r = G*rowl + g) and park the partial sums
         float* slot = parts + e * SLOT;
@@ -223,6 +289,14 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
 #pragma unroll
                 for (int gg = 1; gg < G; gg++)
                     if (g == gg) y = acc[mt][G * jj + gg];
+                if constexpr (QT == QT_Q4_K) {
+                    // this lane's column is one (row, super-group): apply its d and dmin
+                    float ym = accm[mt][G * jj];
+#pragma unroll
+                    for (int gg = 1; gg < G; gg++)
+                        if (g == gg) ym = accm[mt][G * jj + gg];
+                    y = __builtin_fmaf(d, y, -(dmin * ym));
+                }
                 if constexpr (G >= 2) y += dpp_xor(y, 1);
                 if constexpr (G >= 4) y += dpp_xor(y, 2);
                 if (g == 0) slot[(mt * R + (4 * kg) / G + jj) * R + rowl] = y;
@@ -280,7 +354,8 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p) {
         const int nsub = (T + 256 * rounds - 1) / (256 * rounds);
         const int S = nsub * nsteps;
         if (S > kMaxSteps || nsub > kMaxSub) continue;
-        const int64_t lds = kFlagBytes + (int64_t)p.a_bytes + (int64_t)S * kStep + (int64_t)S * MT * R * R * 4;
+        const int64_t tab = g.qtype == QT_Q4_K ? (int64_t)g.M * nsg * 32 : 0;   // block sums
+        const int64_t lds = kFlagBytes + (int64_t)p.a_bytes + (int64_t)S * kStep + (int64_t)S * MT * R * R * 4 + tab;
         if (lds > kMaxLds) {
             if (nsub == 1) return false;
             continue;

@@ -91,14 +91,14 @@ __device__ __forceinline__ void wait_flag(const int* flag) {
     }
 }
 
-// Spin until the n <= 64 consecutive LDS words from `flags` are all nonzero:
+// Spin until the n <= 64 consecutive LDS words from `flags` are all >= v0:
 // lane l polls word l, so one LDS read per round covers all of them.
-__device__ __forceinline__ void wait_flags(const int* flags, int n, int lane) {
+__device__ __forceinline__ void wait_flags(const int* flags, int n, int lane, int v0 = 1) {
     const uint32_t a = lds_addr(flags + (lane < n ? lane : 0));
     for (int it = 0; it < (1 << 20); it++) {
         int v;
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
-        if (__builtin_amdgcn_ballot_w64(v == 0) == 0) return;
+        if (__builtin_amdgcn_ballot_w64(v < v0) == 0) return;
         __builtin_amdgcn_s_sleep(1);
     }
 }

@@ -4,12 +4,18 @@ Bar: bit-exact for the fp16 dequant.  For the GEMM, every value finite, and
   * max |C - ref| <= 0.6 (the repo gate, kernels/q4k_batched.py:102) and
     relative Frobenius error <= 1e-3, where ref is the fp64 dequantize-then-
     matmul of the reference check (kernels/busfill_v1a.cu:159-167) over the
-    oracle's weights -- applied when the output has >= 64 elements (on one or
-    two outputs the relative error of fp16 weights alone can exceed 1e-3);
-  * elementwise |C - ref16| <= 1e-4 * (|A| . |W16|^T) + 1e-6, where ref16 is
-    the fp64 matmul over the bit-exact fp16 dequant W16: a forward-error bound
-    for fp16 weights with fp32 accumulation, which any wrong index, scale or
-    dropped term exceeds by orders of magnitude.
+    oracle's unrounded weights -- applied when the output has >= 64 elements
+    (on one or two outputs the relative error of fp16 weights alone can exceed
+    1e-3);
+  * an elementwise forward-error bound for the kernel's weight form, which any
+    wrong index, scale or dropped term exceeds by orders of magnitude:
+      fp16 weights (the reference kernel's form, kernels/busfill_v1a.cu:85-86):
+        |C - ref16| <= 1e-4 * (|A| . |W16|^T) + 1e-6, ref16 the fp64 matmul
+        over the bit-exact fp16 dequant W16;
+      factored Q4_K (d * sum a (sc q) - dmin * sum m S, unrounded weights):
+        |C - ref| <= 1e-4 * (|A| . (|d sc q| + |dmin m|)^T) + 1e-6, the bound
+        for the difference of the two terms, whose sizes the oracle gives as
+        the dequant with dmin = 0 and with d = 0.
 All calls go through the C-ABI (busfill.* are thin ctypes wrappers).
 """
 import numpy as np
@@ -61,23 +67,45 @@ def assert_gate(C, ref, what):
     return mae, rfe
 
 
+def q4k_term_sizes(w):
+    """|d sc q| + |dmin m| per weight of a Q4_K matrix, from the oracle's
+    unrounded dequant of two copies: dmin zeroed (d sc q) and d zeroed (-dmin m)."""
+    blk = w.W.reshape(-1, 144)
+    wd, wm = blk.copy(), blk.copy()
+    wd[:, 2:4] = 0
+    wm[:, 0:2] = 0
+    t1 = O.dequant_f32(O.QWeights(O.Q4_K, w.N, w.K, wd.reshape(w.W.shape)))
+    t2 = O.dequant_f32(O.QWeights(O.Q4_K, w.N, w.K, wm.reshape(w.W.shape)))
+    return np.abs(t1) + np.abs(t2)
+
+
 class Ref:
-    """Oracle references for weights w and activations A (rows sliceable)."""
+    """Oracle references for weights w and activations A (rows sliceable).
+
+    check(form=...): "f16" for fp16-weight kernels, "f32" for the factored
+    Q4_K form; None accepts either (automatic kernel choice)."""
 
     def __init__(self, w, A):
         self.exact = O.gemm_f64(w, A)
         self.f16w = O.gemm_f64(w, A, round_w=True)
-        W16 = np.abs(O.dequant_f16(w).view(np.float16).astype(np.float32))
         Aabs = np.abs(A.view(np.float16).astype(np.float32))
-        self.bound = 1e-4 * (Aabs @ W16.T).astype(np.float64) + 1e-6
+        W16 = np.abs(O.dequant_f16(w).view(np.float16).astype(np.float32))
+        self.bounds = {"f16": (self.f16w, 1e-4 * (Aabs @ W16.T).astype(np.float64) + 1e-6)}
+        if w.qtype == O.Q4_K:
+            self.bounds["f32"] = (self.exact, 1e-4 * (Aabs @ q4k_term_sizes(w).T).astype(np.float64) + 1e-6)
 
-    def check(self, C, what, rows=None):
+    def check(self, C, what, rows=None, form=None):
         sl = slice(None) if rows is None else slice(0, rows)
         assert np.isfinite(C).all(), f"{what}: non-finite output"
-        err = np.abs(C - self.f16w[sl])
-        bad = err > self.bound[sl]
-        assert not bad.any(), (f"{what}: {int(bad.sum())} elements beyond the fp16-weight bound, "
-                               f"worst excess {float((err / self.bound[sl]).max()):.3g}x")
+        forms = [form] if form is not None else list(self.bounds)
+        excess = {}
+        for f in forms:
+            if f not in self.bounds:
+                continue
+            ref, bound = self.bounds[f]
+            excess[f] = float((np.abs(C - ref[sl]) / bound[sl]).max()) if C.size else 0.0
+        assert excess, f"{what}: no bound for form {form}"
+        assert min(excess.values()) <= 1.0, f"{what}: beyond the forward-error bound, worst excess {excess}"
         if C.size >= 64:
             assert_gate(C, self.exact[sl], what)
 
@@ -136,7 +164,8 @@ def test_gemm_parity_batch_sweep(dev, qt, K):
     for M in M_LIST:
         for algo in (bf.ALGO_AUTO, bf.ALGO_MFMA):
             C = gpu_gemm(w, A_all[:M], dev, algo=algo, dw=dw)
-            ref.check(C, f"{QT_NAME[qt]} K={K} M={M} algo={algo}", rows=M)
+            ref.check(C, f"{QT_NAME[qt]} K={K} M={M} algo={algo}", rows=M,
+                      form=None if algo == bf.ALGO_AUTO else "f16")
 
 
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
@@ -262,7 +291,7 @@ def test_slab_batch_parity(dev, qt, N, K):
     ref = Ref(w, A)
     for M in (1, 5, 9, 16, 17, 31, 32):
         C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_SLAB, dw=dw)
-        ref.check(C, f"slab {QT_NAME[qt]} N={N} K={K} M={M}", rows=M)
+        ref.check(C, f"slab {QT_NAME[qt]} N={N} K={K} M={M}", rows=M, form="f16")
         assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_SLAB, dw=dw) == C).all()
     with pytest.raises(bf.BusfillError):                  # M > 32 is not served
         gpu_gemm(w, O.gen_act(33, K, seed=1), dev, algo=bf.ALGO_SLAB, dw=dw)
@@ -291,6 +320,30 @@ def test_one_hot_probe_lds_segments(dev):
             for ww in (w, O.planes_to_blocks(w)):
                 C = gpu_gemm(ww, A, dev, algo=bf.ALGO_LDS)
                 assert (C == expect).all(), (m, n, k, Mb, ww.qtype)
+
+
+def test_one_hot_probe_lds_q4k_factored(dev):
+    """Known answers for the factored Q4_K form of the LDS-staged kernel: with a
+    single activation a at (m, k), row m of C is a times column k of the
+    unrounded weights (every sub-block's scale and min, through the block-sum
+    table) and every other row is exactly zero."""
+    N, K = 24, 2048
+    w = O.gen_weights(O.Q4_K, N, K, seed=404)
+    dw = upload(w, dev)
+    W32 = O.dequant_f32(w).astype(np.float64)
+    mag = q4k_term_sizes(w).astype(np.float64)
+    for (m, k) in [(0, 0), (7, 2047), (3, 256 + 31), (4, 511), (1, 1024 + 32), (6, 1536 + 200), (2, 64), (5, 95)]:
+        for Mb in (1, 4, 8):
+            if m >= Mb:
+                continue
+            a = -3.0
+            A = np.zeros((Mb, K), np.uint16)
+            A[m, k] = np.float16(a).view(np.uint16)
+            C = gpu_gemm(w, A, dev, algo=bf.ALGO_LDS, dw=dw)
+            others = np.delete(C, m, axis=0)
+            assert (others == 0).all(), (m, k, Mb)
+            err = np.abs(C[m] - a * W32[:, k])
+            assert (err <= 1e-4 * abs(a) * mag[:, k] + 1e-6).all(), (m, k, Mb, float(err.max()))
 
 
 def test_formats_agree_bitwise_and_runs_are_deterministic(dev):
@@ -335,7 +388,7 @@ def test_dot2_small_batch_parity(dev, K, N):
                 gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DOT2, dw=dw)
             continue
         C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DOT2, dw=dw)
-        ref.check(C, f"dot2 N={N} K={K} M={M}", rows=M)
+        ref.check(C, f"dot2 N={N} K={K} M={M}", rows=M, form="f16")
         assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DOT2, dw=dw) == C).all()
 
 
@@ -356,5 +409,5 @@ def test_lds_small_batch_parity(dev, qt, K, N):
         except bf.BusfillError as e:
             assert not must, f"LDS path refused N={N} K={K} M={M}: {e}"
             continue
-        ref.check(C, f"lds {QT_NAME[qt]} N={N} K={K} M={M}", rows=M)
+        ref.check(C, f"lds {QT_NAME[qt]} N={N} K={K} M={M}", rows=M, form="f32" if qt == O.Q4_K else "f16")
         assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_LDS, dw=dw) == C).all()
