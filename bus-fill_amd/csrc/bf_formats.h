@@ -130,6 +130,44 @@ __device__ __forceinline__ SclK scales_int(const Raw<QT_Q4_K>& raw, int kg) {
     return o;
 }
 
+// Per-lane state of the sub-block rows form (codes enter the MFMA as fp16
+// subnormals; scales applied to the per-sub-block sums afterwards):
+//   c_lo16 = 16 sc and c_hi = sc of sub-blocks 2kg and 2kg+1 (the low codes are
+//   q * 2^-24, the high ones 16 q * 2^-24, so d20 * c * P recovers d sc sum a q),
+//   m_lo, m_hi their mins, d20 = d * 2^20, dmin.
+struct BdScl {
+    float c_lo16, c_hi, m_lo, m_hi, d20, dmin;
+};
+
+__device__ __forceinline__ BdScl scales_bd(const Raw<QT_Q4_K>& raw, int kg) {
+    const uint32_t s0 = raw.hdr.y, s1 = raw.hdr.z, s2 = raw.hdr.w;
+    const uint32_t sh = 16u * (uint32_t)(kg & 1);
+    const uint32_t sc_lo = (s0 >> sh) & 0x3F3Fu, mn_lo = (s1 >> sh) & 0x3F3Fu;
+    const uint32_t sc_hi = ((s2 >> sh) & 0x0F0Fu) | ((s0 >> (sh + 2)) & 0x3030u);
+    const uint32_t mn_hi = ((s2 >> (sh + 4)) & 0x0F0Fu) | ((s1 >> (sh + 2)) & 0x3030u);
+    const uint32_t sc = kg < 2 ? sc_lo : sc_hi, mn = kg < 2 ? mn_lo : mn_hi;
+    BdScl o;
+    o.c_lo16 = (float)(sc & 0xFFu) * 16.0f;
+    o.c_hi = (float)(sc >> 8);
+    o.m_lo = (float)(mn & 0xFFu);
+    o.m_hi = (float)(mn >> 8);
+    o.d20 = half_bits_to_float(raw.hdr.x & 0xFFFFu) * 1048576.0f;
+    o.dmin = half_bits_to_float(raw.hdr.x >> 16);
+    return o;
+}
+
+// Codes of bytes 8t .. 8t+7 of the lane's 32-byte run as MFMA operands, in the
+// order b0 b2 b1 b3 b4 b6 b5 b7: `lo` the low nibbles as the fp16 bit patterns
+// q (value q * 2^-24), `hi` the high nibbles masked in place (16 q * 2^-24).
+// One v_alignbit_b32 and four v_and_b32 per word.
+__device__ __forceinline__ void codes_subnormal(const Raw<QT_Q4_K>& raw, int t, h8& lo, h8& hi) {
+    const uint32_t w[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
+    const uint32_t x0 = w[2 * t], x1 = w[2 * t + 1];
+    const uint32_t r0 = __builtin_amdgcn_alignbit(x0, x0, 8), r1 = __builtin_amdgcn_alignbit(x1, x1, 8);
+    lo = __builtin_bit_cast(h8, u4{x0 & 0x000F000Fu, r0 & 0x000F000Fu, x1 & 0x000F000Fu, r1 & 0x000F000Fu});
+    hi = __builtin_bit_cast(h8, u4{x0 & 0x00F000F0u, r0 & 0x00F000F0u, x1 & 0x00F000F0u, r1 & 0x00F000F0u});
+}
+
 // Integer weights sc * q of MFMA i (the same elements as weights() below).
 __device__ __forceinline__ h8 weights_int(const Magic& mg, const Raw<QT_Q4_K>& raw, const SclK& sc, int i) {
     const uint32_t w[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};

@@ -15,25 +15,37 @@
 //   times the same G segments (row m = G*m' + g).  Only the entries with equal
 //   segments are used; they are summed across the G lanes (DPP).  A work unit
 //   ("step") is always 16 (row, super-group) pairs = 2304 bytes, whatever G is.
-// * Loader waves (kNL per workgroup) move every weight byte HBM -> LDS with
-//   direct-to-LDS loads (global_load_lds_dwordx4: one 64-lane instruction moves
-//   1 KB without touching VGPRs), as runs of G*144 contiguous bytes per row;
-//   loader j owns steps j, j + 4, ...  They never wait: after the last load of
-//   each step the loader issues a one-dword "marker" load of a nonzero word into
-//   that step's flag.  A wave's loads return in issue order, so a visible marker
-//   means the step has landed.  Loaders run at the highest issue priority
-//   (s_setprio) and use a precomputed address pattern, so the compute waves'
-//   VALU work never delays the next load.  The first step's loads are issued
-//   before the workgroup's only barrier (the flags are cleared before it).
+// * Loader waves (the first kNL waves: they start first) move every weight
+//   byte HBM -> LDS with direct-to-LDS loads (global_load_lds_dwordx4: one
+//   64-lane instruction moves 1 KB without touching VGPRs), as runs of G*144
+//   contiguous bytes per row; loader j owns steps j, j + 4, ...  A one-dword
+//   load of the workgroup's first weight line, issued before any address is
+//   computed, starts the first translation early.  Loaders never wait: after
+//   the last load of each step the loader issues a one-dword "marker" load of a
+//   nonzero word into that step's flag.  A wave's loads return in issue order,
+//   so a visible marker means the step has landed.  Loaders run at the highest
+//   issue priority (s_setprio) and use a precomputed address pattern, so the
+//   compute waves' VALU work never delays the next load.  The first step's
+//   loads are issued before the workgroup's only barrier (the flags are
+//   cleared before it).
 // * Compute waves (kNC per workgroup) load the activations A[0:M][0:K] the same
 //   way at the start (each raises a flag once its own loads are complete), then
 //   spin on the markers (ds_read + s_sleep) and take steps from a shared LDS
-//   counter (the order in which steps
-//   land), decode each step from LDS into pre-scaled fp16 MFMA operands and run
-//   8 MFMAs per m-tile.  The folded partial sums of each step are parked in LDS;
-//   a per-sub-tile counter (ds_add_rtn) tells the wave that finishes a
-//   sub-tile's last step to add the sub-tile's partials in step order (a fixed
-//   order: results are deterministic) and store them.
+//   counter (the order in which steps land).  Each step is decoded from LDS
+//   into MFMA operands in one of three forms:
+//     - fp16 weights (Q4_0 formats): RN_fp16((q - 8) d), the reference
+//       kernel's weights, 8 MFMAs per m-tile;
+//     - factored Q4_K: d * sum a (sc q) - dmin * sum_j m_j S_j with the exact
+//       integers sc*q as operands and the min term as one more MFMA against a
+//       table of activation block sums S_j;
+//     - sub-block rows (Q4_K, batch 1): the codes enter the MFMA unscaled as
+//       fp16 subnormals and MFMA row 4*kappa + g takes only lane group kappa's
+//       activations, so each row is one sub-block's sum; the lane scales its
+//       two sub-blocks in fp32.  Fewest VALU operations per weight.
+//   The folded partial sums of each step are parked in LDS; a per-sub-tile
+//   counter (ds_add_rtn) tells the wave that finishes a sub-tile's last step
+//   to add the sub-tile's partials in step order (a fixed order: results are
+//   deterministic) and store them.
 //
 // Weight layout in LDS: the workgroup's steps in order, 2304 bytes each; inside
 // a step, the 144-byte super-group image of column n = 0..15 at n*144 (Q4_K and
@@ -57,10 +69,11 @@ namespace {
 // (Q4_K) the activation block sums, 32 bytes per batch row and super-group.
 constexpr int kFlagBytes = 2048;
 constexpr int kMaxSteps = (1024 - 64) / 4;
-constexpr int kMaxSub = (kFlagBytes - 1024) / 4;
+constexpr int kZeroBytes = 128;                   // [1920, 2048): stays zero (sub-block rows form)
+constexpr int kMaxSub = (kFlagBytes - kZeroBytes - 1024) / 4;
 constexpr int kStepCounter = 15;                  // flags[15]: next step to take
 
-template <int QT, int G, int MT, int NC, int NL>
+template <int QT, int G, int MT, int NC, int NL, bool BD>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
                 int nsub, int a_rs, int a_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc,
@@ -68,7 +81,9 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     static_assert(NC <= kStepCounter, "activation flags sit below the step counter");
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
-    constexpr int SLOT = MT * R * R;                   // floats of one parked partial
+    static_assert(!BD || (QT == QT_Q4_K && G == 4), "sub-block rows: Q4_K with four K segments");
+    // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
+    constexpr int SLOT = BD ? MT * R : MT * R * R;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsg = K >> 8, nsteps = nsg / G;
@@ -89,7 +104,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         barrier_lds();
     };
 
-    if (wave >= NC) {
+    if (wave < NL) {
         // ------------------------------------------------------------ loader wave
         // Issues its loads in order and never waits for them: a marker load after
         // each step tells the compute waves that the step has landed.  Runs at
@@ -107,7 +122,13 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         // issues the step's marker after the step's last load.
         __builtin_amdgcn_s_setprio(3);
         static_assert(NL == 4, "one step of each group per loader");
-        const int j = wave - NC;
+        const int j = wave;
+        // touch the workgroup's first weight line before computing any address, so
+        // that its translation and DRAM page are under way early (the value is
+        // unused; its register stays reserved until the final wait)
+        uint32_t warm;
+        asm volatile("global_load_dword %0, %1, off"
+                     : "=v"(warm) : "v"(w_piece<QT>(W, Waux, (int64_t)tile0 * R, 0, 1, K)) : "memory");
         const int pmax = S * 144 - 1;
         const uint32_t m0 = lds0 + (uint32_t)(kFlagBytes + a_bytes);
         const int b_lo = (9 * j) / 4, b_hi = (9 * j + 8) / 4;   // this loader's instructions in a group
@@ -148,8 +169,10 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         }
         if (j >= S) clear_flags_and_meet();
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("" :: "v"(warm));
         return;
     }
+    const int cw = wave - NL;                          // compute wave index
 
     // ---------------------------------------------------------------- compute wave
     // Activations first: row m of A is nIr 1 KB instructions at m * a_rs (lanes
@@ -160,7 +183,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     {
         const int nIr = (nsg * 33 + 63) >> 6, nA = M * nIr;
         const int rot = (int)((blockIdx.x * 7u) % (unsigned)nA);
-        for (int i0 = wave; i0 < nA; i0 += NC) {
+        for (int i0 = cw; i0 < nA; i0 += NC) {
             const int i = i0 + rot < nA ? i0 + rot : i0 + rot - nA;
             const int m = i / nIr, jj = i - m * nIr;
             const int P = 64 * jj + lane;
@@ -170,7 +193,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         }
     }
     clear_flags_and_meet();
-    signal_own_loads(&flags[wave], lane);
+    signal_own_loads(&flags[cw], lane);
 
     // Steps are taken from a shared counter in step order, which is roughly the
     // order in which they land.  Each step's G-folded partial sums go to the
@@ -182,13 +205,46 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     // Q4_K runs in the factored form sum_k a_k w_k = d * sum_k a_k (sc q_k)
     // - dmin * sum_j m_j S_j over the sub-blocks j of a super-block, where
     // S_j = sum_{k in j} a_k.  The block sums are tabulated once: entry
-    // (m, sg, kg) holds fp16 {hi_0, hi_1, lo_0, lo_1} for sub-blocks 2kg, 2kg+1
-    // of super-group sg of batch row m, with S / 32 = hi + lo / 2048 (hi is S / 32
-    // rounded to fp16, lo the rounded remainder: S to about 2^-22).
+    // (m, sg, kg) covers sub-blocks 2kg, 2kg+1 of super-group sg of batch row m:
+    //   MFMA form: fp16 {hi_0, hi_1, lo_0, lo_1} with S / 32 = hi + lo / 2048 (hi
+    //     is S / 32 rounded to fp16, lo the rounded remainder: S to about 2^-22);
+    //   sub-block rows form (BD): fp32 {S_0, S_1}, and the entry's 128 bytes of
+    //     activations are reordered in place, each run of eight to
+    //     a0 a2 a1 a3 a4 a6 a5 a7, the order in which that form decodes codes.
     const uint8_t* const tab = (const uint8_t*)(parts + S * SLOT);
-    if constexpr (QT == QT_Q4_K) {
+    if constexpr (BD) {
         const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-        for (int u = wave * 64 + lane; u < M * nsg * 4; u += NC * 64) {
+        for (int u = cw * 64 + lane; u < M * nsg * 4; u += NC * 64) {
+            const int kq = u & 3, rest = u >> 2;
+            const int m = rest / nsg, sg = rest - m * nsg;
+            uint8_t* src = a_lds + m * a_rs + sg * kASg + 128 * kq;
+            float sum[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float acc = 0.f;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    u4 v = *(const u4*)(src + 64 * h + 16 * q);
+                    acc = __builtin_amdgcn_fdot2(as_h2(v.x), one, acc, false);
+                    acc = __builtin_amdgcn_fdot2(as_h2(v.y), one, acc, false);
+                    acc = __builtin_amdgcn_fdot2(as_h2(v.z), one, acc, false);
+                    acc = __builtin_amdgcn_fdot2(as_h2(v.w), one, acc, false);
+                    const u4 o = {perm_b32(v.y, v.x, 0x05040100u), perm_b32(v.y, v.x, 0x07060302u),
+                                  perm_b32(v.w, v.z, 0x05040100u), perm_b32(v.w, v.z, 0x07060302u)};
+                    *(u4*)(src + 64 * h + 16 * q) = o;
+                }
+                sum[h] = acc;
+            }
+            float* dst = (float*)(tab + 8 * u);
+            dst[0] = sum[0];
+            dst[1] = sum[1];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[cw])), "v"(2) : "memory");
+        wait_flags(flags, NC, lane, 2);
+    } else if constexpr (QT == QT_Q4_K) {
+        const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        for (int u = cw * 64 + lane; u < M * nsg * 4; u += NC * 64) {
             const int kq = u & 3, rest = u >> 2;
             const int m = rest / nsg, sg = rest - m * nsg;
             const uint8_t* src = a_lds + m * a_rs + sg * kASg + 128 * kq;
@@ -215,7 +271,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
             dst[1] = lo[0] | (lo[1] << 16);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[wave])), "v"(2) : "memory");
+        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[cw])), "v"(2) : "memory");
         wait_flags(flags, NC, lane, 2);
     }
 
@@ -224,10 +280,15 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     const int g = r % G, rowl = r / G;
     const uint8_t* arow[MT];
     const uint8_t* trow[MT];                           // this lane's block-sum entries (Q4_K)
+    // sub-block rows form: MFMA row r = 4 kappa + g takes the activations of
+    // segment g from the k slots of lane group kappa only (zeros elsewhere), so
+    // that row holds the partial sums of one sub-block per column
+    const bool bd_on = (r >> 2) == kg;
+    const uint8_t* const zero16 = lds + kFlagBytes - kZeroBytes;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-        const int m = min(mt * R + r / G, M - 1);      // padding batch rows reread row M-1
-        arow[mt] = a_lds + m * a_rs + g * kASg + 128 * kg;
+        const int m = BD ? min(mt, M - 1) : min(mt * R + r / G, M - 1);   // padding rows reread row M-1
+        arow[mt] = (!BD || bd_on) ? a_lds + m * a_rs + g * kASg + 128 * kg : zero16;
         trow[mt] = tab + ((m * nsg + g) * 4 + kg) * 8;
     }
 
@@ -248,7 +309,46 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[mt] = accm[mt] = f4{0.f, 0.f, 0.f, 0.f};
         float d = 1.f, dmin = 0.f;
-        if constexpr (QT == QT_Q4_K) {
+        if constexpr (BD) {
+            // codes as fp16 subnormals: low nibble q -> q * 2^-24, high nibble
+            // (masked in place) -> 16 q * 2^-24; exact products in the MFMA
+            const BdScl sb = scales_bd(raw, kg);
+            f4 alo[MT], ahi[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) alo[mt] = ahi[mt] = f4{0.f, 0.f, 0.f, 0.f};
+            const int astep = bd_on ? aoff : 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                h8 blo, bhi;
+                codes_subnormal(raw, t, blo, bhi);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    alo[mt] = mfma16x16x32(*(const h8*)(arow[mt] + astep + 16 * t), blo, alo[mt]);
+                    ahi[mt] = mfma16x16x32(*(const h8*)(arow[mt] + astep + 16 * (t + 4)), bhi, ahi[mt]);
+                }
+            }
+            float* slot = parts + e * SLOT;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                // this lane's column n = 4 rowl + g and its sub-blocks 2kg, 2kg+1: row 4kg + g
+                float plo = alo[mt][0], phi = ahi[mt][0];
+#pragma unroll
+                for (int gg = 1; gg < 4; gg++)
+                    if (g == gg) {
+                        plo = alo[mt][gg];
+                        phi = ahi[mt][gg];
+                    }
+                const float* ts = (const float*)(trow[mt] + G * s_in * 32);
+                float y = sb.d20 * __builtin_fmaf(sb.c_lo16, plo, sb.c_hi * phi) -
+                          sb.dmin * __builtin_fmaf(sb.m_lo, ts[0], sb.m_hi * ts[1]);
+                // sum the four lane groups (sub-block pairs), then the four segments
+                y = sum_lane_xor16(y);
+                y = sum_lane_xor32(y);
+                y += dpp_xor(y, 1);
+                y += dpp_xor(y, 2);
+                if (g == 0 && kg == 0) slot[mt * R + rowl] = y;
+            }
+        } else if constexpr (QT == QT_Q4_K) {
             const SclK sk = scales_int(raw, kg);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
@@ -278,28 +378,30 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
                     acc[mt] = mfma16x16x32(*(const h8*)(arow[mt] + aoff + 16 * i), b, acc[mt]);
             }
         }
-        // fold the G segments (lanes r = G*rowl + g) and park the partial sums
-        float* slot = parts + e * SLOT;
+        if constexpr (!BD) {
+            // fold the G segments (lanes r = G*rowl + g) and park the partial sums
+            float* slot = parts + e * SLOT;
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
+            for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
-            for (int jj = 0; jj < 4 / G; jj++) {
-                // register G*jj + g holds batch row (4kg)/G + jj of segment g
-                float y = acc[mt][G * jj];
-#pragma unroll
-                for (int gg = 1; gg < G; gg++)
-                    if (g == gg) y = acc[mt][G * jj + gg];
-                if constexpr (QT == QT_Q4_K) {
-                    // this lane's column is one (row, super-group): apply its d and dmin
-                    float ym = accm[mt][G * jj];
+                for (int jj = 0; jj < 4 / G; jj++) {
+                    // register G*jj + g holds batch row (4kg)/G + jj of segment g
+                    float y = acc[mt][G * jj];
 #pragma unroll
                     for (int gg = 1; gg < G; gg++)
-                        if (g == gg) ym = accm[mt][G * jj + gg];
-                    y = __builtin_fmaf(d, y, -(dmin * ym));
+                        if (g == gg) y = acc[mt][G * jj + gg];
+                    if constexpr (QT == QT_Q4_K) {
+                        // this lane's column is one (row, super-group): apply its d and dmin
+                        float ym = accm[mt][G * jj];
+#pragma unroll
+                        for (int gg = 1; gg < G; gg++)
+                            if (g == gg) ym = accm[mt][G * jj + gg];
+                        y = __builtin_fmaf(d, y, -(dmin * ym));
+                    }
+                    if constexpr (G >= 2) y += dpp_xor(y, 1);
+                    if constexpr (G >= 4) y += dpp_xor(y, 2);
+                    if (g == 0) slot[(mt * R + (4 * kg) / G + jj) * R + rowl] = y;
                 }
-                if constexpr (G >= 2) y += dpp_xor(y, 1);
-                if constexpr (G >= 4) y += dpp_xor(y, 2);
-                if (g == 0) slot[(mt * R + (4 * kg) / G + jj) * R + rowl] = y;
             }
         }
         // count the finished step; the last of the sub-tile reduces and stores it
@@ -335,15 +437,17 @@ constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 struct LdsPlan {
     int G, MT, nsub, grid, a_rs, a_bytes, lds;
+    bool BD;                           // sub-block rows form (Q4_K, one batch row per m-tile)
 };
 
 // Sub-tiles per workgroup: about one workgroup per CU when the LDS holds all of
 // its steps, otherwise the fewest rounds of 256 workgroups that fit.
-bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p) {
+bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false) {
     const int nsg = g.K / 256;
     if (nsg % G) return false;
     const int nsteps = nsg / G, R = 16 / G;
-    if (g.M > MT * R) return false;
+    if (BD ? (g.qtype != QT_Q4_K || G != 4 || g.M > MT) : g.M > MT * R) return false;
+    p.BD = BD;
     const int T = (g.N + R - 1) / R;
     p.G = G;
     p.MT = MT;
@@ -355,7 +459,8 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p) {
         const int S = nsub * nsteps;
         if (S > kMaxSteps || nsub > kMaxSub) continue;
         const int64_t tab = g.qtype == QT_Q4_K ? (int64_t)g.M * nsg * 32 : 0;   // block sums
-        const int64_t lds = kFlagBytes + (int64_t)p.a_bytes + (int64_t)S * kStep + (int64_t)S * MT * R * R * 4 + tab;
+        const int64_t slot = BD ? MT * R : MT * R * R;
+        const int64_t lds = kFlagBytes + (int64_t)p.a_bytes + (int64_t)S * kStep + (int64_t)S * slot * 4 + tab;
         if (lds > kMaxLds) {
             if (nsub == 1) return false;
             continue;
@@ -368,9 +473,9 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p) {
     return false;
 }
 
-template <int QT, int G, int MT>
+template <int QT, int G, int MT, bool BD = false>
 hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
-    auto k = k_gemm_lds<QT, G, MT, kNC, kNL>;
+    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -388,6 +493,9 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
 
 template <int QT>
 hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
+    if constexpr (QT == QT_Q4_K) {
+        if (p.BD) return launch_lds<QT, 4, 1, true>(g, p, st);
+    }
     if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1>(g, p, st);
     if (p.G == 4 && p.MT == 2) return launch_lds<QT, 4, 2>(g, p, st);
     if (p.G == 2 && p.MT == 1) return launch_lds<QT, 2, 1>(g, p, st);
@@ -395,6 +503,9 @@ hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
 }
 
 bool choose_lds(const GemmArgs& g, LdsPlan& p) {
+    // sub-block rows at batch 1 only: from two rows on, its MFMA count doubles
+    // and the factored MFMA form is faster
+    if (g.qtype == QT_Q4_K && g.M == 1 && plan_lds(g, 4, 1, p, true)) return true;
     if (g.M <= 4 && plan_lds(g, 4, 1, p)) return true;
     if (g.M <= 8 && plan_lds(g, 4, 2, p)) return true;
     if (g.M <= 8 && plan_lds(g, 2, 1, p)) return true;

@@ -110,6 +110,24 @@ __device__ __forceinline__ void signal_own_loads(int* flag, int lane) {
     if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(flag)), "v"(1) : "memory");
 }
 
+// v + (v of lane ^ 16) and v + (v of lane ^ 32), the same value in both lanes.
+// v_permlane{16,32}_swap exchanges the odd rows (of 16 or 32 lanes) of its
+// first operand with the even rows of its second; with v in both, the two
+// results hold the lane's and its partner's value.  Written as inline asm with
+// two distinct registers: the builtin form has been compiled to add the first
+// result to itself.
+__device__ __forceinline__ float sum_lane_xor16(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
+__device__ __forceinline__ float sum_lane_xor32(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
 __device__ __forceinline__ float dpp_xor(float v, int ctrl_sel) {
     // quad_perm [1,0,3,2] (xor 1) or [2,3,0,1] (xor 2)
     const int x = __builtin_bit_cast(int, v);
