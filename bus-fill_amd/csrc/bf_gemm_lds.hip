@@ -136,7 +136,9 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
 #pragma unroll
         for (int q = 0; q < 3; q++) {
             const int b = b_lo + q;
-            const int P = 64 * b + lane, d = P / 144, r9 = P - 144 * d, nn = r9 / 9, c = r9 - 9 * nn;
+            // P < 576: P / 144 and r9 / 9 by 24-bit multiplies (exact over that range)
+            const uint32_t P = 64u * b + lane, d = __umul24(P, 7282u) >> 20, r9 = P - 144u * d;
+            const uint32_t nn = __umul24(r9, 7282u) >> 16, c = r9 - 9u * nn;
             pat[q] = step_piece_offset<QT>(nn / G, nn % G, c, K) | ((uint32_t)d << 29);
         }
         const bool clamp = (int64_t)(tile0 + nsub) * R > N;   // last workgroup: rows past N reread row N-1

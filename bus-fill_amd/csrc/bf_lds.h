@@ -140,11 +140,13 @@ __device__ __forceinline__ float dpp_xor(float v, int ctrl_sel) {
 // the planes layout's scale array), and the scalar bases of a step.
 template <int QT>
 __device__ __forceinline__ uint32_t step_piece_offset(int rowl, int g, int c, int K) {
+    // rowl < 16, and K < 81920 (the activations fit in LDS), so the row strides
+    // stay far below 2^24 bytes: 24-bit multiplies
     if constexpr (QT == QT_PLANES) {
-        if (c == 0) return (uint32_t)(rowl * (K >> 4) + 16 * g) | (1u << 28);
-        return (uint32_t)(rowl * (K >> 1) + 128 * g + 16 * (c - 1));
+        if (c == 0) return (__umul24((uint32_t)rowl, (uint32_t)(K >> 4)) + 16u * g) | (1u << 28);
+        return __umul24((uint32_t)rowl, (uint32_t)(K >> 1)) + 128u * g + 16u * (c - 1);
     } else {
-        return (uint32_t)(rowl * ((K >> 8) * 144) + 144 * g + 16 * c);
+        return __umul24((uint32_t)rowl, (uint32_t)((K >> 8) * 144)) + 144u * g + 16u * c;
     }
 }
 
