@@ -339,12 +339,12 @@ def main():
     ap.add_argument("--batches", default="1,8,32")
     ap.add_argument("--graph", default="both", choices=["0", "1", "both"],
                     help="issue launches on the stream (0), replay a HIP graph (1), or time both")
-    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "dot2", "simple", "lds", "slab"])
+    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "dot2", "simple", "lds", "slab", "split"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--out", default=None, help="also write the full record to this JSON file")
     args = ap.parse_args()
-    args.algo_id = {"auto": 0, "mfma": 1, "dot2": 2, "simple": 3, "lds": 4, "slab": 5}[args.algo]
+    args.algo_id = {"auto": 0, "mfma": 1, "dot2": 2, "simple": 3, "lds": 4, "slab": 5, "split": 6}[args.algo]
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the GEMM on a single MI355X and has no "

@@ -27,7 +27,7 @@ Q4_0, Q4_0_PLANES, Q4_K = 0, 1, 2
 # bf_otype
 OUT_F32, OUT_F16 = 0, 1
 # bf_algo
-ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB = 0, 1, 2, 3, 4, 5
+ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT = 0, 1, 2, 3, 4, 5, 6
 
 EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_dequant_f16",
            "bf_status_str", "bf_last_error", "bf_version")

@@ -68,7 +68,7 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
     if (otype != BF_OUT_F32 && otype != BF_OUT_F16) return fail(BF_ERR_INVALID, "unknown otype %d", (int)otype);
     if (!aligned(A, 2)) return fail(BF_ERR_INVALID, "A is not 2-byte aligned");
     if (!aligned(C, otype == BF_OUT_F32 ? 4 : 2)) return fail(BF_ERR_INVALID, "C is not aligned to its element");
-    if (algo < BF_ALGO_AUTO || algo > BF_ALGO_SLAB) return fail(BF_ERR_INVALID, "unknown algo %d", (int)algo);
+    if (algo < BF_ALGO_AUTO || algo > BF_ALGO_SPLIT) return fail(BF_ERR_INVALID, "unknown algo %d", (int)algo);
 
     const size_t csize = otype == BF_OUT_F32 ? 4 : 2;
     hipStream_t hs = (hipStream_t)stream;
@@ -91,6 +91,7 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
         if (use == BF_ALGO_AUTO) {
             if (!fast) use = BF_ALGO_SIMPLE;
             else if (bf::lds_supports(g)) use = BF_ALGO_LDS;
+            else if (bf::split_supports(g)) use = BF_ALGO_SPLIT;
             else if (bf::slab_supports(g)) use = BF_ALGO_SLAB;
             else if (g.M <= kDot2MaxM && bf::dot2_supports(g)) use = BF_ALGO_DOT2;
             else use = BF_ALGO_MFMA;
@@ -111,6 +112,12 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
                     return fail(BF_ERR_UNSUPPORTED, "slab path does not serve qtype %d M=%d N=%d K=%d",
                                 (int)qtype, g.M, N, K);
                 e = bf::gemm_slab(g, hs);
+                break;
+            case BF_ALGO_SPLIT:
+                if (!fast || !bf::split_supports(g))
+                    return fail(BF_ERR_UNSUPPORTED, "K-split path does not serve qtype %d M=%d N=%d K=%d",
+                                (int)qtype, g.M, N, K);
+                e = bf::gemm_split(g, hs);
                 break;
             case BF_ALGO_LDS:
                 if (!fast || !bf::lds_supports(g))

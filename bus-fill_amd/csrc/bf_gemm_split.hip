@@ -1,0 +1,366 @@
+// K-split LDS-resident MFMA GEMM for batches of up to 32 rows (k_gemm_split).
+//
+//   C[m][n] = sum_k A[m][k] * dequant(W)[n][k]      (fp32 accumulation)
+//
+// At batch 9-32 the activations, not the weights, decide the time: a
+// workgroup that covers all of K needs all of A (328 KB at M = 32, K = 5120),
+// far more than its share of the weights, and 256 such copies cross the L2.
+// Splitting K in S parts divides both the activations each workgroup reads and
+// the total activation traffic by S:
+//
+// * Workgroup (row group rg, split s) owns nt 16-row tiles and the super-groups
+//   [s * nsgS, (s + 1) * nsgS).  At N = K = 5120, M = 32: S = 4, nt = 5, 256
+//   workgroups, each with 57.6 KB of weights and 82 KB of activations, all of it
+//   resident in LDS at once (no ring, no slot reuse).
+// * The data of one local super-group i (the activation slab A[0:M][256 i ..
+//   256 i + 256) followed by the nt tiles' 144-byte weight images) is one
+//   contiguous LDS "unit" of 16-byte pieces.  Four loader waves split each
+//   unit's 1 KB direct-to-LDS instructions round robin (per-lane addresses are
+//   computed once; a unit only adds a per-piece stride) and each ends its share
+//   of a unit with a one-dword marker load; a unit has landed when its four
+//   markers are visible (a wave's loads return in order).
+// * Compute wave c owns tile c % nt and the super-groups u, u + U, ... of it
+//   (u = c / nt, U = number of waves on that tile), accumulating all batch rows
+//   (MT m-tiles of 16) in registers.  The other waves of a tile park their sums
+//   in LDS and the tile's first wave adds them in wave order.
+// * With S > 1 the tile sums are written to a per-stream workspace; the split
+//   that finishes last (a device-scope counter per row group) adds the S
+//   partials in split order and writes C.  The order never depends on timing,
+//   so results are deterministic; the last split resets the counter, so the
+//   workspace is ready for the next launch on the stream.  Partials are written
+//   and read with device-coherent (agent-scope) accesses, which reach the point
+//   of coherence of the XCDs' L2s: a writer's accesses are complete
+//   (s_waitcnt vmcnt(0)) before its workgroup counts itself, and the last
+//   split reads only after its own count, so no whole-L2 write-back or
+//   invalidate (what a release/acquire fence costs) is needed.
+#include <algorithm>
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "bf_launch.h"
+#include "bf_lds.h"
+
+namespace bf {
+namespace {
+
+// LDS: [0, 2048) flags: owners-done counter at 4, is-last word at 8, unit
+// markers of loader j for unit i at 64 + 16 i + 4 j, park flag of compute wave c
+// at 1024 + 4 c; then the units; then the parked sums.
+constexpr int kSpFlags = 2048;
+constexpr int kSpMaxUnits = (1024 - 64) / 16;
+constexpr int kSpNC = 12, kSpNL = 4;    // compute and loader waves per workgroup
+constexpr int kSpQS = 12;               // instruction slots per loader and unit
+constexpr int kSpMaxPieces = 64 * kSpNL * kSpQS;
+constexpr int kSpCounterStride = 64;    // one row-group counter per 256-byte line: no shared lines
+
+template <int QT, int MT>
+__global__ __launch_bounds__(64 * (kSpNC + kSpNL))
+void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
+                  int nt, int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C,
+                  int ldc, int out_f16, float* __restrict__ ws, unsigned* __restrict__ counters) {
+    constexpr int NC = kSpNC, NL = kSpNL;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rg = blockIdx.x / S, s = blockIdx.x - rg * S;
+    const int sg0 = s * nsgS;
+    int* const flags = (int*)lds;
+    const uint32_t lds0 = lds_addr(lds);
+    const int PA = M * 33, PW = nt * 144;                // activation and weight pieces of a unit
+    const int I = (PA + PW + 63) >> 6;                   // 1 KB instructions per unit
+
+    auto clear_flags_and_meet = [&]() {
+        static_assert((NC + NL) * 128 == kSpFlags, "each wave clears 32 flags");
+        if (lane < 32) flags[32 * wave + lane] = 0;
+        barrier_lds();
+    };
+
+    if (wave < NL) {
+        // ------------------------------------------------------------ loader wave
+        __builtin_amdgcn_s_setprio(3);
+        const int j = wave;
+        // instruction q = j + 4 * slot covers pieces 64 q + lane of every unit;
+        // the piece's address in unit i is src + i * step (step 0: lane idle)
+        const uint8_t* src[kSpQS];
+        uint32_t step[kSpQS];
+#pragma unroll
+        for (int q2 = 0; q2 < kSpQS; q2++) {
+            const uint32_t P = 64u * (j + 4 * q2) + lane;
+            src[q2] = W;
+            step[q2] = 0;
+            if (P < (uint32_t)PA) {
+                // activation piece: row m, 16-byte part c (part 32 is the row's bank padding)
+                const uint32_t m = __umul24(P, 1986u) >> 16, c = P - 33u * m;     // P < 3072
+                if (c < 32) {
+                    src[q2] = (const uint8_t*)(A + (int64_t)m * lda + 256 * sg0 + 8 * c);
+                    step[q2] = 512;
+                }
+            } else if (P < (uint32_t)(PA + PW)) {
+                // weight piece: tile t, row n of the tile, part c of its 144-byte image
+                const uint32_t pw = P - PA, t = __umul24(pw, 7282u) >> 20, rem = pw - 144u * t;
+                const uint32_t n = __umul24(rem, 7282u) >> 16, c = rem - 9u * n;
+                const int64_t row = min((int64_t)(rg * nt + (int)t) * 16 + (int)n, (int64_t)N - 1);
+                src[q2] = w_piece<QT>(W, Waux, row, sg0, (int)c, K);
+                step[q2] = QT == QT_PLANES ? (c == 0 ? 16u : 128u) : 144u;
+            }
+        }
+        for (int i = 0; i < nsgS; i++) {
+            const uint32_t ub = lds0 + (uint32_t)(kSpFlags + i * unit_bytes);
+#pragma unroll
+            for (int q2 = 0; q2 < kSpQS; q2++) {
+                const int q = j + 4 * q2;
+                if (q >= I) break;
+                if (step[q2]) dma16(src[q2] + (uint32_t)i * step[q2], ub + (uint32_t)(q << 10));
+            }
+            if (i == 0) clear_flags_and_meet();
+            dma_marker(g_marker_src + lane, lds0 + (uint32_t)(64 + 16 * i + 4 * j), lane);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
+
+    // ---------------------------------------------------------------- compute wave
+    clear_flags_and_meet();
+    const int c = wave - NL;
+    const int t = c % nt, u = c / nt;
+    const int U = (NC - 1 - t) / nt + 1;                 // waves on tile t
+    const Magic mg = make_magic();
+    const int r = lane & 15, kg = lane >> 4;
+    int arow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) arow[mt] = min(mt * 16 + r, M - 1) * 528 + 128 * kg;   // pad rows reread M-1
+    f4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
+
+    for (int i = u; i < nsgS; i += U) {
+        wait_flags(flags + 16 + 4 * i, NL, lane);
+        const uint8_t* unit = lds + kSpFlags + i * unit_bytes;
+        Raw<QT> raw;
+        lds_raw<QT>(raw, unit + PA * 16 + t * 2304 + r * 144, kg);
+        const auto sc = scales(raw, kg);
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++) {
+            const h8 b = weights(mg, raw, sc, ii);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) acc[mt] = mfma16x16x32(*(const h8*)(unit + arow[mt] + 16 * ii), b, acc[mt]);
+        }
+    }
+
+    // the tile's first wave adds the others' sums (in wave order) and writes the tile
+    float* const park = (float*)(lds + kSpFlags + nsgS * unit_bytes);
+    if (u > 0) {
+        float* mine = park + (c - nt) * MT * 256;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) mine[(mt * 4 + i) * 64 + lane] = acc[mt][i];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[256 + c])), "v"(1) : "memory");
+    } else {
+        for (int u2 = 1; u2 < U; u2++) {
+            const int c2 = t + nt * u2;
+            wait_flag(&flags[256 + c2]);
+            const float* theirs = park + (c2 - nt) * MT * 256;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[mt][i] += theirs[(mt * 4 + i) * 64 + lane];
+        }
+        const int64_t n = (int64_t)(rg * nt + t) * 16 + r;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = mt * 16 + 4 * kg + i;
+                if (m < M && n < N) {
+                    const float v = acc[mt][i];
+                    if (S > 1) __hip_atomic_store(&ws[((int64_t)s * M + m) * N + n], v, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+                    else if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + n] = (_Float16)v;
+                    else ((float*)C)[(int64_t)m * ldc + n] = v;
+                }
+            }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (lane == 0) asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[1])), "v"(1) : "memory");
+    }
+    if (S == 1) return;
+
+    // --------------------------------------------------------- cross-split sum
+    if (c == 0) {
+        wait_flags(&flags[1], 1, lane, min(nt, NC));
+        unsigned old = 0;
+        unsigned* const cnt = counters + rg * kSpCounterStride;
+        if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __builtin_amdgcn_readfirstlane(old);
+        const int last = old == (unsigned)(S - 1);
+        if (last && lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[2])), "v"(last ? 1 : 2) : "memory");
+    }
+    wait_flags(&flags[2], 1, lane);
+    if (flags[2] != 1) return;
+    // each lane takes up to four outputs at a time and issues all of their
+    // partial loads (up to 16) before the first add: one round trip per batch
+    const int rows = nt * 16;
+    const int64_t n0 = (int64_t)rg * rows, plane = (int64_t)M * N;
+    for (int v0 = c * 64 + lane; v0 < rows * M; v0 += 4 * NC * 64) {
+        int64_t at[4];
+        bool ok[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int v = v0 + q * NC * 64;
+            const int m = v / rows, nl = v - m * rows;
+            ok[q] = v < rows * M && n0 + nl < N;
+            at[q] = ok[q] ? (int64_t)m * N + n0 + nl : 0;
+        }
+        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < S; s0 += 4) {
+            float x[4][4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    x[q][k] = ok[q] && s0 + k < S
+                                  ? __hip_atomic_load(&ws[(s0 + k) * plane + at[q]], __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT)
+                                  : 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (s0 + k < S) sum[q] += x[q][k];           // splits in order
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (!ok[q]) continue;
+            const int v = v0 + q * NC * 64;
+            const int m = v / rows, nl = v - m * rows;
+            const int64_t n = n0 + nl;
+            if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + n] = (_Float16)sum[q];
+            else ((float*)C)[(int64_t)m * ldc + n] = sum[q];
+        }
+    }
+}
+
+__global__ void k_zero_u32(unsigned* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+struct SplitPlan {
+    int S, nt, nsgS, MT, grid, unit_bytes, lds;
+};
+
+int split_lds_bytes(int M, int nt, int nsgS, int MT) {
+    const int unit = (M * 33 + nt * 144) * 16;
+    const int parks = (kSpNC > nt ? kSpNC - nt : 0) * MT * 1024;
+    return kSpFlags + nsgS * unit + parks;
+}
+
+// S divides the super-groups; nt tiles per workgroup (<= the compute waves);
+// the estimate is rounds of 256 workgroups times the bytes each one loads,
+// plus the partials' round trip when S > 1.
+bool plan_split(const GemmArgs& g, SplitPlan& p) {
+    if (g.M > 32 || g.K % 256) return false;
+    const int nsg = g.K / 256, T = (g.N + 15) / 16;
+    const int MT = g.M <= 16 ? 1 : 2;
+    double best = 1e300;
+    for (int S = 1; S <= nsg; S++) {
+        if (nsg % S) continue;
+        const int nsgS = nsg / S;
+        if (nsgS > kSpMaxUnits) continue;
+        for (int rounds = 1; rounds <= 16; rounds++) {
+            const int nt = (int)(((int64_t)T * S + 256LL * rounds - 1) / (256LL * rounds));
+            if (nt > kSpNC || g.M * 33 + nt * 144 > kSpMaxPieces) continue;
+            if (split_lds_bytes(g.M, nt, nsgS, MT) > kMaxLds) continue;
+            const int grid = (T + nt - 1) / nt * S;
+            const double per_wg = (double)nt * nsgS * 2304 + (double)g.M * nsgS * 512 +
+                                  (S > 1 ? 3.0 * nt * 16 * g.M * 4 : 0.0);
+            const double est = (double)((grid + 255) / 256) * per_wg;
+            if (est < best) {
+                best = est;
+                p = SplitPlan{S, nt, nsgS, MT, grid, (g.M * 33 + nt * 144) * 16, split_lds_bytes(g.M, nt, nsgS, MT)};
+            }
+            break;                                       // fewer rounds fit first: more would only add rounds
+        }
+    }
+    return best < 1e300;
+}
+
+// Per-(device, stream) workspace: row-group counters (kept zero between
+// launches by the kernel) followed by the split partials.  Grown on demand and
+// kept until the process ends; launches on one stream are ordered, so they can
+// share it.
+hipError_t workspace(hipStream_t st, size_t counter_bytes, size_t part_bytes, unsigned** counters, float** parts) {
+    static std::mutex mu;
+    static std::map<std::pair<int, uintptr_t>, std::pair<uint8_t*, std::pair<size_t, size_t>>> cache;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    auto& slot = cache[{dev, (uintptr_t)st}];
+    if (!slot.first || slot.second.first < counter_bytes || slot.second.second < part_bytes) {
+        const size_t cb = std::max(counter_bytes, slot.second.first), pb = std::max(part_bytes, slot.second.second);
+        uint8_t* p = nullptr;
+        e = hipMalloc((void**)&p, cb + pb);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_zero_u32, dim3(64), dim3(256), 0, st, (unsigned*)p, (int)(cb / 4));
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        slot = {p, {cb, pb}};                            // a replaced buffer is kept: in-flight launches may use it
+    }
+    *counters = (unsigned*)slot.first;
+    *parts = (float*)(slot.first + slot.second.first);
+    return hipSuccess;
+}
+
+template <int QT, int MT>
+hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, hipStream_t st) {
+    auto k = k_gemm_split<QT, MT>;
+    static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(attr_set.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        if (e != hipSuccess) return e;
+        attr_set.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    unsigned* counters = nullptr;
+    float* parts = nullptr;
+    if (p.S > 1) {
+        const int T = (g.N + 15) / 16, rgs = (T + p.nt - 1) / p.nt;
+        e = workspace(st, (size_t)rgs * kSpCounterStride * 4, (size_t)p.S * g.M * g.N * 4, &counters, &parts);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kSpNC + kSpNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K,
+                       p.nt, p.S, p.nsgS, p.unit_bytes, g.Waux, g.C, g.ldc, g.out_f16, parts, counters);
+    return hipGetLastError();
+}
+
+template <int QT>
+hipError_t dispatch_split(const GemmArgs& g, const SplitPlan& p, hipStream_t st) {
+    return p.MT == 1 ? launch_split<QT, 1>(g, p, st) : launch_split<QT, 2>(g, p, st);
+}
+
+}  // namespace
+
+bool split_supports(const GemmArgs& g) {
+    SplitPlan p;
+    if (g.qtype == QT_PLANES && ((uintptr_t)g.Waux & 15)) return false;
+    return plan_split(g, p);
+}
+
+hipError_t gemm_split(const GemmArgs& g, hipStream_t st) {
+    SplitPlan p;
+    if (!plan_split(g, p)) return hipErrorInvalidValue;
+    switch (g.qtype) {
+        case QT_Q4_K: return dispatch_split<QT_Q4_K>(g, p, st);
+        case QT_PLANES: return dispatch_split<QT_PLANES>(g, p, st);
+        default: return dispatch_split<QT_Q4_0>(g, p, st);
+    }
+}
+
+}  // namespace bf

@@ -26,6 +26,8 @@ hipError_t gemm_lds(const GemmArgs& g, hipStream_t st);
 bool lds_supports(const GemmArgs& g);
 hipError_t gemm_slab(const GemmArgs& g, hipStream_t st);
 bool slab_supports(const GemmArgs& g);
+hipError_t gemm_split(const GemmArgs& g, hipStream_t st);
+bool split_supports(const GemmArgs& g);
 bool dot2_supports(const GemmArgs& g);
 hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
                        int N, int K, hipStream_t st);

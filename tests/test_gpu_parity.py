@@ -297,6 +297,49 @@ def test_slab_batch_parity(dev, qt, N, K):
         gpu_gemm(w, O.gen_act(33, K, seed=1), dev, algo=bf.ALGO_SLAB, dw=dw)
 
 
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+@pytest.mark.parametrize("N,K", [(1, 256), (77, 2048), (200, 5120), (5120, 5120), (600, 17408), (7168, 5120)])
+def test_split_batch_parity(dev, qt, N, K):
+    """The K-split kernel: splits combined through the per-stream workspace
+    (last split adds them in split order), ragged N (clamped weight rows), every
+    batch size it serves, identical results on repeated runs."""
+    w = O.gen_weights(qt, N, K, seed=K * 11 + N + qt)
+    dw = upload(w, dev)
+    A = O.gen_act(32, K, seed=K + 17)
+    ref = Ref(w, A)
+    for M in (1, 5, 9, 16, 17, 31, 32):
+        C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_SPLIT, dw=dw)
+        ref.check(C, f"split {QT_NAME[qt]} N={N} K={K} M={M}", rows=M, form="f16")
+        assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_SPLIT, dw=dw) == C).all()
+    with pytest.raises(bf.BusfillError):                  # M > 32 is not served
+        gpu_gemm(w, O.gen_act(33, K, seed=1), dev, algo=bf.ALGO_SPLIT, dw=dw)
+
+
+def test_split_workspace_reuse_across_shapes(dev):
+    """Launches of different shapes back to back on one stream share its
+    workspace: the per-row-group counters must be back at zero after every
+    launch, or a later launch would finish with the wrong split."""
+    cases = [(5120, 5120, 32), (200, 5120, 9), (7168, 5120, 17), (5120, 5120, 32), (600, 17408, 32)]
+    prepared = []
+    for i, (N, K, M) in enumerate(cases):
+        w = O.gen_weights(O.Q4_K, N, K, seed=300 + i)
+        A = O.gen_act(M, K, seed=400 + i)
+        prepared.append((w, upload(w, dev), A, Ref(w, A)))
+    outs = []
+    for rep in range(3):
+        for (w, dw, A, _) in prepared:
+            Ad = to_dev(A, dev)
+            Cd = torch.full((A.shape[0], w.N), float("nan"), device=dev)
+            bf.gemm(w.qtype, dw[0], dw[1], Ad, Cd, A.shape[0], w.N, w.K, algo=bf.ALGO_SPLIT)
+            outs.append(Cd)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i, (w, _, A, ref) in enumerate(prepared):
+            C = outs[rep * len(prepared) + i].cpu().numpy().astype(np.float64)
+            ref.check(C, f"split reuse rep={rep} case={i}", form="f16")
+            assert (C == outs[i].cpu().numpy()).all()
+
+
 def test_one_hot_probe_lds_segments(dev):
     """Known answers for the K-segment mapping of the LDS-staged kernel: one
     weight (n, k) and one activation (m, k) set, everything else zero, for k in
