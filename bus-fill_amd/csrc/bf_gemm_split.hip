@@ -54,6 +54,12 @@ constexpr int kSpNC = 12, kSpNL = 4;    // compute and loader waves per workgrou
 constexpr int kSpQS = 12;               // instruction slots per loader and unit
 constexpr int kSpMaxPieces = 64 * kSpNL * kSpQS;
 constexpr int kSpCounterStride = 64;    // one row-group counter per 256-byte line: no shared lines
+constexpr int kCoherent = 16;           // buffer access cache policy: sc1, coherent across the XCDs' L2s
+
+// Buffer resource over the split partials [S][N][Mp] (fp32).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t workspace_rsrc(float* ws, int S, int N, int Mp) {
+    return __builtin_amdgcn_make_buffer_rsrc(ws, (short)0, (int)((int64_t)S * N * Mp * 4), 0x00020000);
+}
 
 template <int QT, int MT>
 __global__ __launch_bounds__(64 * (kSpNC + kSpNL))
@@ -70,6 +76,7 @@ void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A,
     const uint32_t lds0 = lds_addr(lds);
     const int PA = M * 33, PW = nt * 144;                // activation and weight pieces of a unit
     const int I = (PA + PW + 63) >> 6;                   // 1 KB instructions per unit
+    const int Mp = (M + 3) & ~3;                         // workspace rows, whole quads
 
     auto clear_flags_and_meet = [&]() {
         static_assert((NC + NL) * 128 == kSpFlags, "each wave clears 32 flags");
@@ -170,19 +177,28 @@ void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A,
                 for (int i = 0; i < 4; i++) acc[mt][i] += theirs[(mt * 4 + i) * 64 + lane];
         }
         const int64_t n = (int64_t)(rg * nt + t) * 16 + r;
+        if (S > 1) {
+            // workspace [s][n][Mp]: this lane's four rows of an m-tile are one 16-byte store
+            const __amdgpu_buffer_rsrc_t wr = workspace_rsrc(ws, S, N, Mp);
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = mt * 16 + 4 * kg + i;
-                if (m < M && n < N) {
-                    const float v = acc[mt][i];
-                    if (S > 1) __hip_atomic_store(&ws[((int64_t)s * M + m) * N + n], v, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-                    else if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + n] = (_Float16)v;
-                    else ((float*)C)[(int64_t)m * ldc + n] = v;
-                }
+            for (int mt = 0; mt < MT; mt++) {
+                const int m4 = mt * 16 + 4 * kg;
+                if (m4 < Mp && n < N)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr,
+                                                           (int)((((int64_t)s * N + n) * Mp + m4) * 4), 0, kCoherent);
             }
+        } else {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int m = mt * 16 + 4 * kg + i;
+                    if (m < M && n < N) {
+                        if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + n] = (_Float16)acc[mt][i];
+                        else ((float*)C)[(int64_t)m * ldc + n] = acc[mt][i];
+                    }
+                }
+        }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (lane == 0) asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[1])), "v"(1) : "memory");
     }
@@ -201,31 +217,35 @@ void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A,
     }
     wait_flags(&flags[2], 1, lane);
     if (flags[2] != 1) return;
-    // each lane takes up to four outputs at a time and issues all of their
-    // partial loads (up to 16) before the first add: one round trip per batch
-    const int rows = nt * 16;
-    const int64_t n0 = (int64_t)rg * rows, plane = (int64_t)M * N;
-    for (int v0 = c * 64 + lane; v0 < rows * M; v0 += 4 * NC * 64) {
-        int64_t at[4];
+    // each lane takes up to four quads (one row n, rows m4 .. m4+3) at a time and
+    // issues all of their partial loads (up to 16) before the first add
+    const int rows = nt * 16, nq = rows * (Mp / 4);
+    const int64_t n0 = (int64_t)rg * rows;
+    const __amdgpu_buffer_rsrc_t wr = workspace_rsrc(ws, S, N, Mp);
+    for (int v0 = c * 64 + lane; v0 < nq; v0 += 4 * NC * 64) {
+        int off[4];
         bool ok[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int v = v0 + q * NC * 64;
-            const int m = v / rows, nl = v - m * rows;
-            ok[q] = v < rows * M && n0 + nl < N;
-            at[q] = ok[q] ? (int64_t)m * N + n0 + nl : 0;
+            const int nl = v / (Mp / 4), m4 = 4 * (v - nl * (Mp / 4));
+            ok[q] = v < nq && n0 + nl < N;
+            off[q] = ok[q] ? (int)(((n0 + nl) * Mp + m4) * 4) : 0;
         }
-        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+        f4 sum[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) sum[q] = f4{0.f, 0.f, 0.f, 0.f};
         for (int s0 = 0; s0 < S; s0 += 4) {
-            float x[4][4];
+            f4 x[4][4];
 #pragma unroll
             for (int q = 0; q < 4; q++)
 #pragma unroll
                 for (int k = 0; k < 4; k++)
                     x[q][k] = ok[q] && s0 + k < S
-                                  ? __hip_atomic_load(&ws[(s0 + k) * plane + at[q]], __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT)
-                                  : 0.f;
+                                  ? __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                               wr, off[q] + (int)((int64_t)(s0 + k) * N * Mp * 4), 0,
+                                                               kCoherent))
+                                  : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int q = 0; q < 4; q++)
 #pragma unroll
@@ -236,10 +256,14 @@ void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A,
         for (int q = 0; q < 4; q++) {
             if (!ok[q]) continue;
             const int v = v0 + q * NC * 64;
-            const int m = v / rows, nl = v - m * rows;
+            const int nl = v / (Mp / 4), m4 = 4 * (v - nl * (Mp / 4));
             const int64_t n = n0 + nl;
-            if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + n] = (_Float16)sum[q];
-            else ((float*)C)[(int64_t)m * ldc + n] = sum[q];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (m4 + i >= M) break;
+                if (out_f16) ((_Float16*)C)[(int64_t)(m4 + i) * ldc + n] = (_Float16)sum[q][i];
+                else ((float*)C)[(int64_t)(m4 + i) * ldc + n] = sum[q][i];
+            }
         }
     }
 }
@@ -263,6 +287,7 @@ int split_lds_bytes(int M, int nt, int nsgS, int MT) {
 // plus the partials' round trip when S > 1.
 bool plan_split(const GemmArgs& g, SplitPlan& p) {
     if (g.M > 32 || g.K % 256) return false;
+    if ((int64_t)g.K / 256 * g.N * 32 * 4 >= (1LL << 31)) return false;   // partials addressed by 32-bit offsets
     const int nsg = g.K / 256, T = (g.N + 15) / 16;
     const int MT = g.M <= 16 ? 1 : 2;
     double best = 1e300;
@@ -332,7 +357,8 @@ hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, hipStream_t st) {
     float* parts = nullptr;
     if (p.S > 1) {
         const int T = (g.N + 15) / 16, rgs = (T + p.nt - 1) / p.nt;
-        e = workspace(st, (size_t)rgs * kSpCounterStride * 4, (size_t)p.S * g.M * g.N * 4, &counters, &parts);
+        e = workspace(st, (size_t)rgs * kSpCounterStride * 4, (size_t)p.S * g.N * ((g.M + 3) & ~3) * 4, &counters,
+                      &parts);
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kSpNC + kSpNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K,
