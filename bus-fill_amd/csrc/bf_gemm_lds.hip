@@ -28,10 +28,15 @@
 //   compute waves' VALU work never delays the next load.  The first step's
 //   loads are issued before the workgroup's only barrier (the flags are
 //   cleared before it).
-// * Compute waves (kNC per workgroup) load the activations A[0:M][0:K] the same
-//   way at the start (each raises a flag once its own loads are complete), then
-//   spin on the markers (ds_read + s_sleep) and take steps from a shared LDS
-//   counter (the order in which steps land).  Each step is decoded from LDS
+// * Activations: at batch 2-16 the loaders also load A[0:M][0:K], segment by
+//   segment (a segment = the G super-groups of one step for all M rows), each
+//   segment just before the first step that needs it, with one marker per
+//   loader and segment; a step waits for its segment's four markers, so the
+//   compute starts on the first segment instead of after all of A (80 KB at
+//   M = 8).  At batch 1 (10 KB) the compute waves load A themselves at the
+//   start and each raises a flag once its own loads are complete.
+// * Compute waves (kNC per workgroup) spin on the markers (ds_read + s_sleep)
+//   and take steps from a shared LDS counter (the order in which steps land).  Each step is decoded from LDS
 //   into MFMA operands in one of three forms:
 //     - fp16 weights (Q4_0 formats): RN_fp16((q - 8) d), the reference
 //       kernel's weights, 8 MFMAs per m-tile;
@@ -61,25 +66,29 @@
 namespace bf {
 namespace {
 
-// LDS layout (bytes): [0, 2048) flags: activation flag of compute wave c at 4c,
-// the compute waves' next-step counter at 60, step markers at 64 + 4e,
-// finished-step counters of sub-tile t at 1024 + 4t; [2048, 2048 + a_bytes)
-// activations, row m at m * a_rs; then the W steps of the
-// workgroup in order (2304 bytes each); then one parked partial per step; then
-// (Q4_K) the activation block sums, 32 bytes per batch row and super-group.
-constexpr int kFlagBytes = 2048;
-constexpr int kMaxSteps = (1024 - 64) / 4;
-constexpr int kZeroBytes = 128;                   // [1920, 2048): stays zero (sub-block rows form)
-constexpr int kMaxSub = (kFlagBytes - kZeroBytes - 1024) / 4;
+// LDS layout: [0, 4096) flags (ints): the compute waves' next-step counter at
+// 15; activation markers of loader j for segment s at 16 + 4s + j; block-sum
+// table flag of segment s at 400 + s; step markers at 512 + e; finished-step
+// counters of sub-tile t at 768 + t; [992, 1024) stay zero.  Then the
+// activations, segment-major: segment s (super-groups G s .. G s + G - 1) at
+// s * seg_bytes, its batch row m at m * G * 528, super-group g at g * 528;
+// then the W steps of the workgroup in order (2304 bytes each); then one
+// parked partial per step; then (Q4_K) the activation block sums, 32 bytes per
+// batch row and super-group.
+constexpr int kFlagBytes = 4096;
+constexpr int kAMark = 16, kMaxSeg = 96;
+constexpr int kTabFlag = 400;
+constexpr int kStepMark = 512, kMaxSteps = 240;
+constexpr int kSubCount = 768, kMaxSub = 224;
+constexpr int kZeroBytes = 128, kZeroOff = kFlagBytes - kZeroBytes;
 constexpr int kStepCounter = 15;                  // flags[15]: next step to take
+constexpr int kASlots = 6;                        // activation instructions per loader and segment
 
 template <int QT, int G, int MT, int NC, int NL, bool BD>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
-                int nsub, int a_rs, int a_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc,
-                int out_f16) {
+                int nsub, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc, int out_f16) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    static_assert(NC <= kStepCounter, "activation flags sit below the step counter");
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     static_assert(!BD || (QT == QT_Q4_K && G == 4), "sub-block rows: Q4_K with four K segments");
     // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
@@ -89,18 +98,19 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     const int nsg = K >> 8, nsteps = nsg / G;
     const int S = nsub * nsteps;                       // steps of the workgroup
     const int tile0 = blockIdx.x * nsub;
+    const int seg_bytes = M * G * 528, a_bytes = nsteps * seg_bytes;
     int* const flags = (int*)lds;
     uint8_t* const a_lds = lds + kFlagBytes;
     uint8_t* const w_lds = a_lds + a_bytes;
     float* const parts = (float*)(w_lds + S * kStep);
     const uint32_t lds0 = lds_addr(lds);
 
-    // Every wave clears 128 bytes of the flags, then meets the others at the
-    // one barrier of the kernel.  Loads that write no flag (weights,
-    // activations) are issued before it; every marker after it.
+    // Every wave clears 256 bytes of the flags, then meets the others at the
+    // one barrier of the kernel.  The loaders issue their first group's data
+    // loads before it and every marker after it.
     auto clear_flags_and_meet = [&]() {
-        static_assert((NC + NL) * 128 == kFlagBytes, "each wave clears 32 flags");
-        if (lane < 32) flags[32 * wave + lane] = 0;
+        static_assert((NC + NL) * 256 == kFlagBytes, "each wave clears 64 flags");
+        flags[64 * wave + lane] = 0;
         barrier_lds();
     };
 
@@ -142,155 +152,178 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
             pat[q] = step_piece_offset<QT>(nn / G, nn % G, c, K) | ((uint32_t)d << 29);
         }
         const bool clamp = (int64_t)(tile0 + nsub) * R > N;   // last workgroup: rows past N reread row N-1
+        // Activations: segment s is M*G*33 16-byte pieces (piece P: batch row
+        // P / (33 G), super-group g, part c; part 32 of each super-group is bank
+        // padding and is not loaded), IA 1 KB instructions of which loader j issues
+        // j, j + 4, ...  A piece's address advances 512 G bytes per segment.
+        const int PA = M * G * 33, IA = (PA + 63) >> 6;
+        const uint8_t* asrc[kASlots];
+        bool aon[kASlots];
+#pragma unroll
+        for (int q = 0; q < kASlots; q++) {
+            const uint32_t P = 64u * (j + 4 * q) + lane;     // P < 1600 (M * G <= 32)
+            const uint32_t m = G == 4 ? __umul24(P, 993u) >> 17 : G == 2 ? __umul24(P, 993u) >> 16
+                                                                       : __umul24(P, 1986u) >> 16;
+            const uint32_t rem = P - 33u * G * m, gg = __umul24(rem, 1986u) >> 16, c = rem - 33u * gg;
+            aon[q] = P < (uint32_t)PA && c < 32;
+            asrc[q] = (const uint8_t*)(A + (int64_t)min((int)m, M - 1) * lda + 256 * gg + 8 * min((int)c, 31));
+        }
         int te = 0, se = j;                            // step e = te * nsteps + se
         while (se >= nsteps) { se -= nsteps; te++; }
-        for (int g4 = 0, e = j; e < S; g4++, e += 4) {
-            const StepBase<QT> base = step_base<QT>((int64_t)(tile0 + te) * R, G * se, K);
+        for (int g4 = 0, e = j; 4 * g4 < S; g4++, e += 4) {
+            // the activation segments first needed by this group's steps (those of
+            // the first sub-tile: e < nsteps), then this loader's step of the group
+            const int s_hi = BD ? 0 : min(4 * g4 + 4, nsteps);   // (batch 1: the compute waves load A)
+            for (int s2 = 4 * g4; s2 < s_hi; s2++) {
+                const uint32_t dst = lds0 + (uint32_t)(kFlagBytes + s2 * seg_bytes);
 #pragma unroll
-            for (int q = 0; q < 3; q++) {
-                const int b = b_lo + q;
-                if (b > b_hi) break;
-                const int i = 9 * g4 + b;
-                const int P = 64 * i + lane;
-                const uint32_t pb = pat[q];
-                const uint8_t* src;
-                if (!clamp) {
-                    src = piece_addr<QT>(W, Waux, base, pb & 0x1FFFFFFFu);
-                } else {
-                    const int Pc = min(P, pmax);
-                    const int q9 = Pc - 144 * (Pc / 144), nn = q9 / 9, c = q9 - 9 * nn;
-                    const int64_t row = min((int64_t)(tile0 + te) * R + nn / G, (int64_t)N - 1);
-                    src = w_piece<QT>(W, Waux, row, G * se + nn % G, c, K);
+                for (int q = 0; q < kASlots; q++) {
+                    const int qa = j + 4 * q;
+                    if (qa >= IA) break;
+                    if (aon[q]) dma16(asrc[q] + (uint32_t)(512 * G * s2), dst + (uint32_t)(qa << 10));
                 }
-                if ((pb >> 29) == (uint32_t)j && P <= pmax) dma16(src, m0 + (uint32_t)(i << 10));
+            }
+            if (e < S) {
+                const StepBase<QT> base = step_base<QT>((int64_t)(tile0 + te) * R, G * se, K);
+#pragma unroll
+                for (int q = 0; q < 3; q++) {
+                    const int b = b_lo + q;
+                    if (b > b_hi) break;
+                    const int i = 9 * g4 + b;
+                    const int P = 64 * i + lane;
+                    const uint32_t pb = pat[q];
+                    const uint8_t* src;
+                    if (!clamp) {
+                        src = piece_addr<QT>(W, Waux, base, pb & 0x1FFFFFFFu);
+                    } else {
+                        const int Pc = min(P, pmax);
+                        const int q9 = Pc - 144 * (Pc / 144), nn = q9 / 9, c = q9 - 9 * nn;
+                        const int64_t row = min((int64_t)(tile0 + te) * R + nn / G, (int64_t)N - 1);
+                        src = w_piece<QT>(W, Waux, row, G * se + nn % G, c, K);
+                    }
+                    if ((pb >> 29) == (uint32_t)j && P <= pmax) dma16(src, m0 + (uint32_t)(i << 10));
+                }
             }
             if (g4 == 0) clear_flags_and_meet();
-            dma_marker(g_marker_src + lane, lds0 + 64 + 4 * e, lane);
+            for (int s2 = 4 * g4; s2 < s_hi; s2++)
+                dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kAMark + 4 * s2 + j)), lane);
+            if (e < S) dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kStepMark + e)), lane);
             se += 4;
             while (se >= nsteps) { se -= nsteps; te++; }
         }
-        if (j >= S) clear_flags_and_meet();
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         asm volatile("" :: "v"(warm));
         return;
     }
-    const int cw = wave - NL;                          // compute wave index
 
     // ---------------------------------------------------------------- compute wave
-    // Activations first: row m of A is nIr 1 KB instructions at m * a_rs (lanes
-    // past the row's 33 * nsg pieces are masked); compute wave c issues
-    // instructions c, c + NC, ..., counted from a per-workgroup offset so that
-    // the workgroups, which all read the same activations, do not all ask for the
-    // same lines at once.
-    {
-        const int nIr = (nsg * 33 + 63) >> 6, nA = M * nIr;
-        const int rot = (int)((blockIdx.x * 7u) % (unsigned)nA);
-        for (int i0 = cw; i0 < nA; i0 += NC) {
-            const int i = i0 + rot < nA ? i0 + rot : i0 + rot - nA;
-            const int m = i / nIr, jj = i - m * nIr;
-            const int P = 64 * jj + lane;
-            const int sg = min(P / 33, nsg - 1), c = min(P - 33 * (P / 33), 31);
-            if (P < nsg * 33)
-                dma16(A + (int64_t)m * lda + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + m * a_rs + 1024 * jj));
-        }
-    }
-    clear_flags_and_meet();
-    signal_own_loads(&flags[cw], lane);
-
     // Steps are taken from a shared counter in step order, which is roughly the
     // order in which they land.  Each step's G-folded partial sums go to the
     // step's own slot; the wave that finishes the last step of a sub-tile adds
     // the sub-tile's slots in step order (a fixed order: results do not depend
     // on timing) and stores them.
-    wait_flags(flags, NC, lane);
 
     // Q4_K runs in the factored form sum_k a_k w_k = d * sum_k a_k (sc q_k)
     // - dmin * sum_j m_j S_j over the sub-blocks j of a super-block, where
-    // S_j = sum_{k in j} a_k.  The block sums are tabulated once: entry
-    // (m, sg, kg) covers sub-blocks 2kg, 2kg+1 of super-group sg of batch row m:
+    // S_j = sum_{k in j} a_k.  The block sums are tabulated per segment by the
+    // wave that takes the segment's first step (the others wait for its flag;
+    // at batch 1 all waves tabulate everything before the first step): entry
+    // (m, sg, kg) covers sub-blocks 2kg, 2kg+1 of super-group sg of batch
+    // row m:
     //   MFMA form: fp16 {hi_0, hi_1, lo_0, lo_1} with S / 32 = hi + lo / 2048 (hi
     //     is S / 32 rounded to fp16, lo the rounded remainder: S to about 2^-22);
     //   sub-block rows form (BD): fp32 {S_0, S_1}, and the entry's 128 bytes of
     //     activations are reordered in place, each run of eight to
     //     a0 a2 a1 a3 a4 a6 a5 a7, the order in which that form decodes codes.
-    const uint8_t* const tab = (const uint8_t*)(parts + S * SLOT);
     if constexpr (BD) {
+        // batch 1: the compute waves load A (row 0: 33 nsg pieces, contiguous in
+        // LDS) before the barrier, c, c + NC, ... of its 1 KB instructions from a
+        // per-workgroup offset (the workgroups all read the same lines), and
+        // raise a flag once their own loads are complete
+        const int cw = wave - NL, nA = (nsg * 33 + 63) >> 6;
+        const int rot = (int)((blockIdx.x * 7u) % (unsigned)nA);
+        for (int i0 = cw; i0 < nA; i0 += NC) {
+            const int i = i0 + rot < nA ? i0 + rot : i0 + rot - nA;
+            const int P = 64 * i + lane;
+            const int sg = min(P / 33, nsg - 1), c = min(P - 33 * (P / 33), 31);
+            if (P < nsg * 33) dma16(A + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + 1024 * i));
+        }
+        clear_flags_and_meet();
+        signal_own_loads(&flags[cw], lane);
+        wait_flags(flags, NC, lane);
+    } else {
+        clear_flags_and_meet();
+    }
+    uint8_t* const tab = (uint8_t*)(parts + S * SLOT);
+    // entries u0, u0 + ustep, ... < u_end of the list ordered (segment, row m,
+    // super-group gg of the segment, k-group kq); a segment has M * G * 4
+    auto build_table = [&](int u0, int u_end, int ustep) {
         const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-        for (int u = cw * 64 + lane; u < M * nsg * 4; u += NC * 64) {
-            const int kq = u & 3, rest = u >> 2;
-            const int m = rest / nsg, sg = rest - m * nsg;
-            uint8_t* src = a_lds + m * a_rs + sg * kASg + 128 * kq;
+        for (int u = u0; u < u_end; u += ustep) {
+            const int kq = u & 3, rest = u >> 2, s_seg = rest / (M * G), mg4 = rest - s_seg * (M * G);
+            const int m = mg4 / G, gg = mg4 - m * G;
+            uint8_t* src = a_lds + s_seg * seg_bytes + (m * G + gg) * 528 + 128 * kq;
             float sum[2];
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 float acc = 0.f;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    u4 v = *(const u4*)(src + 64 * h + 16 * q);
+                    const u4 v = *(const u4*)(src + 64 * h + 16 * q);
                     acc = __builtin_amdgcn_fdot2(as_h2(v.x), one, acc, false);
                     acc = __builtin_amdgcn_fdot2(as_h2(v.y), one, acc, false);
                     acc = __builtin_amdgcn_fdot2(as_h2(v.z), one, acc, false);
                     acc = __builtin_amdgcn_fdot2(as_h2(v.w), one, acc, false);
-                    const u4 o = {perm_b32(v.y, v.x, 0x05040100u), perm_b32(v.y, v.x, 0x07060302u),
-                                  perm_b32(v.w, v.z, 0x05040100u), perm_b32(v.w, v.z, 0x07060302u)};
-                    *(u4*)(src + 64 * h + 16 * q) = o;
+                    if constexpr (BD) {
+                        const u4 o = {perm_b32(v.y, v.x, 0x05040100u), perm_b32(v.y, v.x, 0x07060302u),
+                                      perm_b32(v.w, v.z, 0x05040100u), perm_b32(v.w, v.z, 0x07060302u)};
+                        *(u4*)(src + 64 * h + 16 * q) = o;
+                    }
                 }
                 sum[h] = acc;
             }
-            float* dst = (float*)(tab + 8 * u);
-            dst[0] = sum[0];
-            dst[1] = sum[1];
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[cw])), "v"(2) : "memory");
-        wait_flags(flags, NC, lane, 2);
-    } else if constexpr (QT == QT_Q4_K) {
-        const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-        for (int u = cw * 64 + lane; u < M * nsg * 4; u += NC * 64) {
-            const int kq = u & 3, rest = u >> 2;
-            const int m = rest / nsg, sg = rest - m * nsg;
-            const uint8_t* src = a_lds + m * a_rs + sg * kASg + 128 * kq;
-            uint32_t hi[2], lo[2];
+            uint32_t* dst = (uint32_t*)(tab + ((m * nsg + G * s_seg + gg) * 4 + kq) * 8);
+            if constexpr (BD) {
+                dst[0] = __builtin_bit_cast(uint32_t, sum[0]);
+                dst[1] = __builtin_bit_cast(uint32_t, sum[1]);
+            } else {
+                uint32_t hi[2], lo[2];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                float sum = 0.f;
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const u4 v = *(const u4*)(src + 64 * h + 16 * q);
-                    sum = __builtin_amdgcn_fdot2(as_h2(v.x), one, sum, false);
-                    sum = __builtin_amdgcn_fdot2(as_h2(v.y), one, sum, false);
-                    sum = __builtin_amdgcn_fdot2(as_h2(v.z), one, sum, false);
-                    sum = __builtin_amdgcn_fdot2(as_h2(v.w), one, sum, false);
+                for (int h = 0; h < 2; h++) {
+                    const float mean = sum[h] * 0.03125f;
+                    const _Float16 mh = (_Float16)mean;
+                    const _Float16 ml = (_Float16)((mean - (float)mh) * 2048.0f);
+                    hi[h] = __builtin_bit_cast(uint16_t, mh);
+                    lo[h] = __builtin_bit_cast(uint16_t, ml);
                 }
-                const float mean = sum * 0.03125f;
-                const _Float16 mh = (_Float16)mean;
-                const _Float16 ml = (_Float16)((mean - (float)mh) * 2048.0f);
-                hi[h] = __builtin_bit_cast(uint16_t, mh);
-                lo[h] = __builtin_bit_cast(uint16_t, ml);
+                dst[0] = hi[0] | (hi[1] << 16);
+                dst[1] = lo[0] | (lo[1] << 16);
             }
-            uint32_t* dst = (uint32_t*)(tab + 8 * u);
-            dst[0] = hi[0] | (hi[1] << 16);
-            dst[1] = lo[0] | (lo[1] << 16);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[cw])), "v"(2) : "memory");
+    };
+
+    if constexpr (BD) {
+        // batch 1: all of A (10 KB at K = 5120) at once, tabulated before the first step
+        build_table((wave - NL) * 64 + lane, nsteps * M * G * 4, NC * 64);
+        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[wave - NL])), "v"(2) : "memory");
         wait_flags(flags, NC, lane, 2);
     }
 
     const Magic mg = make_magic();
     const int r = lane & 15, kg = lane >> 4;
     const int g = r % G, rowl = r / G;
-    const uint8_t* arow[MT];
+    int arow[MT];                                      // this lane's A fragment within a segment
     const uint8_t* trow[MT];                           // this lane's block-sum entries (Q4_K)
     // sub-block rows form: MFMA row r = 4 kappa + g takes the activations of
     // segment g from the k slots of lane group kappa only (zeros elsewhere), so
     // that row holds the partial sums of one sub-block per column
     const bool bd_on = (r >> 2) == kg;
-    const uint8_t* const zero16 = lds + kFlagBytes - kZeroBytes;
+    const uint8_t* const zero16 = lds + kZeroOff;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const int m = BD ? min(mt, M - 1) : min(mt * R + r / G, M - 1);   // padding rows reread row M-1
-        arow[mt] = (!BD || bd_on) ? a_lds + m * a_rs + g * kASg + 128 * kg : zero16;
+        arow[mt] = (m * G + g) * 528 + 128 * kg;
         trow[mt] = tab + ((m * nsg + g) * 4 + kg) * 8;
     }
 
@@ -303,10 +336,22 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         e = __builtin_amdgcn_readfirstlane(e);
         if (e >= S) break;
         const int t_in = e / nsteps, s_in = e - t_in * nsteps;
-        wait_flag(&flags[16 + e]);
+        if constexpr (!BD) {
+            wait_flags(flags + kAMark + 4 * s_in, NL, lane);   // the step's activation segment
+            if constexpr (QT == QT_Q4_K) {
+                if (t_in == 0) {
+                    build_table(s_in * M * G * 4 + lane, (s_in + 1) * M * G * 4, 64);
+                    if (lane == 0)
+                        asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kTabFlag + s_in])), "v"(1) : "memory");
+                } else {
+                    wait_flag(&flags[kTabFlag + s_in]);
+                }
+            }
+        }
+        wait_flag(&flags[kStepMark + e]);
         Raw<QT> raw;
         lds_raw<QT>(raw, w_lds + e * kStep + r * 144, kg);
-        const int aoff = G * s_in * kASg;
+        const uint8_t* const aseg = a_lds + s_in * seg_bytes;
         f4 acc[MT], accm[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[mt] = accm[mt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -318,15 +363,17 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
             f4 alo[MT], ahi[MT];
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) alo[mt] = ahi[mt] = f4{0.f, 0.f, 0.f, 0.f};
-            const int astep = bd_on ? aoff : 0;
+            const uint8_t* abase[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) abase[mt] = bd_on ? aseg + arow[mt] : zero16;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 h8 blo, bhi;
                 codes_subnormal(raw, t, blo, bhi);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
-                    alo[mt] = mfma16x16x32(*(const h8*)(arow[mt] + astep + 16 * t), blo, alo[mt]);
-                    ahi[mt] = mfma16x16x32(*(const h8*)(arow[mt] + astep + 16 * (t + 4)), bhi, ahi[mt]);
+                    alo[mt] = mfma16x16x32(*(const h8*)(abase[mt] + 16 * t), blo, alo[mt]);
+                    ahi[mt] = mfma16x16x32(*(const h8*)(abase[mt] + 16 * (t + 4)), bhi, ahi[mt]);
                 }
             }
             float* slot = parts + e * SLOT;
@@ -357,7 +404,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
                 const h8 b = weights_int(mg, raw, sk, i);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++)
-                    acc[mt] = mfma16x16x32(*(const h8*)(arow[mt] + aoff + 16 * i), b, acc[mt]);
+                    acc[mt] = mfma16x16x32(*(const h8*)(aseg + arow[mt] + 16 * i), b, acc[mt]);
             }
             // sum_j m_j S_j: the mins {32m, m/64} of sub-blocks 2kg, 2kg+1 meet the
             // block sums {hi, lo} of the same sub-blocks (k slots 8kg .. 8kg+3)
@@ -377,7 +424,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
                 const h8 b = weights(mg, raw, sc, i);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++)
-                    acc[mt] = mfma16x16x32(*(const h8*)(arow[mt] + aoff + 16 * i), b, acc[mt]);
+                    acc[mt] = mfma16x16x32(*(const h8*)(aseg + arow[mt] + 16 * i), b, acc[mt]);
             }
         }
         if constexpr (!BD) {
@@ -410,7 +457,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         int old = 0;
         if (lane == 0)
             asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
-                         : "=v"(old) : "v"(lds_addr(&flags[256 + t_in])), "v"(1) : "memory");
+                         : "=v"(old) : "v"(lds_addr(&flags[kSubCount + t_in])), "v"(1) : "memory");
         if (__builtin_amdgcn_readfirstlane(old) == nsteps - 1) {
             const int64_t row0 = (int64_t)(tile0 + t_in) * R;
             for (int v = lane; v < SLOT; v += 64) {
@@ -428,17 +475,10 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     }
 }
 
-// LDS row stride for activations: whole kilobytes for the 528-byte super-group
-// images of one row, plus 16*G bytes, so that the rows m' of one k-group sit on
-// distinct bank groups (stride = 16*G mod 256 bytes).
-inline int a_row_stride(int nsg, int G) {
-    return (nsg * kASg + 1023) / 1024 * 1024 + 16 * G;
-}
-
 constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 struct LdsPlan {
-    int G, MT, nsub, grid, a_rs, a_bytes, lds;
+    int G, MT, nsub, grid, lds;
     bool BD;                           // sub-block rows form (Q4_K, one batch row per m-tile)
 };
 
@@ -453,16 +493,18 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false) {
     const int T = (g.N + R - 1) / R;
     p.G = G;
     p.MT = MT;
-    p.a_rs = a_row_stride(nsg, G);
-    if ((int64_t)g.M * p.a_rs > kMaxLds) return false;
-    p.a_bytes = (int)(((int64_t)g.M * p.a_rs + 15) / 16 * 16);
+    // activation segments of G super-groups x M rows (528-byte super-group images:
+    // the 16 lanes of a k-group read 16 distinct bank groups for G = 1, 2, 4)
+    if (nsteps > kMaxSeg || g.M * G > 32) return false;
+    const int64_t a_bytes = (int64_t)nsteps * g.M * G * 528;
+    if (a_bytes > kMaxLds) return false;
     for (int rounds = 1; rounds <= 64; rounds++) {
         const int nsub = (T + 256 * rounds - 1) / (256 * rounds);
         const int S = nsub * nsteps;
         if (S > kMaxSteps || nsub > kMaxSub) continue;
         const int64_t tab = g.qtype == QT_Q4_K ? (int64_t)g.M * nsg * 32 : 0;   // block sums
         const int64_t slot = BD ? MT * R : MT * R * R;
-        const int64_t lds = kFlagBytes + (int64_t)p.a_bytes + (int64_t)S * kStep + (int64_t)S * slot * 4 + tab;
+        const int64_t lds = kFlagBytes + a_bytes + (int64_t)S * kStep + (int64_t)S * slot * 4 + tab;
         if (lds > kMaxLds) {
             if (nsub == 1) return false;
             continue;
@@ -489,7 +531,7 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
         attr_set.fetch_or(bit, std::memory_order_acq_rel);
     }
     hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kNC + kNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K, p.nsub,
-                       p.a_rs, p.a_bytes, g.Waux, g.C, g.ldc, g.out_f16);
+                       g.Waux, g.C, g.ldc, g.out_f16);
     return hipGetLastError();
 }
 
