@@ -36,8 +36,10 @@
 //   M = 8).  At batch 1 (10 KB) the compute waves load A themselves at the
 //   start and each raises a flag once its own loads are complete.
 // * Compute waves (kNC per workgroup) spin on the markers (ds_read + s_sleep)
-//   and take steps from a shared LDS counter (the order in which steps land).  Each step is decoded from LDS
-//   into MFMA operands in one of three forms:
+//   and take steps in the order in which they land: from a shared LDS counter,
+//   or at batch 1 wave c takes steps c, c + kNC, ... and reads a step's marker
+//   and data in one round trip.  Each step is decoded from LDS into MFMA
+//   operands in one of three forms:
 //     - fp16 weights (Q4_0 formats): RN_fp16((q - 8) d), the reference
 //       kernel's weights, 8 MFMAs per m-tile;
 //     - factored Q4_K: d * sum a (sc q) - dmin * sum_j m_j S_j with the exact
@@ -50,7 +52,10 @@
 //   The folded partial sums of each step are parked in LDS; a per-sub-tile
 //   counter (ds_add_rtn) tells the wave that finishes a sub-tile's last step
 //   to add the sub-tile's partials in step order (a fixed order: results are
-//   deterministic) and store them.
+//   deterministic) and store them.  At batch 1 each lane parks its own
+//   unreduced value (the cross-lane sums run once per sub-tile instead of
+//   once per step), the count is a plain ds_add, and the wave that took the
+//   sub-tile's last step waits for the count once its own steps are done.
 //
 // Weight layout in LDS: the workgroup's steps in order, 2304 bytes each; inside
 // a step, the 144-byte super-group image of column n = 0..15 at n*144 (Q4_K and
@@ -69,7 +74,7 @@ namespace {
 // LDS layout: [0, 4096) flags (ints): the compute waves' next-step counter at
 // 15; activation markers of loader j for segment s at 16 + 4s + j; block-sum
 // table flag of segment s at 400 + s; step markers at 512 + e; finished-step
-// counters of sub-tile t at 768 + t; [992, 1024) stay zero.  Then the
+// counters of sub-tile t at 768 + t.  Then the
 // activations, segment-major: segment s (super-groups G s .. G s + G - 1) at
 // s * seg_bytes, its batch row m at m * G * 528, super-group g at g * 528;
 // then the W steps of the workgroup in order (2304 bytes each); then one
@@ -80,7 +85,6 @@ constexpr int kAMark = 16, kMaxSeg = 96;
 constexpr int kTabFlag = 400;
 constexpr int kStepMark = 512, kMaxSteps = 240;
 constexpr int kSubCount = 768, kMaxSub = 224;
-constexpr int kZeroBytes = 128, kZeroOff = kFlagBytes - kZeroBytes;
 constexpr int kStepCounter = 15;                  // flags[15]: next step to take
 constexpr int kASlots = 6;                        // activation instructions per loader and segment
 
@@ -92,7 +96,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     static_assert(!BD || (QT == QT_Q4_K && G == 4), "sub-block rows: Q4_K with four K segments");
     // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
-    constexpr int SLOT = BD ? MT * R : MT * R * R;
+    constexpr int SLOT = BD ? MT * 64 : MT * R * R;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsg = K >> 8, nsteps = nsg / G;
@@ -217,11 +221,10 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     }
 
     // ---------------------------------------------------------------- compute wave
-    // Steps are taken from a shared counter in step order, which is roughly the
-    // order in which they land.  Each step's G-folded partial sums go to the
-    // step's own slot; the wave that finishes the last step of a sub-tile adds
-    // the sub-tile's slots in step order (a fixed order: results do not depend
-    // on timing) and stores them.
+    // Steps are taken in step order, which is roughly the order in which they
+    // land.  Each step's partial sums go to the step's own slot; the slots of a
+    // sub-tile are added in step order (a fixed order: results do not depend on
+    // timing) and stored.
 
     // Q4_K runs in the factored form sum_k a_k w_k = d * sum_k a_k (sc q_k)
     // - dmin * sum_j m_j S_j over the sub-blocks j of a super-block, where
@@ -319,7 +322,15 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     // segment g from the k slots of lane group kappa only (zeros elsewhere), so
     // that row holds the partial sums of one sub-block per column
     const bool bd_on = (r >> 2) == kg;
-    const uint8_t* const zero16 = lds + kZeroOff;
+    // sub-block rows form: the activation operands stay zero in the lanes off
+    // the block diagonal; only the 16 lanes on it read them (exec-masked)
+    h8 abd[MT][8];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) abd[mt][t] = h8{};
+    // t_in = e / nsteps as (e * inv) >> 16: exact for e < 240, nsteps <= 96
+    const uint32_t inv_nsteps = (65536u + (uint32_t)nsteps - 1u) / (uint32_t)nsteps;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const int m = BD ? min(mt, M - 1) : min(mt * R + r / G, M - 1);   // padding rows reread row M-1
@@ -327,15 +338,23 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         trow[mt] = tab + ((m * nsg + g) * 4 + kg) * 8;
     }
 
+    // Steps in the order in which they land: batch 1 (sub-block rows form):
+    // compute wave c takes steps c, c + NC, ...; otherwise a free wave takes the
+    // next step from the shared counter.
+    int e_static = wave - NL;
     for (;;) {
-        // take the next step (steps land roughly in order; a free wave takes the next one)
         int e = 0;
-        if (lane == 0)
-            asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
-                         : "=v"(e) : "v"(lds_addr(&flags[kStepCounter])), "v"(1) : "memory");
-        e = __builtin_amdgcn_readfirstlane(e);
+        if constexpr (BD) {
+            e = e_static;
+            e_static += NC;
+        } else {
+            if (lane == 0)
+                asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+                             : "=v"(e) : "v"(lds_addr(&flags[kStepCounter])), "v"(1) : "memory");
+            e = __builtin_amdgcn_readfirstlane(e);
+        }
         if (e >= S) break;
-        const int t_in = e / nsteps, s_in = e - t_in * nsteps;
+        const int t_in = (int)(((uint32_t)e * inv_nsteps) >> 16), s_in = e - t_in * nsteps;
         if constexpr (!BD) {
             wait_flags(flags + kAMark + 4 * s_in, NL, lane);   // the step's activation segment
             if constexpr (QT == QT_Q4_K) {
@@ -348,10 +367,30 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
                 }
             }
         }
-        wait_flag(&flags[kStepMark + e]);
         Raw<QT> raw;
-        lds_raw<QT>(raw, w_lds + e * kStep + r * 144, kg);
         const uint8_t* const aseg = a_lds + s_in * seg_bytes;
+        if constexpr (BD) {
+            // the step's marker with the step's weight and activation reads right
+            // behind it: a wave's LDS reads complete in order, so a nonzero marker
+            // means the reads behind it saw the landed step (one round trip)
+            for (int it = 0;; it++) {
+                int mark;
+                asm volatile("ds_read_b32 %0, %1" : "=v"(mark) : "v"(lds_addr(&flags[kStepMark + e])) : "memory");
+                lds_raw<QT>(raw, w_lds + e * kStep + r * 144, kg);
+                if (bd_on) {
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                        for (int t = 0; t < 8; t++) abd[mt][t] = *(const h8*)(aseg + arow[mt] + 16 * t);
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(mark) :: "memory");
+                if (__builtin_amdgcn_readfirstlane(mark) != 0 || it >= (1 << 20)) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        } else {
+            wait_flag(&flags[kStepMark + e]);
+            lds_raw<QT>(raw, w_lds + e * kStep + r * 144, kg);
+        }
         f4 acc[MT], accm[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[mt] = accm[mt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -363,17 +402,14 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
             f4 alo[MT], ahi[MT];
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) alo[mt] = ahi[mt] = f4{0.f, 0.f, 0.f, 0.f};
-            const uint8_t* abase[MT];
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) abase[mt] = bd_on ? aseg + arow[mt] : zero16;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 h8 blo, bhi;
                 codes_subnormal(raw, t, blo, bhi);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
-                    alo[mt] = mfma16x16x32(*(const h8*)(abase[mt] + 16 * t), blo, alo[mt]);
-                    ahi[mt] = mfma16x16x32(*(const h8*)(abase[mt] + 16 * (t + 4)), bhi, ahi[mt]);
+                    alo[mt] = mfma16x16x32(abd[mt][t], blo, alo[mt]);
+                    ahi[mt] = mfma16x16x32(abd[mt][t + 4], bhi, ahi[mt]);
                 }
             }
             float* slot = parts + e * SLOT;
@@ -390,12 +426,9 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
                 const float* ts = (const float*)(trow[mt] + G * s_in * 32);
                 float y = sb.d20 * __builtin_fmaf(sb.c_lo16, plo, sb.c_hi * phi) -
                           sb.dmin * __builtin_fmaf(sb.m_lo, ts[0], sb.m_hi * ts[1]);
-                // sum the four lane groups (sub-block pairs), then the four segments
-                y = sum_lane_xor16(y);
-                y = sum_lane_xor32(y);
-                y += dpp_xor(y, 1);
-                y += dpp_xor(y, 2);
-                if (g == 0 && kg == 0) slot[mt * R + rowl] = y;
+                // parked per lane: the lane groups and segments are summed once per
+                // sub-tile, after its steps
+                slot[mt * 64 + lane] = y;
             }
         } else if constexpr (QT == QT_Q4_K) {
             const SclK sk = scales_int(raw, kg);
@@ -453,6 +486,13 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
                 }
             }
         }
+        if constexpr (BD) {
+            // count the finished step (no return value: the wave that took the
+            // sub-tile's last step waits for the count after its own steps)
+            if (lane == 0)
+                asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[kSubCount + t_in])), "v"(1) : "memory");
+            continue;
+        }
         // count the finished step; the last of the sub-tile reduces and stores it
         int old = 0;
         if (lane == 0)
@@ -469,6 +509,30 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
                 if (m < M && row < N) {
                     if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + row] = (_Float16)sum;
                     else ((float*)C)[(int64_t)m * ldc + row] = sum;
+                }
+            }
+        }
+    }
+    if constexpr (BD) {
+        // the sub-tiles whose last step this wave took: once all their steps are
+        // parked, each lane adds its parked values in step order, then the lane
+        // groups (sub-block pairs) and the four segments are summed
+        for (int t_in = 0; t_in < nsub; t_in++) {
+            if ((t_in * nsteps + nsteps - 1) % NC != wave - NL) continue;
+            wait_count(&flags[kSubCount + t_in], nsteps);
+            const int64_t row = (int64_t)(tile0 + t_in) * R + rowl;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const float* pp = parts + t_in * nsteps * SLOT + mt * 64 + lane;
+                float y = 0.f;
+                for (int s2 = 0; s2 < nsteps; s2++) y += pp[s2 * SLOT];
+                y = sum_lane_xor16(y);
+                y = sum_lane_xor32(y);
+                y += dpp_xor(y, 1);
+                y += dpp_xor(y, 2);
+                if (g == 0 && kg == 0 && mt < M && row < N) {
+                    if (out_f16) ((_Float16*)C)[(int64_t)mt * ldc + row] = (_Float16)y;
+                    else ((float*)C)[(int64_t)mt * ldc + row] = y;
                 }
             }
         }
@@ -503,7 +567,7 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false) {
         const int S = nsub * nsteps;
         if (S > kMaxSteps || nsub > kMaxSub) continue;
         const int64_t tab = g.qtype == QT_Q4_K ? (int64_t)g.M * nsg * 32 : 0;   // block sums
-        const int64_t slot = BD ? MT * R : MT * R * R;
+        const int64_t slot = BD ? MT * 64 : MT * R * R;
         const int64_t lds = kFlagBytes + a_bytes + (int64_t)S * kStep + (int64_t)S * slot * 4 + tab;
         if (lds > kMaxLds) {
             if (nsub == 1) return false;

@@ -91,6 +91,17 @@ __device__ __forceinline__ void wait_flag(const int* flag) {
     }
 }
 
+// Spin until the LDS word at `flag` is at least n.
+__device__ __forceinline__ void wait_count(const int* flag, int n) {
+    const uint32_t a = lds_addr(flag);
+    for (int it = 0; it < (1 << 20); it++) {
+        int v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+        if (__builtin_amdgcn_readfirstlane(v) >= n) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // Spin until the n <= 64 consecutive LDS words from `flags` are all >= v0:
 // lane l polls word l, so one LDS read per round covers all of them.
 __device__ __forceinline__ void wait_flags(const int* flags, int n, int lane, int v0 = 1) {
