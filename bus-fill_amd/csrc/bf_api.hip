@@ -30,6 +30,7 @@ bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0;
 
 constexpr int kMaxMPerLaunch = 128;   // MFMA kernels cover up to 8 batch tiles of 16
 constexpr int kDot2MaxM = 4;          // crossover dot2 -> MFMA (see the batch sweep)
+constexpr int kSplitMaxM = 32;        // batch rows of one K-split launch
 
 bf_status check_weights(bf_qtype qt, const void* W, const void* W_aux, int N, int K) {
     if (qt != BF_Q4_0 && qt != BF_Q4_0_PLANES && qt != BF_Q4_K)
@@ -72,7 +73,26 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
 
     const size_t csize = otype == BF_OUT_F32 ? 4 : 2;
     hipStream_t hs = (hipStream_t)stream;
-    for (int m0 = 0; m0 < M; m0 += kMaxMPerLaunch) {
+    // Batches above 32 rows: the K-split kernel over slices of 32 rows (the
+    // weights are streamed once per slice) beats the register-streaming MFMA
+    // kernel, whose activation traffic grows with every 16-row tile.
+    int slice = kMaxMPerLaunch;
+    if (algo == BF_ALGO_AUTO && M > kSplitMaxM) {
+        bf::GemmArgs probe;
+        probe.qtype = (int)qtype;
+        probe.W = (const uint8_t*)W;
+        probe.Waux = (const uint8_t*)W_aux;
+        probe.A = A;
+        probe.lda = lda;
+        probe.C = C;
+        probe.ldc = ldc;
+        probe.out_f16 = otype == BF_OUT_F16;
+        probe.M = kSplitMaxM;
+        probe.N = N;
+        probe.K = K;
+        if (fast_eligible(probe) && bf::split_supports(probe)) slice = kSplitMaxM;
+    }
+    for (int m0 = 0; m0 < M; m0 += slice) {
         bf::GemmArgs g;
         g.qtype = (int)qtype;
         g.W = (const uint8_t*)W;
@@ -82,7 +102,7 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
         g.C = (char*)C + (size_t)m0 * ldc * csize;
         g.ldc = ldc;
         g.out_f16 = otype == BF_OUT_F16;
-        g.M = M - m0 < kMaxMPerLaunch ? M - m0 : kMaxMPerLaunch;
+        g.M = M - m0 < slice ? M - m0 : slice;
         g.N = N;
         g.K = K;
 
