@@ -156,12 +156,50 @@ __device__ __forceinline__ BdScl scales_bd(const Raw<QT_Q4_K>& raw, int kg) {
     return o;
 }
 
-// Codes of bytes 8t .. 8t+7 of the lane's 32-byte run as MFMA operands, in the
+// The lane's 32 code bytes for the sub-block rows form, as eight words: Q4_K
+// the run of sub-blocks 2kg (low nibbles) and 2kg+1 (high nibbles); Q4_0 and
+// planes the code bytes of blocks 2kg (words 0-3) and 2kg+1 (words 4-7).
+__device__ __forceinline__ void bd_code_words(const Raw<QT_Q4_K>& raw, uint32_t w[8]) {
+    const uint32_t v[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = v[i];
+}
+
+__device__ __forceinline__ void bd_code_words(const Raw<QT_PLANES>& raw, uint32_t w[8]) {
+    const uint32_t v[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = v[i];
+}
+
+__device__ __forceinline__ void bd_code_words(const Raw<QT_Q4_0>& raw, uint32_t w[8]) {
+    // block 2kg: d at bytes 0-1, codes at 2..17 (realigned by two bytes);
+    // block 2kg+1: d at 18-19, codes at 20..35 (words 5..8, aligned)
+    w[0] = __builtin_amdgcn_alignbit(raw.a.y, raw.a.x, 16);
+    w[1] = __builtin_amdgcn_alignbit(raw.a.z, raw.a.y, 16);
+    w[2] = __builtin_amdgcn_alignbit(raw.a.w, raw.a.z, 16);
+    w[3] = __builtin_amdgcn_alignbit(raw.b.x, raw.a.w, 16);
+    w[4] = raw.b.y;
+    w[5] = raw.b.z;
+    w[6] = raw.b.w;
+    w[7] = raw.c;
+}
+
+// fp32 scales d of the lane's two blocks (Q4_0 formats), times 2^20.
+__device__ __forceinline__ void bd_block_scales(const Raw<QT_Q4_0>& raw, float& da20, float& db20) {
+    da20 = half_bits_to_float(raw.a.x & 0xFFFFu) * 1048576.0f;
+    db20 = half_bits_to_float(raw.b.x >> 16) * 1048576.0f;
+}
+
+__device__ __forceinline__ void bd_block_scales(const Raw<QT_PLANES>& raw, float& da20, float& db20) {
+    da20 = half_bits_to_float(raw.sc & 0xFFFFu) * 1048576.0f;
+    db20 = half_bits_to_float(raw.sc >> 16) * 1048576.0f;
+}
+
+// Codes of bytes 8t .. 8t+7 of the lane's code words as MFMA operands, in the
 // order b0 b2 b1 b3 b4 b6 b5 b7: `lo` the low nibbles as the fp16 bit patterns
 // q (value q * 2^-24), `hi` the high nibbles masked in place (16 q * 2^-24).
 // One v_alignbit_b32 and four v_and_b32 per word.
-__device__ __forceinline__ void codes_subnormal(const Raw<QT_Q4_K>& raw, int t, h8& lo, h8& hi) {
-    const uint32_t w[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
+__device__ __forceinline__ void codes_subnormal(const uint32_t w[8], int t, h8& lo, h8& hi) {
     const uint32_t x0 = w[2 * t], x1 = w[2 * t + 1];
     const uint32_t r0 = __builtin_amdgcn_alignbit(x0, x0, 8), r1 = __builtin_amdgcn_alignbit(x1, x1, 8);
     lo = __builtin_bit_cast(h8, u4{x0 & 0x000F000Fu, r0 & 0x000F000Fu, x1 & 0x000F000Fu, r1 & 0x000F000Fu});

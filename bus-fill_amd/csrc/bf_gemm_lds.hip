@@ -94,7 +94,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
                 int nsub, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc, int out_f16) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
-    static_assert(!BD || (QT == QT_Q4_K && G == 4), "sub-block rows: Q4_K with four K segments");
+    static_assert(!BD || G == 4, "sub-block rows: four K segments");
     // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
     constexpr int SLOT = BD ? MT * 64 : MT * R * R;
     const int lane = threadIdx.x & 63;
@@ -266,24 +266,47 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
             const int kq = u & 3, rest = u >> 2, s_seg = rest / (M * G), mg4 = rest - s_seg * (M * G);
             const int m = mg4 / G, gg = mg4 - m * G;
             uint8_t* src = a_lds + s_seg * seg_bytes + (m * G + gg) * 528 + 128 * kq;
+            u4 v[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) v[q] = *(const u4*)(src + 16 * q);
             float sum[2];
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 float acc = 0.f;
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const u4 v = *(const u4*)(src + 64 * h + 16 * q);
-                    acc = __builtin_amdgcn_fdot2(as_h2(v.x), one, acc, false);
-                    acc = __builtin_amdgcn_fdot2(as_h2(v.y), one, acc, false);
-                    acc = __builtin_amdgcn_fdot2(as_h2(v.z), one, acc, false);
-                    acc = __builtin_amdgcn_fdot2(as_h2(v.w), one, acc, false);
-                    if constexpr (BD) {
-                        const u4 o = {perm_b32(v.y, v.x, 0x05040100u), perm_b32(v.y, v.x, 0x07060302u),
-                                      perm_b32(v.w, v.z, 0x05040100u), perm_b32(v.w, v.z, 0x07060302u)};
-                        *(u4*)(src + 64 * h + 16 * q) = o;
-                    }
+                for (int q = 4 * h; q < 4 * h + 4; q++) {
+                    acc = __builtin_amdgcn_fdot2(as_h2(v[q].x), one, acc, false);
+                    acc = __builtin_amdgcn_fdot2(as_h2(v[q].y), one, acc, false);
+                    acc = __builtin_amdgcn_fdot2(as_h2(v[q].z), one, acc, false);
+                    acc = __builtin_amdgcn_fdot2(as_h2(v[q].w), one, acc, false);
                 }
                 sum[h] = acc;
+            }
+            if constexpr (BD) {
+                // 16-byte slot j of the entry = the operand of codes word pair t = j % 4
+                // (low nibbles for j < 4, high for j >= 4), in the decode order
+                // 0 2 1 3 4 6 5 7 of its eight code positions
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    u4 o;
+                    if constexpr (QT == QT_PLANES) {
+                        // code byte b of the run holds weights 2b (low) and 2b+1 (high)
+                        const int t = j & 3;
+                        const uint32_t sel = j < 4 ? 0x05040100u : 0x07060302u;
+                        const u4 x = v[2 * t], y = v[2 * t + 1];
+                        o = u4{perm_b32(x.z, x.x, sel), perm_b32(x.w, x.y, sel), perm_b32(y.z, y.x, sel),
+                               perm_b32(y.w, y.y, sel)};
+                    } else {
+                        // Q4_K: runs in order (sub-block 2kg low, 2kg+1 high nibbles);
+                        // Q4_0: block 2kg's code bytes hold weights b and 16+b, block
+                        // 2kg+1's 32+b and 48+b: runs 0 1 4 5 | 2 3 6 7
+                        constexpr int kRun0[8] = {0, 1, 4, 5, 2, 3, 6, 7};
+                        const u4 x = v[QT == QT_Q4_K ? j : kRun0[j]];
+                        o = u4{perm_b32(x.y, x.x, 0x05040100u), perm_b32(x.y, x.x, 0x07060302u),
+                               perm_b32(x.w, x.z, 0x05040100u), perm_b32(x.w, x.z, 0x07060302u)};
+                    }
+                    *(u4*)(src + 16 * j) = o;
+                }
             }
             uint32_t* dst = (uint32_t*)(tab + ((m * nsg + G * s_seg + gg) * 4 + kq) * 8);
             if constexpr (BD) {
@@ -397,35 +420,56 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         float d = 1.f, dmin = 0.f;
         if constexpr (BD) {
             // codes as fp16 subnormals: low nibble q -> q * 2^-24, high nibble
-            // (masked in place) -> 16 q * 2^-24; exact products in the MFMA
-            const BdScl sb = scales_bd(raw, kg);
-            f4 alo[MT], ahi[MT];
+            // (masked in place) -> 16 q * 2^-24; exact products in the MFMA.
+            // Accumulators: Q4_K {sub-block 2kg, sub-block 2kg+1} over t = 0..3;
+            // Q4_0 formats {block 2kg low, high nibbles} over t = 0, 1 and
+            // {block 2kg+1 low, high} over t = 2, 3 (each block has one scale)
+            constexpr bool K4 = QT == QT_Q4_K;
+            constexpr int NA = K4 ? 2 : 4;
+            uint32_t wq[8];
+            bd_code_words(raw, wq);
+            f4 ab[MT][NA];
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) alo[mt] = ahi[mt] = f4{0.f, 0.f, 0.f, 0.f};
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int ia = 0; ia < NA; ia++) ab[mt][ia] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 h8 blo, bhi;
-                codes_subnormal(raw, t, blo, bhi);
+                codes_subnormal(wq, t, blo, bhi);
+                const int ia = K4 ? 0 : 2 * (t >> 1);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
-                    alo[mt] = mfma16x16x32(abd[mt][t], blo, alo[mt]);
-                    ahi[mt] = mfma16x16x32(abd[mt][t + 4], bhi, ahi[mt]);
+                    ab[mt][ia] = mfma16x16x32(abd[mt][t], blo, ab[mt][ia]);
+                    ab[mt][ia + 1] = mfma16x16x32(abd[mt][t + 4], bhi, ab[mt][ia + 1]);
                 }
             }
             float* slot = parts + e * SLOT;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                // this lane's column n = 4 rowl + g and its sub-blocks 2kg, 2kg+1: row 4kg + g
-                float plo = alo[mt][0], phi = ahi[mt][0];
+                // this lane's column n = 4 rowl + g and its two blocks: MFMA row 4kg + g
+                float p[NA];
 #pragma unroll
-                for (int gg = 1; gg < 4; gg++)
-                    if (g == gg) {
-                        plo = alo[mt][gg];
-                        phi = ahi[mt][gg];
-                    }
+                for (int ia = 0; ia < NA; ia++) {
+                    p[ia] = ab[mt][ia][0];
+#pragma unroll
+                    for (int gg = 1; gg < 4; gg++)
+                        if (g == gg) p[ia] = ab[mt][ia][gg];
+                }
                 const float* ts = (const float*)(trow[mt] + G * s_in * 32);
-                float y = sb.d20 * __builtin_fmaf(sb.c_lo16, plo, sb.c_hi * phi) -
-                          sb.dmin * __builtin_fmaf(sb.m_lo, ts[0], sb.m_hi * ts[1]);
+                float y;
+                if constexpr (K4) {
+                    const BdScl sb = scales_bd(raw, kg);
+                    y = sb.d20 * __builtin_fmaf(sb.c_lo16, p[0], sb.c_hi * p[1]) -
+                        sb.dmin * __builtin_fmaf(sb.m_lo, ts[0], sb.m_hi * ts[1]);
+                } else {
+                    // sum a (q - 8) d = d (2^20 (16 p_lo + p_hi) - 8 S) per block
+                    float da20, db20;
+                    bd_block_scales(raw, da20, db20);
+                    // (8 d S = 2^-17 d20 S)
+                    y = __builtin_fmaf(da20, __builtin_fmaf(16.0f, p[0], p[1]), db20 * __builtin_fmaf(16.0f, p[2], p[3])) -
+                        0x1p-17f * __builtin_fmaf(da20, ts[0], db20 * ts[1]);
+                }
                 // parked per lane: the lane groups and segments are summed once per
                 // sub-tile, after its steps
                 slot[mt * 64 + lane] = y;
@@ -552,7 +596,7 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false) {
     const int nsg = g.K / 256;
     if (nsg % G) return false;
     const int nsteps = nsg / G, R = 16 / G;
-    if (BD ? (g.qtype != QT_Q4_K || G != 4 || g.M > MT) : g.M > MT * R) return false;
+    if (BD ? (G != 4 || g.M > MT) : g.M > MT * R) return false;
     p.BD = BD;
     const int T = (g.N + R - 1) / R;
     p.G = G;
@@ -566,7 +610,7 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false) {
         const int nsub = (T + 256 * rounds - 1) / (256 * rounds);
         const int S = nsub * nsteps;
         if (S > kMaxSteps || nsub > kMaxSub) continue;
-        const int64_t tab = g.qtype == QT_Q4_K ? (int64_t)g.M * nsg * 32 : 0;   // block sums
+        const int64_t tab = g.qtype == QT_Q4_K || BD ? (int64_t)g.M * nsg * 32 : 0;   // block sums
         const int64_t slot = BD ? MT * 64 : MT * R * R;
         const int64_t lds = kFlagBytes + a_bytes + (int64_t)S * kStep + (int64_t)S * slot * 4 + tab;
         if (lds > kMaxLds) {
@@ -601,9 +645,7 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
 
 template <int QT>
 hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
-    if constexpr (QT == QT_Q4_K) {
-        if (p.BD) return launch_lds<QT, 4, 1, true>(g, p, st);
-    }
+    if (p.BD) return launch_lds<QT, 4, 1, true>(g, p, st);
     if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1>(g, p, st);
     if (p.G == 4 && p.MT == 2) return launch_lds<QT, 4, 2>(g, p, st);
     if (p.G == 2 && p.MT == 1) return launch_lds<QT, 2, 1>(g, p, st);
@@ -613,7 +655,7 @@ hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
 bool choose_lds(const GemmArgs& g, LdsPlan& p) {
     // sub-block rows at batch 1 only: from two rows on, its MFMA count doubles
     // and the factored MFMA form is faster
-    if (g.qtype == QT_Q4_K && g.M == 1 && plan_lds(g, 4, 1, p, true)) return true;
+    if (g.M == 1 && plan_lds(g, 4, 1, p, true)) return true;
     if (g.M <= 4 && plan_lds(g, 4, 1, p)) return true;
     if (g.M <= 8 && plan_lds(g, 4, 2, p)) return true;
     if (g.M <= 8 && plan_lds(g, 2, 1, p)) return true;
