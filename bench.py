@@ -98,10 +98,11 @@ def bench_lib():
     vp, i, d = ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_double)
     L.bfb_time_gemms.argtypes = [i, vp, vp, i, vp, i, vp, i, i, i, i, i, i, i, i, i, vp, d]
     L.bfb_time_sequence.argtypes = [i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, d]
+    L.bfb_time_sequence_batched.argtypes = [i, i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, vp, d]
     L.bfb_read_peak.argtypes = [vp, ctypes.c_size_t, i, vp, vp, d]
     L.bfb_copy.argtypes = [vp, vp, ctypes.c_size_t, i, vp, d]
     L.bfb_last_error.restype = ctypes.c_char_p
-    for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_read_peak", "bfb_copy"):
+    for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_time_sequence_batched", "bfb_read_peak", "bfb_copy"):
         getattr(L, f).restype = i
     return L
 
@@ -265,27 +266,38 @@ def run_layer(L, args, dev):
     cnt = len(seq)
     arr = lambda t, xs: P((t * cnt)(*xs))
     ms = ctypes.c_double()
-    steps = (args.steps // len(LAYER)) * len(LAYER) or len(LAYER)
+    nlin = len(LAYER)
+    steps = (args.steps // nlin) * nlin or nlin
+    warmup = (args.warmup // nlin) * nlin
+    common = (arr(ctypes.c_int, [2] * cnt), arr(ctypes.c_void_p, [s[0] for s in seq]), None,
+              arr(ctypes.c_void_p, [s[1] for s in seq]), arr(ctypes.c_int, [s[4] for s in seq]),
+              arr(ctypes.c_void_p, [s[2] for s in seq]), arr(ctypes.c_int, [s[3] for s in seq]),
+              arr(ctypes.c_int, [M] * cnt), arr(ctypes.c_int, [s[3] for s in seq]),
+              arr(ctypes.c_int, [s[4] for s in seq]), 0)
     out = []
-    for graph in ((0, 1) if args.graph == "both" else (int(args.graph),)):
-        torch.cuda.synchronize()
-        rc = L.bfb_time_sequence(cnt, arr(ctypes.c_int, [2] * cnt), arr(ctypes.c_void_p, [s[0] for s in seq]), None,
-                                 arr(ctypes.c_void_p, [s[1] for s in seq]), arr(ctypes.c_int, [s[4] for s in seq]),
-                                 arr(ctypes.c_void_p, [s[2] for s in seq]), arr(ctypes.c_int, [s[3] for s in seq]),
-                                 arr(ctypes.c_int, [M] * cnt), arr(ctypes.c_int, [s[3] for s in seq]),
-                                 arr(ctypes.c_int, [s[4] for s in seq]), 0, args.algo_id,
-                                 args.warmup, steps, graph, stream_handle(), ctypes.byref(ms))
-        torch.cuda.synchronize()
-        if rc != 0:
-            raise RuntimeError("bench host: " + L.bfb_last_error().decode())
-        t_layer = ms.value / 1e3 / (steps / len(LAYER))
-        rec = {"M": M, "us_per_layer": round(t_layer * 1e6, 3), "layer_tok_s": round(M / t_layer, 1),
-               "weight_GBps": round(layer_bytes / t_layer / 1e9, 2),
-               "hbm_frac": round(layer_bytes / t_layer / 1e9 / HBM_PEAK_GBPS, 4),
-               "launch": "graph" if graph else "stream", "layers_rotated": nl}
-        log(f"[bench] layer M=32 {rec['launch']}: {rec['us_per_layer']:.2f} us/layer "
-            f"{rec['weight_GBps']:.1f} GB/s {rec['layer_tok_s']:.0f} tok/s")
-        out.append(rec)
+    # "single": one bf_gemm per linear; "batched": the layer's five linears in one
+    # bf_gemm_batched call (one launch when all of them are K-split GEMMs)
+    modes = ("single", "batched") if args.layer_launch == "both" else (args.layer_launch,)
+    for mode in modes:
+        for graph in ((0, 1) if args.graph == "both" else (int(args.graph),)):
+            torch.cuda.synchronize()
+            if mode == "single":
+                rc = L.bfb_time_sequence(cnt, *common, args.algo_id, warmup, steps, graph, stream_handle(),
+                                         ctypes.byref(ms))
+            else:
+                rc = L.bfb_time_sequence_batched(cnt, nlin, *common, warmup, steps, graph, stream_handle(),
+                                                 ctypes.byref(ms))
+            torch.cuda.synchronize()
+            if rc != 0:
+                raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+            t_layer = ms.value / 1e3 / (steps / nlin)
+            rec = {"M": M, "us_per_layer": round(t_layer * 1e6, 3), "layer_tok_s": round(M / t_layer, 1),
+                   "weight_GBps": round(layer_bytes / t_layer / 1e9, 2),
+                   "hbm_frac": round(layer_bytes / t_layer / 1e9 / HBM_PEAK_GBPS, 4),
+                   "launch": "graph" if graph else "stream", "calls": mode, "layers_rotated": nl}
+            log(f"[bench] layer M=32 {mode} {rec['launch']}: {rec['us_per_layer']:.2f} us/layer "
+                f"{rec['weight_GBps']:.1f} GB/s {rec['layer_tok_s']:.0f} tok/s")
+            out.append(rec)
     return out
 
 
@@ -339,6 +351,8 @@ def main():
     ap.add_argument("--batches", default="1,8,32")
     ap.add_argument("--graph", default="both", choices=["0", "1", "both"],
                     help="issue launches on the stream (0), replay a HIP graph (1), or time both")
+    ap.add_argument("--layer-launch", default="both", choices=["single", "batched", "both"],
+                    help="layer workload: one bf_gemm per linear, one bf_gemm_batched per layer, or both")
     ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "dot2", "simple", "lds", "slab", "split"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -395,7 +409,7 @@ def main():
                   "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
                   "data": "synthetic",
                   "config": {"workload": "q4_k qkv 5120->7168, o 5120->5120, gate/up 5120->17408, down 17408->5120",
-                             "M": 32, "launch": b["launch"]},
+                             "M": 32, "launch": b["launch"], "calls": b["calls"]},
                   "layer_tok_s": b["layer_tok_s"], "runs": recs}
     elif args.workload == "copy":
         record = run_copy(L, args, dev)

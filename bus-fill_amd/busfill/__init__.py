@@ -29,8 +29,15 @@ OUT_F32, OUT_F16 = 0, 1
 # bf_algo
 ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT = 0, 1, 2, 3, 4, 5, 6
 
-EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_dequant_f16",
+EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16",
            "bf_status_str", "bf_last_error", "bf_version")
+
+
+class GemmDesc(ctypes.Structure):
+    """bf_gemm_desc: one GEMM of a bf_gemm_batched call."""
+    _fields_ = [("W", ctypes.c_void_p), ("W_aux", ctypes.c_void_p), ("A", ctypes.c_void_p),
+                ("lda", ctypes.c_int), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int),
+                ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int)]
 
 
 class BusfillError(RuntimeError):
@@ -59,7 +66,8 @@ def lib() -> ctypes.CDLL:
         L.bf_gemm.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
         L.bf_gemm_ex.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, i, vp]
         L.bf_dequant_f16.argtypes = [i, vp, vp, vp, i, i, vp]
-        for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_dequant_f16"):
+        L.bf_gemm_batched.argtypes = [i, i, i, ctypes.POINTER(GemmDesc), vp]
+        for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16"):
             getattr(L, f).restype = i
         L.bf_status_str.argtypes = [i]
         L.bf_status_str.restype = ctypes.c_char_p
@@ -100,6 +108,17 @@ def gemm(qtype: int, W, W_aux, A, C, M: int, N: int, K: int, *, lda: int | None 
     st = lib().bf_gemm_ex(qtype, _ptr(W), _ptr(W_aux), _ptr(A), K if lda is None else lda,
                           _ptr(C), N if ldc is None else ldc, otype, M, N, K, algo, _stream(stream))
     _check(st, "bf_gemm_ex")
+
+
+def gemm_batched(qtype: int, gemms, *, otype: int = OUT_F32, stream=None) -> None:
+    """Independent GEMMs in as few launches as the library can: `gemms` is a
+    list of (W, W_aux, A, C, M, N, K) with device tensors or addresses (lda = K,
+    ldc = N); each C is overwritten as by gemm()."""
+    descs = (GemmDesc * max(1, len(gemms)))()
+    for d, (W, W_aux, A, C, M, N, K) in zip(descs, gemms):
+        d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, d.M, d.N, d.K = (_ptr(W), _ptr(W_aux), _ptr(A), K, _ptr(C), N,
+                                                               M, N, K)
+    _check(lib().bf_gemm_batched(qtype, otype, len(gemms), descs, _stream(stream)), "bf_gemm_batched")
 
 
 def busfill_q4(A, Wq, Ws, C, Bsz: int, K: int, N: int, stream=None) -> None:

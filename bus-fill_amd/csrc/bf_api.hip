@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "bf_device.h"
 #include "bf_launch.h"
@@ -57,9 +58,8 @@ bool fast_eligible(const bf::GemmArgs& g) {
     return true;
 }
 
-bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
-                   int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream) {
-    g_last_error[0] = '\0';
+bf_status check_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
+                     int ldc, bf_otype otype, int M, int N, int K) {
     bf_status st = check_weights(qtype, W, W_aux, N, K);
     if (st != BF_OK) return st;
     if (!A || !C) return fail(BF_ERR_INVALID, "A or C is NULL");
@@ -69,6 +69,14 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
     if (otype != BF_OUT_F32 && otype != BF_OUT_F16) return fail(BF_ERR_INVALID, "unknown otype %d", (int)otype);
     if (!aligned(A, 2)) return fail(BF_ERR_INVALID, "A is not 2-byte aligned");
     if (!aligned(C, otype == BF_OUT_F32 ? 4 : 2)) return fail(BF_ERR_INVALID, "C is not aligned to its element");
+    return BF_OK;
+}
+
+bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
+                   int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream) {
+    g_last_error[0] = '\0';
+    bf_status st = check_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K);
+    if (st != BF_OK) return st;
     if (algo < BF_ALGO_AUTO || algo > BF_ALGO_SPLIT) return fail(BF_ERR_INVALID, "unknown algo %d", (int)algo);
 
     const size_t csize = otype == BF_OUT_F32 ? 4 : 2;
@@ -167,6 +175,46 @@ bf_status bf_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16
 bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
                      int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream) {
     return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, algo, stream);
+}
+
+bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs, void* stream) {
+    g_last_error[0] = '\0';
+    if (count < 0) return fail(BF_ERR_INVALID, "count=%d must be >= 0", count);
+    if (count > 0 && !descs) return fail(BF_ERR_INVALID, "descs is NULL");
+    for (int i = 0; i < count; i++) {
+        const bf_gemm_desc& d = descs[i];
+        const bf_status st = check_gemm(qtype, d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, otype, d.M, d.N, d.K);
+        if (st != BF_OK) return st;
+    }
+    // one launch per eight GEMMs when every one of them is a K-split GEMM (the
+    // automatic choice at 9-32 rows when the activations do not fit in LDS)
+    std::vector<bf::GemmArgs> gs(count);
+    bool together = count > 1;
+    for (int i = 0; i < count && together; i++) {
+        const bf_gemm_desc& d = descs[i];
+        bf::GemmArgs& g = gs[i];
+        g.qtype = (int)qtype;
+        g.W = (const uint8_t*)d.W;
+        g.Waux = (const uint8_t*)d.W_aux;
+        g.A = d.A;
+        g.lda = d.lda;
+        g.C = d.C;
+        g.ldc = d.ldc;
+        g.out_f16 = otype == BF_OUT_F16;
+        g.M = d.M;
+        g.N = d.N;
+        g.K = d.K;
+        together = d.M <= kSplitMaxM && fast_eligible(g) && !bf::lds_supports(g) && bf::split_supports(g);
+    }
+    if (together && bf::split_batched_supports(gs.data(), count))
+        return from_hip(bf::gemm_split_batched(gs.data(), count, (hipStream_t)stream), "batched launch");
+    for (int i = 0; i < count; i++) {
+        const bf_gemm_desc& d = descs[i];
+        const bf_status st =
+            run_gemm(qtype, d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, otype, d.M, d.N, d.K, BF_ALGO_AUTO, stream);
+        if (st != BF_OK) return st;
+    }
+    return BF_OK;
 }
 
 bf_status bf_busfill_q4(const uint16_t* A, const uint8_t* Wq, const uint16_t* Ws, float* C, int Bsz, int K, int N,

@@ -61,16 +61,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t workspace_rsrc(float* ws, int 
     return __builtin_amdgcn_make_buffer_rsrc(ws, (short)0, (int)((int64_t)S * N * Mp * 4), 0x00020000);
 }
 
+// One GEMM's share of a launch: workgroup `bid` of its grid.
 template <int QT, int MT>
-__global__ __launch_bounds__(64 * (kSpNC + kSpNL))
-void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
-                  int nt, int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C,
-                  int ldc, int out_f16, float* __restrict__ ws, unsigned* __restrict__ counters) {
+__device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
+                                           const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nt,
+                                           int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux,
+                                           void* __restrict__ C, int ldc, int out_f16, float* __restrict__ ws,
+                                           unsigned* __restrict__ counters) {
     constexpr int NC = kSpNC, NL = kSpNL;
-    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int rg = blockIdx.x / S, s = blockIdx.x - rg * S;
+    const int rg = bid / S, s = bid - rg * S;
     const int sg0 = s * nsgS;
     int* const flags = (int*)lds;
     const uint32_t lds0 = lds_addr(lds);
@@ -268,6 +269,49 @@ void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A,
     }
 }
 
+template <int QT, int MT>
+__global__ __launch_bounds__(64 * (kSpNC + kSpNL))
+void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
+                  int nt, int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C,
+                  int ldc, int out_f16, float* __restrict__ ws, unsigned* __restrict__ counters) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    split_body<QT, MT>((int)blockIdx.x, lds, W, A, lda, M, N, K, nt, S, nsgS, unit_bytes, Waux, C, ldc, out_f16, ws,
+                       counters);
+}
+
+// Several independent GEMMs in one launch (their grids back to back): a
+// workgroup finds its GEMM by its id.  Workgroups of a later GEMM start as
+// those of an earlier one retire, so one GEMM's cross-split exchange overlaps
+// the next one's weight stream, and the launch gaps between them disappear.
+constexpr int kSpMaxJobs = 8;
+struct SplitJob {
+    const uint8_t* W;
+    const uint8_t* Waux;
+    const uint16_t* A;
+    void* C;
+    float* ws;
+    unsigned* counters;
+    int lda, ldc, M, N, K, nt, S, nsgS, unit_bytes, grid0;
+};
+struct SplitJobs {
+    SplitJob job[kSpMaxJobs];
+    int n, out_f16;
+};
+
+template <int QT, int MT>
+__global__ __launch_bounds__(64 * (kSpNC + kSpNL))
+void k_gemm_split_batched(const SplitJobs jobs) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    // the last job whose grid starts at or before this workgroup (uniform
+    // selects over the kernel arguments: no dynamic indexing)
+    SplitJob j = jobs.job[0];
+#pragma unroll
+    for (int i = 1; i < kSpMaxJobs; i++)
+        if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
+    split_body<QT, MT>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nt, j.S, j.nsgS,
+                       j.unit_bytes, j.Waux, j.C, j.ldc, jobs.out_f16, j.ws, j.counters);
+}
+
 __global__ void k_zero_u32(unsigned* p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
 }
@@ -371,12 +415,103 @@ hipError_t dispatch_split(const GemmArgs& g, const SplitPlan& p, hipStream_t st)
     return p.MT == 1 ? launch_split<QT, 1>(g, p, st) : launch_split<QT, 2>(g, p, st);
 }
 
+// Up to kSpMaxJobs GEMMs of one format and one m-tile count in one launch.
+template <int QT, int MT>
+hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, hipStream_t st) {
+    auto k = k_gemm_split_batched<QT, MT>;
+    static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(attr_set.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        if (e != hipSuccess) return e;
+        attr_set.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    // one workspace for the launch: every job's counters (kept zero between
+    // launches), then every job's partials, at 256-byte offsets
+    size_t cb[kSpMaxJobs] = {}, pb[kSpMaxJobs] = {}, ctot = 0, ptot = 0;
+    for (int i = 0; i < n; i++) {
+        if (ps[i].S == 1) continue;
+        const int T = (gs[i].N + 15) / 16, rgs = (T + ps[i].nt - 1) / ps[i].nt;
+        cb[i] = ((size_t)rgs * kSpCounterStride * 4 + 255) & ~(size_t)255;
+        pb[i] = ((size_t)ps[i].S * gs[i].N * ((gs[i].M + 3) & ~3) * 4 + 255) & ~(size_t)255;
+        ctot += cb[i];
+        ptot += pb[i];
+    }
+    unsigned* counters = nullptr;
+    float* parts = nullptr;
+    if (ctot) {
+        e = workspace(st, ctot, ptot, &counters, &parts);
+        if (e != hipSuccess) return e;
+    }
+    SplitJobs jobs = {};
+    jobs.n = n;
+    jobs.out_f16 = gs[0].out_f16;
+    int grid = 0, lds = 0;
+    size_t co = 0, po = 0;
+    for (int i = 0; i < n; i++) {
+        const GemmArgs& g = gs[i];
+        const SplitPlan& p = ps[i];
+        jobs.job[i] = SplitJob{g.W, g.Waux, g.A, g.C,
+                               p.S > 1 ? (float*)((uint8_t*)parts + po) : nullptr,
+                               p.S > 1 ? (unsigned*)((uint8_t*)counters + co) : nullptr,
+                               g.lda, g.ldc, g.M, g.N, g.K, p.nt, p.S, p.nsgS, p.unit_bytes, grid};
+        co += cb[i];
+        po += pb[i];
+        grid += p.grid;
+        lds = std::max(lds, p.lds);
+    }
+    hipLaunchKernelGGL(k, dim3(grid), dim3(64 * (kSpNC + kSpNL)), lds, st, jobs);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 bool split_supports(const GemmArgs& g) {
     SplitPlan p;
     if (g.qtype == QT_PLANES && ((uintptr_t)g.Waux & 15)) return false;
     return plan_split(g, p);
+}
+
+bool split_batched_supports(const GemmArgs* gs, int n) {
+    if (n < 1) return false;
+    for (int i = 0; i < n; i++) {
+        SplitPlan p;
+        if (gs[i].qtype != gs[0].qtype || gs[i].out_f16 != gs[0].out_f16) return false;
+        if ((gs[i].M <= 16) != (gs[0].M <= 16)) return false;      // one m-tile count per launch
+        if (gs[i].qtype == QT_PLANES && ((uintptr_t)gs[i].Waux & 15)) return false;
+        if (!plan_split(gs[i], p)) return false;
+    }
+    return true;
+}
+
+hipError_t gemm_split_batched(const GemmArgs* gs, int n, hipStream_t st) {
+    if (!split_batched_supports(gs, n)) return hipErrorInvalidValue;
+    for (int i0 = 0; i0 < n; i0 += kSpMaxJobs) {
+        const int m = std::min(kSpMaxJobs, n - i0);
+        SplitPlan ps[kSpMaxJobs];
+        for (int i = 0; i < m; i++) plan_split(gs[i0 + i], ps[i]);
+        const bool mt1 = gs[0].M <= 16;
+        hipError_t e;
+        switch (gs[0].qtype) {
+            case QT_Q4_K:
+                e = mt1 ? launch_split_batched<QT_Q4_K, 1>(gs + i0, ps, m, st)
+                        : launch_split_batched<QT_Q4_K, 2>(gs + i0, ps, m, st);
+                break;
+            case QT_PLANES:
+                e = mt1 ? launch_split_batched<QT_PLANES, 1>(gs + i0, ps, m, st)
+                        : launch_split_batched<QT_PLANES, 2>(gs + i0, ps, m, st);
+                break;
+            default:
+                e = mt1 ? launch_split_batched<QT_Q4_0, 1>(gs + i0, ps, m, st)
+                        : launch_split_batched<QT_Q4_0, 2>(gs + i0, ps, m, st);
+                break;
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t gemm_split(const GemmArgs& g, hipStream_t st) {

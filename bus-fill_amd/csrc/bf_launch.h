@@ -28,6 +28,10 @@ hipError_t gemm_slab(const GemmArgs& g, hipStream_t st);
 bool slab_supports(const GemmArgs& g);
 hipError_t gemm_split(const GemmArgs& g, hipStream_t st);
 bool split_supports(const GemmArgs& g);
+// Independent GEMMs of one format, one output type and one side of M = 16, in
+// launches of up to eight (their grids back to back).
+hipError_t gemm_split_batched(const GemmArgs* gs, int n, hipStream_t st);
+bool split_batched_supports(const GemmArgs* gs, int n);
 bool dot2_supports(const GemmArgs& g);
 hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
                        int N, int K, hipStream_t st);

@@ -53,21 +53,41 @@ int issue(const Launch& l, int otype, int algo, hipStream_t st) {
     return 0;
 }
 
-// Runs `warmup` then `steps` launches taken cyclically from seq; returns ms.
+// `group` consecutive GEMMs from seq (cyclically) in one bf_gemm_batched call.
+int issue_group(const std::vector<Launch>& seq, size_t first, int group, int otype, hipStream_t st) {
+    std::vector<bf_gemm_desc> d(group);
+    for (int j = 0; j < group; j++) {
+        const Launch& l = seq[(first + j) % seq.size()];
+        d[j] = bf_gemm_desc{l.W, l.W_aux, l.A, l.lda, l.C, l.ldc, l.M, l.N, l.K};
+    }
+    bf_status s = bf_gemm_batched((bf_qtype)seq[first % seq.size()].qtype, (bf_otype)otype, group, d.data(), st);
+    if (s != BF_OK) {
+        g_bf = s;
+        return -1;
+    }
+    return 0;
+}
+
+// Runs `warmup` then `steps` GEMMs taken cyclically from seq, one launch call
+// per GEMM (group 1) or one bf_gemm_batched call per `group` GEMMs; returns ms.
 int time_seq(const std::vector<Launch>& seq, int otype, int algo, int warmup, int steps, int use_graph,
-             hipStream_t st, double* ms_out) {
+             hipStream_t st, double* ms_out, int group = 1) {
     const size_t n = seq.size();
+    auto issue = [&](const Launch&, int i) -> int {
+        if (group > 1) return (i % group) ? 0 : issue_group(seq, (size_t)i, group, otype, st);
+        return ::issue(seq[i % n], otype, algo, st);
+    };
     hipEvent_t e0, e1;
     HCK(hipEventCreate(&e0));
     HCK(hipEventCreate(&e1));
     float ms = 0.f;
     if (!use_graph) {
         for (int i = 0; i < warmup; i++)
-            if (issue(seq[i % n], otype, algo, st)) return -1;
+            if (issue(seq[i % n], i)) return -1;
         HCK(hipStreamSynchronize(st));
         HCK(hipEventRecord(e0, st));
         for (int i = 0; i < steps; i++)
-            if (issue(seq[i % n], otype, algo, st)) return -1;
+            if (issue(seq[i % n], i)) return -1;
         HCK(hipEventRecord(e1, st));
         HCK(hipEventSynchronize(e1));
         HCK(hipEventElapsedTime(&ms, e0, e1));
@@ -76,7 +96,7 @@ int time_seq(const std::vector<Launch>& seq, int otype, int algo, int warmup, in
             hipGraph_t g;
             HCK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
             for (int i = 0; i < count; i++)
-                if (issue(seq[i % n], otype, algo, st)) {
+                if (issue(seq[i % n], i)) {
                     hipGraph_t dead;
                     (void)hipStreamEndCapture(st, &dead);
                     return -1;
@@ -145,6 +165,22 @@ int bfb_time_sequence(int n, const int* qtype, const void* const* W, const void*
     for (int i = 0; i < n; i++)
         seq.push_back(Launch{qtype[i], W[i], W_aux ? W_aux[i] : nullptr, A[i], lda[i], C[i], ldc[i], M[i], N[i], K[i]});
     return time_seq(seq, otype, algo, warmup, steps, use_graph, (hipStream_t)stream, ms_out);
+}
+
+// The same list issued as bf_gemm_batched calls of `group` consecutive GEMMs
+// (warmup and steps count GEMMs and must be multiples of group).
+int bfb_time_sequence_batched(int n, int group, const int* qtype, const void* const* W, const void* const* W_aux,
+                              const uint16_t* const* A, const int* lda, void* const* C, const int* ldc,
+                              const int* M, const int* N, const int* K, int otype, int warmup, int steps,
+                              int use_graph, void* stream, double* ms_out) {
+    if (group < 1 || n % group || warmup % group || steps % group) {
+        g_err = hipErrorInvalidValue;
+        return -1;
+    }
+    std::vector<Launch> seq;
+    for (int i = 0; i < n; i++)
+        seq.push_back(Launch{qtype[i], W[i], W_aux ? W_aux[i] : nullptr, A[i], lda[i], C[i], ldc[i], M[i], N[i], K[i]});
+    return time_seq(seq, otype, 0, warmup, steps, use_graph, (hipStream_t)stream, ms_out, group);
 }
 
 // Streaming 128-bit read of `bytes` at `src`, `reps` times; returns ms.

@@ -87,6 +87,28 @@ bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux,
                      const uint16_t* A, int lda, void* C, int ldc, bf_otype otype,
                      int M, int N, int K, bf_algo algo, void* stream);
 
+/* One GEMM of a batch: bf_gemm's arguments C[0:M][0:N] = A[0:M][0:K] . dequant(W)^T. */
+typedef struct {
+    const void* W;
+    const void* W_aux;
+    const uint16_t* A;
+    int lda;
+    void* C;
+    int ldc;
+    int M, N, K;
+} bf_gemm_desc;
+
+/* `count` independent GEMMs of one format and one output type on `stream`,
+ * with the results of calling bf_gemm for each (bit-identical).  No GEMM's
+ * output may overlap another one's inputs or output: they may run
+ * concurrently.  When every GEMM is a K-split GEMM (9-32 rows whose
+ * activations do not fit in LDS) they share one launch per eight GEMMs, so one
+ * GEMM's cross-split exchange overlaps the next one's weight stream and the
+ * launch gaps go away (a decoder layer's linears at batch 32); otherwise one
+ * launch per GEMM.  No counterpart in the reference, whose only entry point is
+ * the single-GEMM kernel (kernels/busfill_v1a.cu:41-46). */
+bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs, void* stream);
+
 /* Bit-exact fp16 dequant: W_f16[N][K] = RN_fp16(value), value computed in fp32
  * exactly as kernels/busfill_v0.cu:74,78-81 ((q-8)*fp32(d)) for the Q4_0
  * formats and as ggml dequantize_row_q4_K ((d*sc)*q - dmin*m) for Q4_K. */

@@ -100,3 +100,25 @@ def test_product_sources_do_not_use_the_oracle():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "liboracle" not in text, f
+
+
+def test_batched_rejects_invalid_descs_before_any_launch():
+    L = bf.lib()
+    d = (bf.GemmDesc * 2)()
+    for x in d:
+        x.W, x.W_aux, x.A, x.lda, x.C, x.ldc, x.M, x.N, x.K = FAKE, None, FAKE, 512, FAKE, 64, 32, 64, 512
+    d[1].M = 0
+    assert L.bf_gemm_batched(bf.Q4_0, bf.OUT_F32, 2, d, None) == bf.ERR_INVALID
+    assert "M=0" in L.bf_last_error().decode()
+    d[1].M, d[1].lda = 32, 100
+    assert L.bf_gemm_batched(bf.Q4_0, bf.OUT_F32, 2, d, None) == bf.ERR_INVALID
+    assert L.bf_gemm_batched(bf.Q4_0, bf.OUT_F32, -1, d, None) == bf.ERR_INVALID
+    assert L.bf_gemm_batched(bf.Q4_0, bf.OUT_F32, 1, None, None) == bf.ERR_INVALID
+    assert L.bf_gemm_batched(bf.Q4_0, bf.OUT_F32, 0, None, None) == bf.OK
+
+
+def test_gemm_desc_layout_matches_header():
+    # pointers at 0, 8, 16; lda at 24; C at 32 (after padding); ldc, M, N, K at 40..52
+    assert ctypes.sizeof(bf.GemmDesc) == 56
+    assert bf.GemmDesc.C.offset == 32 and bf.GemmDesc.K.offset == 52
+    assert "bf_gemm_desc" in HDR

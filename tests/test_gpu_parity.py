@@ -418,6 +418,34 @@ def test_formats_agree_bitwise_and_runs_are_deterministic(dev):
         assert (gpu_gemm(b, A, dev) == Cb).all()
 
 
+BATCH_SHAPES = [(1792, 5120), (1280, 5120), (600, 17408), (77, 2048), (5120, 5120)]
+
+
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+@pytest.mark.parametrize("Ms,otype", [((32,) * 5, bf.OUT_F32), ((16,) * 5, bf.OUT_F32), ((32,) * 5, bf.OUT_F16),
+                                      ((32, 32, 1, 32, 9), bf.OUT_F32)],
+                         ids=["m32", "m16", "m32-f16", "mixed"])
+def test_batched_matches_single_launches(dev, qt, Ms, otype):
+    """bf_gemm_batched: GEMMs of different shapes in one call give bit-identical
+    results to one bf_gemm each (one launch when all of them are K-split GEMMs,
+    one launch per GEMM otherwise), and the per-stream workspace stays
+    consistent when single and batched calls alternate."""
+    ws = [O.gen_weights(qt, N, K, seed=N + K + 13 * qt + i) for i, (N, K) in enumerate(BATCH_SHAPES)]
+    dws = [upload(w, dev) for w in ws]
+    As = [O.gen_act(M, w.K, seed=w.K + 7 * i) for i, (M, w) in enumerate(zip(Ms, ws))]
+    dAs = [to_dev(A, dev) for A in As]
+    dt = torch.float32 if otype == bf.OUT_F32 else torch.float16
+    for rep in range(2):
+        singles = [gpu_gemm(w, A, dev, otype=otype, dw=dw) for w, A, dw in zip(ws, As, dws)]
+        Cs = [torch.full((M, w.N), float("nan"), device=dev, dtype=dt) for M, w in zip(Ms, ws)]
+        bf.gemm_batched(qt, [(dw[0], dw[1], dA, C, M, w.N, w.K) for dw, dA, C, M, w in zip(dws, dAs, Cs, Ms, ws)],
+                        otype=otype)
+        torch.cuda.synchronize()
+        for i, (C, ref) in enumerate(zip(Cs, singles)):
+            got = C.float().cpu().numpy().astype(np.float64)
+            assert (got == ref).all(), (rep, i, BATCH_SHAPES[i], Ms[i])
+
+
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
 def test_full_size_exact_properties(dev, qt):
     """Size-independent checks at the benchmark shape: scaling A by 2 is exact
