@@ -251,7 +251,7 @@ def best(recs, M):
 
 def run_layer(L, args, dev):
     import torch
-    M = 32
+    M = args.layer_m
     layer_bytes = sum(n * k * 9 // 16 for _, n, k in LAYER)
     nl = max(1, math.ceil(ROTATION_BYTES / layer_bytes))
     log(f"[bench] layer: {nl} distinct layers x {layer_bytes / 1e6:.1f} MB")
@@ -295,7 +295,7 @@ def run_layer(L, args, dev):
                    "weight_GBps": round(layer_bytes / t_layer / 1e9, 2),
                    "hbm_frac": round(layer_bytes / t_layer / 1e9 / HBM_PEAK_GBPS, 4),
                    "launch": "graph" if graph else "stream", "calls": mode, "layers_rotated": nl}
-            log(f"[bench] layer M=32 {mode} {rec['launch']}: {rec['us_per_layer']:.2f} us/layer "
+            log(f"[bench] layer M={M} {mode} {rec['launch']}: {rec['us_per_layer']:.2f} us/layer "
                 f"{rec['weight_GBps']:.1f} GB/s {rec['layer_tok_s']:.0f} tok/s")
             out.append(rec)
     return out
@@ -351,6 +351,7 @@ def main():
     ap.add_argument("--batches", default="1,8,32")
     ap.add_argument("--graph", default="both", choices=["0", "1", "both"],
                     help="issue launches on the stream (0), replay a HIP graph (1), or time both")
+    ap.add_argument("--layer-m", type=int, default=32, help="layer workload: batch rows (config: 32)")
     ap.add_argument("--layer-launch", default="both", choices=["single", "batched", "both"],
                     help="layer workload: one bf_gemm per linear, one bf_gemm_batched per layer, or both")
     ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "dot2", "simple", "lds", "slab", "split"])
@@ -403,13 +404,14 @@ def main():
     elif args.workload == "layer":
         recs = run_layer(L, args, dev)
         b = min(recs, key=lambda r: r["us_per_layer"])
-        record = {"metric": "layer-sum weight-stream GB/s + tok/s, 27B-class decoder layer Q4_K linears at batch 32",
+        record = {"metric": "layer-sum weight-stream GB/s + tok/s, 27B-class decoder layer Q4_K linears at batch "
+                            f"{args.layer_m}",
                   "value": b["weight_GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
                   "warmup": args.warmup, "ms_per_step": round(b["us_per_layer"] / 1e3 / len(LAYER), 6),
                   "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
                   "data": "synthetic",
                   "config": {"workload": "q4_k qkv 5120->7168, o 5120->5120, gate/up 5120->17408, down 17408->5120",
-                             "M": 32, "launch": b["launch"], "calls": b["calls"]},
+                             "M": args.layer_m, "launch": b["launch"], "calls": b["calls"]},
                   "layer_tok_s": b["layer_tok_s"], "runs": recs}
     elif args.workload == "copy":
         record = run_copy(L, args, dev)

@@ -186,11 +186,12 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
         const bf_status st = check_gemm(qtype, d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, otype, d.M, d.N, d.K);
         if (st != BF_OK) return st;
     }
-    // one launch per eight GEMMs when every one of them is a K-split GEMM (the
+    // one launch per eight GEMMs when every one of them takes the same
+    // LDS-staged kernel shape (batch 1-8) or every one is a K-split GEMM (the
     // automatic choice at 9-32 rows when the activations do not fit in LDS)
     std::vector<bf::GemmArgs> gs(count);
-    bool together = count > 1;
-    for (int i = 0; i < count && together; i++) {
+    bool all_lds = count > 1, all_split = count > 1;
+    for (int i = 0; i < count && (all_lds || all_split); i++) {
         const bf_gemm_desc& d = descs[i];
         bf::GemmArgs& g = gs[i];
         g.qtype = (int)qtype;
@@ -204,9 +205,13 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
         g.M = d.M;
         g.N = d.N;
         g.K = d.K;
-        together = d.M <= kSplitMaxM && fast_eligible(g) && !bf::lds_supports(g) && bf::split_supports(g);
+        const bool fast = fast_eligible(g), lds = fast && bf::lds_supports(g);
+        all_lds = all_lds && lds;
+        all_split = all_split && fast && !lds && d.M <= kSplitMaxM && bf::split_supports(g);
     }
-    if (together && bf::split_batched_supports(gs.data(), count))
+    if (all_lds && bf::lds_batched_supports(gs.data(), count))
+        return from_hip(bf::gemm_lds_batched(gs.data(), count, (hipStream_t)stream), "batched launch");
+    if (all_split && bf::split_batched_supports(gs.data(), count))
         return from_hip(bf::gemm_split_batched(gs.data(), count, (hipStream_t)stream), "batched launch");
     for (int i = 0; i < count; i++) {
         const bf_gemm_desc& d = descs[i];

@@ -63,6 +63,7 @@
 // the eight block scales followed by the 128 code bytes).  Lane (r, kg) reads
 // column r at a 36-dword stride: the 16 lanes of a k-group fall on 16 distinct
 // 4-bank groups.
+#include <algorithm>
 #include <atomic>
 
 #include "bf_launch.h"
@@ -88,11 +89,12 @@ constexpr int kSubCount = 768, kMaxSub = 224;
 constexpr int kStepCounter = 15;                  // flags[15]: next step to take
 constexpr int kASlots = 6;                        // activation instructions per loader and segment
 
+// One GEMM's share of a launch: workgroup `bid` of its grid.
 template <int QT, int G, int MT, int NC, int NL, bool BD>
-__global__ __launch_bounds__(64 * (NC + NL))
-void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
-                int nsub, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc, int out_f16) {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+__device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
+                                         const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
+                                         const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc,
+                                         int out_f16) {
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     static_assert(!BD || G == 4, "sub-block rows: four K segments");
     // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
@@ -101,7 +103,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsg = K >> 8, nsteps = nsg / G;
     const int S = nsub * nsteps;                       // steps of the workgroup
-    const int tile0 = blockIdx.x * nsub;
+    const int tile0 = bid * nsub;
     const int seg_bytes = M * G * 528, a_bytes = nsteps * seg_bytes;
     int* const flags = (int*)lds;
     uint8_t* const a_lds = lds + kFlagBytes;
@@ -244,7 +246,7 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
         // per-workgroup offset (the workgroups all read the same lines), and
         // raise a flag once their own loads are complete
         const int cw = wave - NL, nA = (nsg * 33 + 63) >> 6;
-        const int rot = (int)((blockIdx.x * 7u) % (unsigned)nA);
+        const int rot = (int)(((unsigned)bid * 7u) % (unsigned)nA);
         for (int i0 = cw; i0 < nA; i0 += NC) {
             const int i = i0 + rot < nA ? i0 + rot : i0 + rot - nA;
             const int P = 64 * i + lane;
@@ -583,6 +585,43 @@ void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, i
     }
 }
 
+template <int QT, int G, int MT, int NC, int NL, bool BD>
+__global__ __launch_bounds__(64 * (NC + NL))
+void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
+                int nsub, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc, int out_f16) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, Waux, C, ldc, out_f16);
+}
+
+// Several independent GEMMs of one kernel shape in one launch (their grids
+// back to back): a workgroup finds its GEMM by its id, and workgroups of a
+// later GEMM start as those of an earlier one retire, so one GEMM's compute
+// tail overlaps the next one's weight stream.
+constexpr int kLdsMaxJobs = 8;
+struct LdsJob {
+    const uint8_t* W;
+    const uint8_t* Waux;
+    const uint16_t* A;
+    void* C;
+    int lda, ldc, M, N, K, nsub, grid0;
+};
+struct LdsJobs {
+    LdsJob job[kLdsMaxJobs];
+    int n, out_f16;
+};
+
+template <int QT, int G, int MT, int NC, int NL, bool BD>
+__global__ __launch_bounds__(64 * (NC + NL))
+void k_gemm_lds_batched(const LdsJobs jobs) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    LdsJob j = jobs.job[0];
+#pragma unroll
+    for (int i = 1; i < kLdsMaxJobs; i++)
+        if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
+    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub, j.Waux,
+                                    j.C, j.ldc, jobs.out_f16);
+}
+
 constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 struct LdsPlan {
@@ -663,7 +702,76 @@ bool choose_lds(const GemmArgs& g, LdsPlan& p) {
     return false;
 }
 
+template <int QT, int G, int MT, bool BD>
+hipError_t launch_lds_batched(const GemmArgs* gs, const LdsPlan* ps, int n, hipStream_t st) {
+    auto k = k_gemm_lds_batched<QT, G, MT, kNC, kNL, BD>;
+    static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(attr_set.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        if (e != hipSuccess) return e;
+        attr_set.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    LdsJobs jobs = {};
+    jobs.n = n;
+    jobs.out_f16 = gs[0].out_f16;
+    int grid = 0, lds = 0;
+    for (int i = 0; i < n; i++) {
+        const GemmArgs& g = gs[i];
+        jobs.job[i] = LdsJob{g.W, g.Waux, g.A, g.C, g.lda, g.ldc, g.M, g.N, g.K, ps[i].nsub, grid};
+        grid += ps[i].grid;
+        lds = std::max(lds, ps[i].lds);
+    }
+    hipLaunchKernelGGL(k, dim3(grid), dim3(64 * (kNC + kNL)), lds, st, jobs);
+    return hipGetLastError();
+}
+
+// The kernel shapes that have a batched launch: batch 1 (sub-block rows) and
+// G = 4 with one or two m-tiles (batch 2-8).
+bool lds_batchable(const LdsPlan& p) { return p.G == 4 && (p.BD || p.MT <= 2); }
+
+template <int QT>
+hipError_t dispatch_lds_batched(const GemmArgs* gs, const LdsPlan* ps, int n, hipStream_t st) {
+    if (ps[0].BD) return launch_lds_batched<QT, 4, 1, true>(gs, ps, n, st);
+    if (ps[0].MT == 1) return launch_lds_batched<QT, 4, 1, false>(gs, ps, n, st);
+    return launch_lds_batched<QT, 4, 2, false>(gs, ps, n, st);
+}
+
 }  // namespace
+
+bool lds_batched_supports(const GemmArgs* gs, int n) {
+    if (n < 1) return false;
+    LdsPlan p0;
+    for (int i = 0; i < n; i++) {
+        LdsPlan p;
+        if (gs[i].qtype != gs[0].qtype || gs[i].out_f16 != gs[0].out_f16) return false;
+        if (gs[i].qtype == QT_PLANES && ((uintptr_t)gs[i].Waux & 15)) return false;
+        if (!choose_lds(gs[i], p) || !lds_batchable(p)) return false;
+        if (i == 0) p0 = p;
+        else if (p.G != p0.G || p.MT != p0.MT || p.BD != p0.BD) return false;
+    }
+    return true;
+}
+
+hipError_t gemm_lds_batched(const GemmArgs* gs, int n, hipStream_t st) {
+    if (!lds_batched_supports(gs, n)) return hipErrorInvalidValue;
+    for (int i0 = 0; i0 < n; i0 += kLdsMaxJobs) {
+        const int m = std::min(kLdsMaxJobs, n - i0);
+        LdsPlan ps[kLdsMaxJobs];
+        for (int i = 0; i < m; i++) choose_lds(gs[i0 + i], ps[i]);
+        hipError_t e;
+        switch (gs[0].qtype) {
+            case QT_Q4_K: e = dispatch_lds_batched<QT_Q4_K>(gs + i0, ps, m, st); break;
+            case QT_PLANES: e = dispatch_lds_batched<QT_PLANES>(gs + i0, ps, m, st); break;
+            default: e = dispatch_lds_batched<QT_Q4_0>(gs + i0, ps, m, st); break;
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
 
 bool lds_supports(const GemmArgs& g) {
     LdsPlan p;

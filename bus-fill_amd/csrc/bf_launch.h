@@ -24,6 +24,10 @@ hipError_t gemm_dot2(const GemmArgs& g, hipStream_t st);
 hipError_t gemm_simple(const GemmArgs& g, hipStream_t st);
 hipError_t gemm_lds(const GemmArgs& g, hipStream_t st);
 bool lds_supports(const GemmArgs& g);
+// Independent GEMMs that all take the same LDS-staged kernel shape (batch 1,
+// or G = 4 at batch 2-8), in launches of up to eight.
+hipError_t gemm_lds_batched(const GemmArgs* gs, int n, hipStream_t st);
+bool lds_batched_supports(const GemmArgs* gs, int n);
 hipError_t gemm_slab(const GemmArgs& g, hipStream_t st);
 bool slab_supports(const GemmArgs& g);
 hipError_t gemm_split(const GemmArgs& g, hipStream_t st);

@@ -101,11 +101,11 @@ typedef struct {
 /* `count` independent GEMMs of one format and one output type on `stream`,
  * with the results of calling bf_gemm for each (bit-identical).  No GEMM's
  * output may overlap another one's inputs or output: they may run
- * concurrently.  When every GEMM is a K-split GEMM (9-32 rows whose
- * activations do not fit in LDS) they share one launch per eight GEMMs, so one
- * GEMM's cross-split exchange overlaps the next one's weight stream and the
- * launch gaps go away (a decoder layer's linears at batch 32); otherwise one
- * launch per GEMM.  No counterpart in the reference, whose only entry point is
+ * concurrently.  When every GEMM takes the same LDS-staged kernel shape
+ * (batch 1-8) or every one is a K-split GEMM (9-32 rows whose activations do
+ * not fit in LDS) they share one launch per eight GEMMs, so one GEMM's tail
+ * overlaps the next one's weight stream and the launch gaps go away (a decoder
+ * layer's linears); otherwise one launch per GEMM.  No counterpart in the reference, whose only entry point is
  * the single-GEMM kernel (kernels/busfill_v1a.cu:41-46). */
 bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs, void* stream);
 

@@ -423,13 +423,15 @@ BATCH_SHAPES = [(1792, 5120), (1280, 5120), (600, 17408), (77, 2048), (5120, 512
 
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
 @pytest.mark.parametrize("Ms,otype", [((32,) * 5, bf.OUT_F32), ((16,) * 5, bf.OUT_F32), ((32,) * 5, bf.OUT_F16),
-                                      ((32, 32, 1, 32, 9), bf.OUT_F32)],
-                         ids=["m32", "m16", "m32-f16", "mixed"])
+                                      ((1,) * 5, bf.OUT_F32), ((1,) * 5, bf.OUT_F16), ((2,) * 5, bf.OUT_F32),
+                                      ((8,) * 5, bf.OUT_F32), ((32, 32, 1, 32, 9), bf.OUT_F32)],
+                         ids=["m32", "m16", "m32-f16", "m1", "m1-f16", "m2", "m8", "mixed"])
 def test_batched_matches_single_launches(dev, qt, Ms, otype):
     """bf_gemm_batched: GEMMs of different shapes in one call give bit-identical
-    results to one bf_gemm each (one launch when all of them are K-split GEMMs,
-    one launch per GEMM otherwise), and the per-stream workspace stays
-    consistent when single and batched calls alternate."""
+    results to one bf_gemm each (one launch when all of them take the same
+    LDS-staged kernel shape or all are K-split GEMMs, one launch per GEMM
+    otherwise), and the per-stream workspace stays consistent when single and
+    batched calls alternate."""
     ws = [O.gen_weights(qt, N, K, seed=N + K + 13 * qt + i) for i, (N, K) in enumerate(BATCH_SHAPES)]
     dws = [upload(w, dev) for w in ws]
     As = [O.gen_act(M, w.K, seed=w.K + 7 * i) for i, (M, w) in enumerate(zip(Ms, ws))]
