@@ -30,6 +30,8 @@ OUT_F32, OUT_F16 = 0, 1
 ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT = 0, 1, 2, 3, 4, 5, 6
 
 EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16",
+           "bf_gguf_open", "bf_gguf_close", "bf_gguf_tensor_count", "bf_gguf_tensor_at", "bf_gguf_find",
+           "bf_gguf_get_u64", "bf_gguf_get_str", "bf_gguf_upload",
            "bf_status_str", "bf_last_error", "bf_version")
 
 
@@ -38,6 +40,13 @@ class GemmDesc(ctypes.Structure):
     _fields_ = [("W", ctypes.c_void_p), ("W_aux", ctypes.c_void_p), ("A", ctypes.c_void_p),
                 ("lda", ctypes.c_int), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int),
                 ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int)]
+
+
+class GgufTensor(ctypes.Structure):
+    """bf_gguf_tensor: one tensor of a GGUF file."""
+    _fields_ = [("name", ctypes.c_char_p), ("ggml_type", ctypes.c_uint32), ("qtype", ctypes.c_int32),
+                ("n_dims", ctypes.c_uint32), ("dims", ctypes.c_uint64 * 4), ("offset", ctypes.c_uint64),
+                ("nbytes", ctypes.c_uint64), ("data", ctypes.c_void_p)]
 
 
 class BusfillError(RuntimeError):
@@ -67,6 +76,20 @@ def lib() -> ctypes.CDLL:
         L.bf_gemm_ex.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, i, vp]
         L.bf_dequant_f16.argtypes = [i, vp, vp, vp, i, i, vp]
         L.bf_gemm_batched.argtypes = [i, i, i, ctypes.POINTER(GemmDesc), vp]
+        L.bf_gguf_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(vp)]
+        L.bf_gguf_close.argtypes = [vp]
+        L.bf_gguf_close.restype = None
+        L.bf_gguf_tensor_count.argtypes = [vp]
+        L.bf_gguf_tensor_count.restype = ctypes.c_int64
+        L.bf_gguf_tensor_at.argtypes = [vp, ctypes.c_int64, ctypes.POINTER(GgufTensor)]
+        L.bf_gguf_find.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(GgufTensor)]
+        L.bf_gguf_get_u64.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]
+        L.bf_gguf_get_str.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p),
+                                      ctypes.POINTER(ctypes.c_uint64)]
+        L.bf_gguf_upload.argtypes = [vp, ctypes.POINTER(GgufTensor), vp, vp]
+        for f in ("bf_gguf_open", "bf_gguf_tensor_at", "bf_gguf_find", "bf_gguf_get_u64", "bf_gguf_get_str",
+                  "bf_gguf_upload"):
+            getattr(L, f).restype = i
         for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16"):
             getattr(L, f).restype = i
         L.bf_status_str.argtypes = [i]
@@ -119,6 +142,66 @@ def gemm_batched(qtype: int, gemms, *, otype: int = OUT_F32, stream=None) -> Non
         d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, d.M, d.N, d.K = (_ptr(W), _ptr(W_aux), _ptr(A), K, _ptr(C), N,
                                                                M, N, K)
     _check(lib().bf_gemm_batched(qtype, otype, len(gemms), descs, _stream(stream)), "bf_gemm_batched")
+
+
+class Gguf:
+    """A GGUF file opened by the library's reader (memory-mapped).
+
+    tensors(): every tensor's GgufTensor; find(name); get_u64 / get_str for
+    metadata; upload(tensor, device_tensor_or_address) copies the bytes to the
+    device unchanged (Q4_0 / Q4_K blocks are bf_gemm's layouts)."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        _check(lib().bf_gguf_open(os.fsencode(path), ctypes.byref(h)), "bf_gguf_open")
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().bf_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self):
+        out = []
+        for i in range(lib().bf_gguf_tensor_count(self._h)):
+            t = GgufTensor()
+            _check(lib().bf_gguf_tensor_at(self._h, i, ctypes.byref(t)), "bf_gguf_tensor_at")
+            out.append(t)
+        return out
+
+    def find(self, name: str) -> GgufTensor:
+        t = GgufTensor()
+        _check(lib().bf_gguf_find(self._h, name.encode(), ctypes.byref(t)), "bf_gguf_find")
+        return t
+
+    def get_u64(self, key: str) -> int:
+        v = ctypes.c_uint64()
+        _check(lib().bf_gguf_get_u64(self._h, key.encode(), ctypes.byref(v)), "bf_gguf_get_u64")
+        return v.value
+
+    def get_str(self, key: str) -> bytes:
+        p, n = ctypes.c_char_p(), ctypes.c_uint64()
+        _check(lib().bf_gguf_get_str(self._h, key.encode(), ctypes.byref(p), ctypes.byref(n)), "bf_gguf_get_str")
+        return ctypes.string_at(p, n.value)
+
+    def data(self, t: GgufTensor) -> bytes:
+        """The tensor's bytes as mapped (a copy)."""
+        return ctypes.string_at(t.data, t.nbytes) if t.nbytes else b""
+
+    def upload(self, t: GgufTensor, dst, stream=None) -> None:
+        _check(lib().bf_gguf_upload(self._h, ctypes.byref(t), _ptr(dst), _stream(stream)), "bf_gguf_upload")
 
 
 def busfill_q4(A, Wq, Ws, C, Bsz: int, K: int, N: int, stream=None) -> None:

@@ -251,6 +251,14 @@ const char* bf_status_str(bf_status s) {
 
 const char* bf_last_error(void) { return g_last_error; }
 
+}  // extern "C"
+
+namespace bf {
+void set_last_error(const char* text) { snprintf(g_last_error, sizeof g_last_error, "%s", text); }
+}  // namespace bf
+
+extern "C" {
+
 int bf_version(void) { return 100; }
 
 }  // extern "C"

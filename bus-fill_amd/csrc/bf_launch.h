@@ -37,6 +37,9 @@ bool split_supports(const GemmArgs& g);
 hipError_t gemm_split_batched(const GemmArgs* gs, int n, hipStream_t st);
 bool split_batched_supports(const GemmArgs* gs, int n);
 bool dot2_supports(const GemmArgs& g);
+// The calling thread's text for bf_last_error().
+void set_last_error(const char* text);
+
 hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
                        int N, int K, hipStream_t st);
 

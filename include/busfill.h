@@ -115,6 +115,39 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
 bf_status bf_dequant_f16(bf_qtype qtype, const void* W, const void* W_aux,
                          uint16_t* W_f16, int N, int K, void* stream);
 
+/* ---------------------------------------------------------------- GGUF files
+ * A reader of llama.cpp's model files (GGUF versions 2 and 3, public
+ * specification), memory-mapped.  Q4_0 and Q4_K tensors are stored in the
+ * block layouts bf_gemm takes, so their bytes go to the device unchanged (no
+ * repack).  The file is treated as untrusted input: every length and offset
+ * is checked against the file size.  No counterpart in the reference, which
+ * names the format (kernels/q4k_batched.py:7-8) but reads no file. */
+typedef struct bf_gguf bf_gguf;
+
+typedef struct {
+    const char* name;      /* NUL-terminated; valid until bf_gguf_close */
+    uint32_t ggml_type;    /* ggml type code: 0 F32, 1 F16, 2 Q4_0, 12 Q4_K, ... */
+    int32_t qtype;         /* the matching bf_qtype (BF_Q4_0, BF_Q4_K), or -1 */
+    uint32_t n_dims;
+    uint64_t dims[4];      /* dims[0] = weights per row (K), dims[1] = rows (N); unused dims are 1 */
+    uint64_t offset;       /* byte offset of the data in the file */
+    uint64_t nbytes;       /* 0 when the type's size is unknown to the reader */
+    const void* data;      /* host address of the mapped data (NULL when nbytes is 0) */
+} bf_gguf_tensor;
+
+bf_status bf_gguf_open(const char* path, bf_gguf** out);
+void bf_gguf_close(bf_gguf* g);
+int64_t bf_gguf_tensor_count(const bf_gguf* g);
+bf_status bf_gguf_tensor_at(const bf_gguf* g, int64_t index, bf_gguf_tensor* out);
+bf_status bf_gguf_find(const bf_gguf* g, const char* name, bf_gguf_tensor* out);
+/* Metadata: a non-negative integer value of any integer type (or bool), or a
+ * string (not NUL-terminated: *len bytes at *out, inside the mapping). */
+bf_status bf_gguf_get_u64(const bf_gguf* g, const char* key, uint64_t* out);
+bf_status bf_gguf_get_str(const bf_gguf* g, const char* key, const char** out, uint64_t* len);
+/* Copies a tensor's bytes to device memory dst (t->nbytes bytes) on stream and
+ * waits for the copy. */
+bf_status bf_gguf_upload(const bf_gguf* g, const bf_gguf_tensor* t, void* dst, void* stream);
+
 /* Static text for a status code. */
 const char* bf_status_str(bf_status status);
 

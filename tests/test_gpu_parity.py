@@ -503,3 +503,25 @@ def test_lds_small_batch_parity(dev, qt, K, N):
         ref.check(C, f"lds {QT_NAME[qt]} N={N} K={K} M={M}", rows=M,
                   form="f32" if qt == O.Q4_K or M == 1 else "f16")
         assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_LDS, dw=dw) == C).all()
+
+
+def test_gguf_tensors_feed_the_gemm(dev, tmp_path):
+    """Weights written to a GGUF file, read back and uploaded by the library's
+    reader, give the oracle's GEMM results (the blocks need no repack)."""
+    from test_gguf import GGML, write_gguf
+    wk = O.gen_weights(O.Q4_K, 256, 5120, seed=77)
+    w0 = O.gen_weights(O.Q4_0, 100, 2048, seed=78)
+    path = tmp_path / "model.gguf"
+    write_gguf(path, [(b"general.architecture", 8, b"llama")],
+               [(b"blk.0.ffn_down.weight", GGML["q4_k"][0], [5120, 256], wk.W.tobytes()),
+                (b"blk.0.attn_k.weight", GGML["q4_0"][0], [2048, 100], w0.W.tobytes())], alignment=64)
+    with bf.Gguf(path) as g:
+        for name, w in (("blk.0.ffn_down.weight", wk), ("blk.0.attn_k.weight", w0)):
+            t = g.find(name)
+            assert t.qtype == w.qtype and (t.dims[0], t.dims[1]) == (w.K, w.N)
+            Wd = torch.empty(t.nbytes, dtype=torch.uint8, device=dev)
+            g.upload(t, Wd)
+            for M in (1, 8, 32):
+                A = O.gen_act(M, w.K, seed=M + w.K)
+                C = gpu_gemm(w, A, dev, dw=(Wd, None))
+                Ref(w, A).check(C, f"gguf {name} M={M}")
