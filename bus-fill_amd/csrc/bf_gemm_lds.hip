@@ -80,7 +80,8 @@ namespace {
 // s * seg_bytes, its batch row m at m * G * 528, super-group g at g * 528;
 // then the W steps of the workgroup in order (2304 bytes each); then one
 // parked partial per step; then (Q4_K) the activation block sums, 32 bytes per
-// batch row and super-group.
+// batch row and super-group.  When the steps do not all fit, the W steps
+// region is a ring of nslot step slots (whole groups of four steps).
 constexpr int kFlagBytes = 4096;
 constexpr int kAMark = 16, kMaxSeg = 96;
 constexpr int kTabFlag = 400;
@@ -88,13 +89,14 @@ constexpr int kStepMark = 512, kMaxSteps = 240;
 constexpr int kSubCount = 768, kMaxSub = 224;
 constexpr int kStepCounter = 15;                  // flags[15]: next step to take
 constexpr int kASlots = 6;                        // activation instructions per loader and segment
+constexpr int kMinRing = 16;                      // fewest steps in a ring of reused step slots
 
 // One GEMM's share of a launch: workgroup `bid` of its grid.
 template <int QT, int G, int MT, int NC, int NL, bool BD>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                          const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
-                                         const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc,
-                                         int out_f16) {
+                                         int nslot, const uint8_t* __restrict__ Waux, void* __restrict__ C,
+                                         int ldc, int out_f16) {
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     static_assert(!BD || G == 4, "sub-block rows: four K segments");
     // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
@@ -107,8 +109,8 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     const int seg_bytes = M * G * 528, a_bytes = nsteps * seg_bytes;
     int* const flags = (int*)lds;
     uint8_t* const a_lds = lds + kFlagBytes;
-    uint8_t* const w_lds = a_lds + a_bytes;
-    float* const parts = (float*)(w_lds + S * kStep);
+    uint8_t* const w_lds = a_lds + a_bytes;            // ring of nslot steps (nslot = S: no reuse)
+    float* const parts = (float*)(w_lds + nslot * kStep);
     const uint32_t lds0 = lds_addr(lds);
 
     // Every wave clears 256 bytes of the flags, then meets the others at the
@@ -147,6 +149,9 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                      : "=v"(warm) : "v"(w_piece<QT>(W, Waux, (int64_t)tile0 * R, 0, 1, K)) : "memory");
         const int pmax = S * 144 - 1;
         const uint32_t m0 = lds0 + (uint32_t)(kFlagBytes + a_bytes);
+        // groups in the ring: nslot is a multiple of 4 when the ring wraps, and
+        // nslot = S (every group at its own place) when it does not
+        const int G4R = (nslot + 3) >> 2;
         const int b_lo = (9 * j) / 4, b_hi = (9 * j + 8) / 4;   // this loader's instructions in a group
         uint32_t pat[3];
 #pragma unroll
@@ -190,6 +195,10 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                 }
             }
             if (e < S) {
+                // the slot's previous step must be consumed (its marker set to 2
+                // by the compute wave that read it) before it is overwritten
+                if (e >= nslot) wait_flag_value(&flags[kStepMark + e - nslot], 2);
+                const uint32_t gbase = m0 + (uint32_t)((g4 % G4R) * 4 * kStep);
                 const StepBase<QT> base = step_base<QT>((int64_t)(tile0 + te) * R, G * se, K);
 #pragma unroll
                 for (int q = 0; q < 3; q++) {
@@ -207,7 +216,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                         const int64_t row = min((int64_t)(tile0 + te) * R + nn / G, (int64_t)N - 1);
                         src = w_piece<QT>(W, Waux, row, G * se + nn % G, c, K);
                     }
-                    if ((pb >> 29) == (uint32_t)j && P <= pmax) dma16(src, m0 + (uint32_t)(i << 10));
+                    if ((pb >> 29) == (uint32_t)j && P <= pmax) dma16(src, gbase + (uint32_t)(b << 10));
                 }
             }
             if (g4 == 0) clear_flags_and_meet();
@@ -401,7 +410,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             for (int it = 0;; it++) {
                 int mark;
                 asm volatile("ds_read_b32 %0, %1" : "=v"(mark) : "v"(lds_addr(&flags[kStepMark + e])) : "memory");
-                lds_raw<QT>(raw, w_lds + e * kStep + r * 144, kg);
+                lds_raw<QT>(raw, w_lds + (e % nslot) * kStep + r * 144, kg);
                 if (bd_on) {
 #pragma unroll
                     for (int mt = 0; mt < MT; mt++)
@@ -412,9 +421,14 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                 if (__builtin_amdgcn_readfirstlane(mark) != 0 || it >= (1 << 20)) break;
                 __builtin_amdgcn_s_sleep(1);
             }
+            // the step's slot is free again (its reads have completed)
+            if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kStepMark + e])), "v"(2) : "memory");
         } else {
             wait_flag(&flags[kStepMark + e]);
-            lds_raw<QT>(raw, w_lds + e * kStep + r * 144, kg);
+            lds_raw<QT>(raw, w_lds + (e % nslot) * kStep + r * 144, kg);
+            // a wave's LDS operations complete in order: the slot is free once this
+            // write is visible
+            if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kStepMark + e])), "v"(2) : "memory");
         }
         f4 acc[MT], accm[MT];
 #pragma unroll
@@ -588,9 +602,9 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
 template <int QT, int G, int MT, int NC, int NL, bool BD>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
-                int nsub, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc, int out_f16) {
+                int nsub, int nslot, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc, int out_f16) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, Waux, C, ldc, out_f16);
+    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, Waux, C, ldc, out_f16);
 }
 
 // Several independent GEMMs of one kernel shape in one launch (their grids
@@ -603,7 +617,7 @@ struct LdsJob {
     const uint8_t* Waux;
     const uint16_t* A;
     void* C;
-    int lda, ldc, M, N, K, nsub, grid0;
+    int lda, ldc, M, N, K, nsub, nslot, grid0;
 };
 struct LdsJobs {
     LdsJob job[kLdsMaxJobs];
@@ -618,14 +632,14 @@ void k_gemm_lds_batched(const LdsJobs jobs) {
 #pragma unroll
     for (int i = 1; i < kLdsMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
-    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub, j.Waux,
-                                    j.C, j.ldc, jobs.out_f16);
+    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub, j.nslot,
+                                    j.Waux, j.C, j.ldc, jobs.out_f16);
 }
 
 constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 struct LdsPlan {
-    int G, MT, nsub, grid, lds;
+    int G, MT, nsub, nslot, grid, lds;
     bool BD;                           // sub-block rows form (Q4_K, one batch row per m-tile)
 };
 
@@ -651,14 +665,21 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false) {
         if (S > kMaxSteps || nsub > kMaxSub) continue;
         const int64_t tab = g.qtype == QT_Q4_K || BD ? (int64_t)g.M * nsg * 32 : 0;   // block sums
         const int64_t slot = BD ? MT * 64 : MT * R * R;
-        const int64_t lds = kFlagBytes + a_bytes + (int64_t)S * kStep + (int64_t)S * slot * 4 + tab;
-        if (lds > kMaxLds) {
-            if (nsub == 1) return false;
-            continue;
+        const int64_t fixed = kFlagBytes + a_bytes + (int64_t)S * slot * 4 + tab;
+        // all steps resident, or a ring of whole groups of four steps (at least
+        // kMinRing steps) reused as the compute waves release them
+        int nslot = S;
+        if (fixed + (int64_t)S * kStep > kMaxLds) {
+            nslot = fixed < kMaxLds ? (int)((kMaxLds - fixed) / kStep) & ~3 : 0;
+            if (nslot < kMinRing) {
+                if (nsub == 1) return false;
+                continue;
+            }
         }
         p.nsub = nsub;
+        p.nslot = nslot;
         p.grid = (T + nsub - 1) / nsub;
-        p.lds = (int)lds;
+        p.lds = (int)(fixed + (int64_t)nslot * kStep);
         return true;
     }
     return false;
@@ -678,7 +699,7 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
         attr_set.fetch_or(bit, std::memory_order_acq_rel);
     }
     hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kNC + kNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K, p.nsub,
-                       g.Waux, g.C, g.ldc, g.out_f16);
+                       p.nslot, g.Waux, g.C, g.ldc, g.out_f16);
     return hipGetLastError();
 }
 
@@ -721,7 +742,7 @@ hipError_t launch_lds_batched(const GemmArgs* gs, const LdsPlan* ps, int n, hipS
     int grid = 0, lds = 0;
     for (int i = 0; i < n; i++) {
         const GemmArgs& g = gs[i];
-        jobs.job[i] = LdsJob{g.W, g.Waux, g.A, g.C, g.lda, g.ldc, g.M, g.N, g.K, ps[i].nsub, grid};
+        jobs.job[i] = LdsJob{g.W, g.Waux, g.A, g.C, g.lda, g.ldc, g.M, g.N, g.K, ps[i].nsub, ps[i].nslot, grid};
         grid += ps[i].grid;
         lds = std::max(lds, ps[i].lds);
     }

@@ -91,6 +91,17 @@ __device__ __forceinline__ void wait_flag(const int* flag) {
     }
 }
 
+// Spin until the LDS word at `flag` equals v.
+__device__ __forceinline__ void wait_flag_value(const int* flag, int v) {
+    const uint32_t a = lds_addr(flag);
+    for (int it = 0; it < (1 << 20); it++) {
+        int x;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(x) : "v"(a) : "memory");
+        if (__builtin_amdgcn_readfirstlane(x) == v) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // Spin until the LDS word at `flag` is at least n.
 __device__ __forceinline__ void wait_count(const int* flag, int n) {
     const uint32_t a = lds_addr(flag);
