@@ -666,11 +666,12 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false) {
         const int64_t tab = g.qtype == QT_Q4_K || BD ? (int64_t)g.M * nsg * 32 : 0;   // block sums
         const int64_t slot = BD ? MT * 64 : MT * R * R;
         const int64_t fixed = kFlagBytes + a_bytes + (int64_t)S * slot * 4 + tab;
-        // all steps resident, or a ring of whole groups of four steps (at least
-        // kMinRing steps) reused as the compute waves release them
+        // all steps resident, or (one workgroup per CU only: a second round of
+        // workgroups costs more than the ring saves) a ring of whole groups of
+        // four steps, at least kMinRing, reused as the compute waves release them
         int nslot = S;
         if (fixed + (int64_t)S * kStep > kMaxLds) {
-            nslot = fixed < kMaxLds ? (int)((kMaxLds - fixed) / kStep) & ~3 : 0;
+            nslot = rounds == 1 && fixed < kMaxLds ? (int)((kMaxLds - fixed) / kStep) & ~3 : 0;
             if (nslot < kMinRing) {
                 if (nsub == 1) return false;
                 continue;
