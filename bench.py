@@ -331,7 +331,7 @@ def run_sweep(L, args, dev):
     res = []
     for (N, K) in ((17408, 5120), (5120, 17408)):
         rot = Rotation("q4_k", N, K, ROTATION_BYTES, seed=N, dev=dev)
-        for M in (1, 2, 4, 8, 16, 32, 64, 128):
+        for M in (1, 2, 3, 4, 6, 8, 16, 32, 64, 128):
             ms = time_gemm(L, rot, M, args.steps, args.warmup, int(args.graph == "1"), args.algo_id, dev)
             r = gemm_record(rot, M, ms, args.steps, args.graph == "1")
             r.update({"N": N, "K": K})

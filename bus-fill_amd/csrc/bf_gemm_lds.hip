@@ -75,18 +75,24 @@ namespace {
 // LDS layout: [0, 4096) flags (ints): the compute waves' next-step counter at
 // 15; activation markers of loader j for segment s at 16 + 4s + j; block-sum
 // table flag of segment s at 400 + s; step markers at 512 + e; finished-step
-// counters of sub-tile t at 768 + t.  Then the
+// counters of sub-tile t at 768 + t; steps done with activation segment s at
+// 896 + s (activation ring only).  Then the
 // activations, segment-major: segment s (super-groups G s .. G s + G - 1) at
 // s * seg_bytes, its batch row m at m * G * 528, super-group g at g * 528;
 // then the W steps of the workgroup in order (2304 bytes each); then one
 // parked partial per step; then (Q4_K) the activation block sums, 32 bytes per
 // batch row and super-group.  When the steps do not all fit, the W steps
-// region is a ring of nslot step slots (whole groups of four steps).
+// region is a ring of nslot step slots (whole groups of four steps); when the
+// activations do not all fit either (batch 2-8 at K = 17408), they are a ring
+// of na segment slots and the steps run segment-major (all sub-tiles of
+// segment 0, then of segment 1, ...), so that each segment is released after
+// its nsub steps.
 constexpr int kFlagBytes = 4096;
 constexpr int kAMark = 16, kMaxSeg = 96;
 constexpr int kTabFlag = 400;
 constexpr int kStepMark = 512, kMaxSteps = 240;
-constexpr int kSubCount = 768, kMaxSub = 224;
+constexpr int kSubCount = 768, kMaxSub = 128;
+constexpr int kSegCount = 896;                    // steps done with activation segment s, at 896 + s
 constexpr int kStepCounter = 15;                  // flags[15]: next step to take
 constexpr int kASlots = 6;                        // activation instructions per loader and segment
 constexpr int kMinRing = 16;                      // fewest steps in a ring of reused step slots
@@ -95,7 +101,7 @@ constexpr int kMinRing = 16;                      // fewest steps in a ring of r
 template <int QT, int G, int MT, int NC, int NL, bool BD>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                          const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
-                                         int nslot, const uint8_t* __restrict__ Waux, void* __restrict__ C,
+                                         int nslot, int na, const uint8_t* __restrict__ Waux, void* __restrict__ C,
                                          int ldc, int out_f16) {
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     static_assert(!BD || G == 4, "sub-block rows: four K segments");
@@ -106,7 +112,9 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     const int nsg = K >> 8, nsteps = nsg / G;
     const int S = nsub * nsteps;                       // steps of the workgroup
     const int tile0 = bid * nsub;
-    const int seg_bytes = M * G * 528, a_bytes = nsteps * seg_bytes;
+    // na < nsteps: activation ring, steps in segment-major order
+    const bool seg_major = na < nsteps;
+    const int seg_bytes = M * G * 528, a_bytes = na * seg_bytes;
     int* const flags = (int*)lds;
     uint8_t* const a_lds = lds + kFlagBytes;
     uint8_t* const w_lds = a_lds + a_bytes;            // ring of nslot steps (nslot = S: no reuse)
@@ -179,14 +187,30 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             aon[q] = P < (uint32_t)PA && c < 32;
             asrc[q] = (const uint8_t*)(A + (int64_t)min((int)m, M - 1) * lda + 256 * gg + 8 * min((int)c, 31));
         }
-        int te = 0, se = j;                            // step e = te * nsteps + se
-        while (se >= nsteps) { se -= nsteps; te++; }
+        // step e = te * nsteps + se (sub-tile-major) or se * nsub + te (segment-major)
+        int te = 0, se = 0;
+        if (seg_major) {
+            te = j;
+            while (te >= nsub) { te -= nsub; se++; }
+        } else {
+            se = j;
+            while (se >= nsteps) { se -= nsteps; te++; }
+        }
         for (int g4 = 0, e = j; 4 * g4 < S; g4++, e += 4) {
             // the activation segments first needed by this group's steps (those of
-            // the first sub-tile: e < nsteps), then this loader's step of the group
-            const int s_hi = BD ? 0 : min(4 * g4 + 4, nsteps);   // (batch 1: the compute waves load A)
-            for (int s2 = 4 * g4; s2 < s_hi; s2++) {
-                const uint32_t dst = lds0 + (uint32_t)(kFlagBytes + s2 * seg_bytes);
+            // the first sub-tile: e < nsteps; segment-major: segments whose first
+            // step s * nsub is in the group), then this loader's step of the group
+            // (batch 1: the compute waves load A)
+            int s_lo = 4 * g4, s_hi = BD ? 0 : min(4 * g4 + 4, nsteps);
+            if (seg_major) {
+                s_lo = (4 * g4 + nsub - 1) / nsub;
+                s_hi = min((4 * g4 + 3) / nsub + 1, nsteps);
+            }
+            for (int s2 = s_lo; s2 < s_hi; s2++) {
+                // the segment's slot must be released by all nsub steps of its
+                // previous segment
+                if (s2 >= na) wait_flag_value(&flags[kSegCount + s2 - na], nsub);
+                const uint32_t dst = lds0 + (uint32_t)(kFlagBytes + (s2 % na) * seg_bytes);
 #pragma unroll
                 for (int q = 0; q < kASlots; q++) {
                     const int qa = j + 4 * q;
@@ -220,11 +244,16 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                 }
             }
             if (g4 == 0) clear_flags_and_meet();
-            for (int s2 = 4 * g4; s2 < s_hi; s2++)
+            for (int s2 = s_lo; s2 < s_hi; s2++)
                 dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kAMark + 4 * s2 + j)), lane);
             if (e < S) dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kStepMark + e)), lane);
-            se += 4;
-            while (se >= nsteps) { se -= nsteps; te++; }
+            if (seg_major) {
+                te += 4;
+                while (te >= nsub) { te -= nsub; se++; }
+            } else {
+                se += 4;
+                while (se >= nsteps) { se -= nsteps; te++; }
+            }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         asm volatile("" :: "v"(warm));
@@ -276,7 +305,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         for (int u = u0; u < u_end; u += ustep) {
             const int kq = u & 3, rest = u >> 2, s_seg = rest / (M * G), mg4 = rest - s_seg * (M * G);
             const int m = mg4 / G, gg = mg4 - m * G;
-            uint8_t* src = a_lds + s_seg * seg_bytes + (m * G + gg) * 528 + 128 * kq;
+            uint8_t* src = a_lds + (s_seg % na) * seg_bytes + (m * G + gg) * 528 + 128 * kq;
             u4 v[8];
 #pragma unroll
             for (int q = 0; q < 8; q++) v[q] = *(const u4*)(src + 16 * q);
@@ -363,8 +392,10 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int t = 0; t < 8; t++) abd[mt][t] = h8{};
-    // t_in = e / nsteps as (e * inv) >> 16: exact for e < 240, nsteps <= 96
-    const uint32_t inv_nsteps = (65536u + (uint32_t)nsteps - 1u) / (uint32_t)nsteps;
+    // e / div as (e * inv) >> 16 (div = nsteps, or nsub segment-major): exact
+    // for e < 240, div <= 128
+    const uint32_t div = seg_major ? (uint32_t)nsub : (uint32_t)nsteps;
+    const uint32_t inv_div = (65536u + div - 1u) / div;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const int m = BD ? min(mt, M - 1) : min(mt * R + r / G, M - 1);   // padding rows reread row M-1
@@ -388,7 +419,8 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             e = __builtin_amdgcn_readfirstlane(e);
         }
         if (e >= S) break;
-        const int t_in = (int)(((uint32_t)e * inv_nsteps) >> 16), s_in = e - t_in * nsteps;
+        const int q_in = (int)(((uint32_t)e * inv_div) >> 16), r_in = e - q_in * (int)div;
+        const int t_in = seg_major ? r_in : q_in, s_in = seg_major ? q_in : r_in;
         if constexpr (!BD) {
             wait_flags(flags + kAMark + 4 * s_in, NL, lane);   // the step's activation segment
             if constexpr (QT == QT_Q4_K) {
@@ -402,7 +434,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             }
         }
         Raw<QT> raw;
-        const uint8_t* const aseg = a_lds + s_in * seg_bytes;
+        const uint8_t* const aseg = a_lds + (s_in % na) * seg_bytes;
         if constexpr (BD) {
             // the step's marker with the step's weight and activation reads right
             // behind it: a wave's LDS reads complete in order, so a nonzero marker
@@ -521,8 +553,13 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             }
         }
         if constexpr (!BD) {
+            // the step's activation reads are issued (a wave's LDS operations
+            // complete in order): count it against its segment's slot
+            if (seg_major && lane == 0)
+                asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[kSegCount + s_in])), "v"(1) : "memory");
             // fold the G segments (lanes r = G*rowl + g) and park the partial sums
-            float* slot = parts + e * SLOT;
+            // (slots in sub-tile-major order whatever the step order)
+            float* slot = parts + (t_in * nsteps + s_in) * SLOT;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
@@ -602,9 +639,10 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
 template <int QT, int G, int MT, int NC, int NL, bool BD>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
-                int nsub, int nslot, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc, int out_f16) {
+                int nsub, int nslot, int na, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc,
+                int out_f16) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, Waux, C, ldc, out_f16);
+    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, Waux, C, ldc, out_f16);
 }
 
 // Several independent GEMMs of one kernel shape in one launch (their grids
@@ -617,7 +655,7 @@ struct LdsJob {
     const uint8_t* Waux;
     const uint16_t* A;
     void* C;
-    int lda, ldc, M, N, K, nsub, nslot, grid0;
+    int lda, ldc, M, N, K, nsub, nslot, na, grid0;
 };
 struct LdsJobs {
     LdsJob job[kLdsMaxJobs];
@@ -633,19 +671,21 @@ void k_gemm_lds_batched(const LdsJobs jobs) {
     for (int i = 1; i < kLdsMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
     lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub, j.nslot,
-                                    j.Waux, j.C, j.ldc, jobs.out_f16);
+                                    j.na, j.Waux, j.C, j.ldc, jobs.out_f16);
 }
 
 constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 struct LdsPlan {
-    int G, MT, nsub, nslot, grid, lds;
+    int G, MT, nsub, nslot, na, grid, lds;
     bool BD;                           // sub-block rows form (Q4_K, one batch row per m-tile)
 };
 
 // Sub-tiles per workgroup: about one workgroup per CU when the LDS holds all of
-// its steps, otherwise the fewest rounds of 256 workgroups that fit.
-bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false) {
+// its steps, otherwise the fewest rounds of 256 workgroups that fit.  With one
+// round only, the weight steps may be a ring of reused slots, and (MFMA form,
+// aring) the activation segments too, the steps then run segment-major.
+bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false, bool aring = false) {
     const int nsg = g.K / 256;
     if (nsg % G) return false;
     const int nsteps = nsg / G, R = 16 / G;
@@ -657,30 +697,53 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false) {
     // activation segments of G super-groups x M rows (528-byte super-group images:
     // the 16 lanes of a k-group read 16 distinct bank groups for G = 1, 2, 4)
     if (nsteps > kMaxSeg || g.M * G > 32) return false;
-    const int64_t a_bytes = (int64_t)nsteps * g.M * G * 528;
-    if (a_bytes > kMaxLds) return false;
+    const int64_t seg = (int64_t)g.M * G * 528;
     for (int rounds = 1; rounds <= 64; rounds++) {
         const int nsub = (T + 256 * rounds - 1) / (256 * rounds);
         const int S = nsub * nsteps;
         if (S > kMaxSteps || nsub > kMaxSub) continue;
         const int64_t tab = g.qtype == QT_Q4_K || BD ? (int64_t)g.M * nsg * 32 : 0;   // block sums
         const int64_t slot = BD ? MT * 64 : MT * R * R;
-        const int64_t fixed = kFlagBytes + a_bytes + (int64_t)S * slot * 4 + tab;
-        // all steps resident, or (one workgroup per CU only: a second round of
-        // workgroups costs more than the ring saves) a ring of whole groups of
-        // four steps, at least kMinRing, reused as the compute waves release them
-        int nslot = S;
-        if (fixed + (int64_t)S * kStep > kMaxLds) {
-            nslot = rounds == 1 && fixed < kMaxLds ? (int)((kMaxLds - fixed) / kStep) & ~3 : 0;
-            if (nslot < kMinRing) {
+        const int64_t base = kFlagBytes + (int64_t)S * slot * 4 + tab;
+        // step slots left beside na activation segments (whole groups of four)
+        auto ring = [&](int na) {
+            const int64_t f = base + na * seg;
+            return f < kMaxLds ? (int)((kMaxLds - f) / kStep) & ~3 : 0;
+        };
+        int na = nsteps, nslot = S;
+        if (base + nsteps * seg + (int64_t)S * kStep > kMaxLds) {
+            // a second round of workgroups costs more than a ring saves
+            nslot = rounds == 1 ? ring(nsteps) : 0;
+            if (nslot < kMinRing && rounds == 1 && aring && !BD) {
+                // both rings: the loaders run na * nsub steps at most ahead of the
+                // compute waves and nslot at most; the best of the two bounds.
+                // (na - 1) nsub >= 4: a segment's slot is released by steps of
+                // earlier groups of four (no loader waits for its own loads)
+                int best = 0;
+                for (int a = 2; a < nsteps; a++) {
+                    if ((a - 1) * nsub < 4) continue;
+                    const int rs = std::min(ring(a), S);
+                    if (rs < kMinRing && rs < S) continue;
+                    const int score = std::min(rs, a * nsub);
+                    if (score > best) {
+                        best = score;
+                        na = a;
+                        nslot = rs;
+                    }
+                }
+                if (best == 0) nslot = 0;
+            }
+            if (nslot < kMinRing && nslot < S) {
                 if (nsub == 1) return false;
+                na = nsteps;
                 continue;
             }
         }
         p.nsub = nsub;
         p.nslot = nslot;
+        p.na = na;
         p.grid = (T + nsub - 1) / nsub;
-        p.lds = (int)(fixed + (int64_t)nslot * kStep);
+        p.lds = (int)(base + na * seg + (int64_t)nslot * kStep);
         return true;
     }
     return false;
@@ -700,7 +763,7 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
         attr_set.fetch_or(bit, std::memory_order_acq_rel);
     }
     hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kNC + kNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K, p.nsub,
-                       p.nslot, g.Waux, g.C, g.ldc, g.out_f16);
+                       p.nslot, p.na, g.Waux, g.C, g.ldc, g.out_f16);
     return hipGetLastError();
 }
 
@@ -717,9 +780,9 @@ bool choose_lds(const GemmArgs& g, LdsPlan& p) {
     // sub-block rows at batch 1 only: from two rows on, its MFMA count doubles
     // and the factored MFMA form is faster
     if (g.M == 1 && plan_lds(g, 4, 1, p, true)) return true;
-    if (g.M <= 4 && plan_lds(g, 4, 1, p)) return true;
-    if (g.M <= 8 && plan_lds(g, 4, 2, p)) return true;
-    if (g.M <= 8 && plan_lds(g, 2, 1, p)) return true;
+    if (g.M <= 4 && plan_lds(g, 4, 1, p, false, true)) return true;
+    if (g.M <= 8 && plan_lds(g, 4, 2, p, false, true)) return true;
+    if (g.M <= 8 && plan_lds(g, 2, 1, p, false, true)) return true;
     if (g.M <= 16 && plan_lds(g, 1, 1, p)) return true;
     return false;
 }
@@ -743,7 +806,8 @@ hipError_t launch_lds_batched(const GemmArgs* gs, const LdsPlan* ps, int n, hipS
     int grid = 0, lds = 0;
     for (int i = 0; i < n; i++) {
         const GemmArgs& g = gs[i];
-        jobs.job[i] = LdsJob{g.W, g.Waux, g.A, g.C, g.lda, g.ldc, g.M, g.N, g.K, ps[i].nsub, ps[i].nslot, grid};
+        jobs.job[i] = LdsJob{g.W, g.Waux, g.A, g.C, g.lda, g.ldc, g.M, g.N, g.K, ps[i].nsub, ps[i].nslot,
+                             ps[i].na, grid};
         grid += ps[i].grid;
         lds = std::max(lds, ps[i].lds);
     }

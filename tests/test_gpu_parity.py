@@ -527,22 +527,22 @@ def test_gguf_tensors_feed_the_gemm(dev, tmp_path):
                 Ref(w, A).check(C, f"gguf {name} M={M}")
 
 
-@pytest.mark.parametrize("qt", [O.Q4_K, O.Q4_0], ids=lambda q: QT_NAME[q])
-@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408)])
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408), (600, 17408), (4096, 13824)])
 def test_lds_step_ring_parity(dev, qt, N, K):
     """Shapes whose steps do not all fit in LDS next to the activations (85
-    steps of 2,304 bytes per workgroup): the steps cycle through a ring of
-    slots, each reloaded once the compute wave that read it has released it,
-    instead of a second round of workgroups."""
+    steps of 2,304 bytes per workgroup at 5120 x 17408): the steps cycle through
+    a ring of slots, each reloaded once the compute wave that read it has
+    released it, instead of a second round of workgroups; from batch 3-5 on at
+    K = 17408 the activation segments do not fit either and cycle through a
+    ring of their own, the steps then taken segment by segment."""
     w = O.gen_weights(qt, N, K, seed=N + K + qt)
     dw = upload(w, dev)
     A = O.gen_act(8, K, seed=K + 3)
     ref = Ref(w, A)
-    for M in (1, 2, 4, 8):
-        try:
-            C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_LDS, dw=dw)
-        except bf.BusfillError:
-            assert M > 2 and K > 5120, f"LDS path refused N={N} K={K} M={M}"
-            continue
-        ref.check(C, f"ring {QT_NAME[qt]} N={N} K={K} M={M}", rows=M, form="f32" if qt == O.Q4_K or M == 1 else "f16")
+    for M in range(1, 9):
+        C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_LDS, dw=dw)
+        # batch 1 takes the sub-block rows form (fp32 scaling) when K is a multiple of 1024
+        bd = M == 1 and (K // 256) % 4 == 0
+        ref.check(C, f"ring {QT_NAME[qt]} N={N} K={K} M={M}", rows=M, form="f32" if qt == O.Q4_K or bd else "f16")
         assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_LDS, dw=dw) == C).all()
