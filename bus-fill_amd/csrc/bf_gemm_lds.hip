@@ -96,13 +96,14 @@ constexpr int kSegCount = 896;                    // steps done with activation 
 constexpr int kStepCounter = 15;                  // flags[15]: next step to take
 constexpr int kASlots = 6;                        // activation instructions per loader and segment
 constexpr int kMinRing = 16;                      // fewest steps in a ring of reused step slots
+constexpr int kRingAhead = 16;                    // steps of lead that keep the weight stream going
 
 // One GEMM's share of a launch: workgroup `bid` of its grid.
 template <int QT, int G, int MT, int NC, int NL, bool BD>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                          const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
-                                         int nslot, int na, const uint8_t* __restrict__ Waux, void* __restrict__ C,
-                                         int ldc, int out_f16) {
+                                         int nslot, int na, int win, const uint8_t* __restrict__ Waux,
+                                         void* __restrict__ C, int ldc, int out_f16) {
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     static_assert(!BD || G == 4, "sub-block rows: four K segments");
     // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
@@ -112,8 +113,27 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     const int nsg = K >> 8, nsteps = nsg / G;
     const int S = nsub * nsteps;                       // steps of the workgroup
     const int tile0 = bid * nsub;
-    // na < nsteps: activation ring, steps in segment-major order
-    const bool seg_major = na < nsteps;
+    // Step order: windows of Wn segments; in window w every sub-tile in turn
+    // takes the window's segments in order (Wn = nsteps: sub-tile-major; the
+    // last window may hold fewer, Wl).  na < nsteps: activation ring.
+    const int Wn = BD ? nsteps : win;
+    const int EW = nsub * Wn, nfull = nsteps / Wn, Wl = nsteps - nfull * Wn, E_full = nfull * EW;
+    const bool a_ring = na < nsteps;
+    // e / d as (e * inv) >> 16: exact for e < 240, d <= 240
+    const uint32_t inv_EW = (65536u + EW - 1u) / (uint32_t)EW, inv_W = (65536u + Wn - 1u) / (uint32_t)Wn;
+    const uint32_t inv_Wl = Wl ? (65536u + Wl - 1u) / (uint32_t)Wl : 0u;
+    // step e -> (sub-tile t, segment s)
+    auto step_ts = [&](int e, int& t, int& sg) {
+        if (e < E_full) {
+            const int w = (int)(((uint32_t)e * inv_EW) >> 16), e1 = e - w * EW;
+            t = (int)(((uint32_t)e1 * inv_W) >> 16);
+            sg = w * Wn + e1 - t * Wn;
+        } else {
+            const int e1 = e - E_full;
+            t = (int)(((uint32_t)e1 * inv_Wl) >> 16);
+            sg = nfull * Wn + e1 - t * Wl;
+        }
+    };
     const int seg_bytes = M * G * 528, a_bytes = na * seg_bytes;
     int* const flags = (int*)lds;
     uint8_t* const a_lds = lds + kFlagBytes;
@@ -187,25 +207,20 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             aon[q] = P < (uint32_t)PA && c < 32;
             asrc[q] = (const uint8_t*)(A + (int64_t)min((int)m, M - 1) * lda + 256 * gg + 8 * min((int)c, 31));
         }
-        // step e = te * nsteps + se (sub-tile-major) or se * nsub + te (segment-major)
-        int te = 0, se = 0;
-        if (seg_major) {
-            te = j;
-            while (te >= nsub) { te -= nsub; se++; }
-        } else {
-            se = j;
-            while (se >= nsteps) { se -= nsteps; te++; }
-        }
+        // the next activation segment to load, its window and place in it: its
+        // first step (sub-tile 0) is sw * EW + so
+        int s_next = 0, sw = 0, so = 0;
         for (int g4 = 0, e = j; 4 * g4 < S; g4++, e += 4) {
-            // the activation segments first needed by this group's steps (those of
-            // the first sub-tile: e < nsteps; segment-major: segments whose first
-            // step s * nsub is in the group), then this loader's step of the group
-            // (batch 1: the compute waves load A)
-            int s_lo = 4 * g4, s_hi = BD ? 0 : min(4 * g4 + 4, nsteps);
-            if (seg_major) {
-                s_lo = (4 * g4 + nsub - 1) / nsub;
-                s_hi = min((4 * g4 + 3) / nsub + 1, nsteps);
+            // the activation segments first needed by this group's steps, then this
+            // loader's step of the group (batch 1: the compute waves load A)
+            const int s_lo = s_next;
+            while (!BD && s_next < nsteps && sw * EW + so <= 4 * g4 + 3) {
+                s_next++;
+                if (++so == Wn) { so = 0; sw++; }
             }
+            const int s_hi = s_next;
+            int te = 0, se = 0;
+            step_ts(e, te, se);
             for (int s2 = s_lo; s2 < s_hi; s2++) {
                 // the segment's slot must be released by all nsub steps of its
                 // previous segment
@@ -247,13 +262,6 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             for (int s2 = s_lo; s2 < s_hi; s2++)
                 dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kAMark + 4 * s2 + j)), lane);
             if (e < S) dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kStepMark + e)), lane);
-            if (seg_major) {
-                te += 4;
-                while (te >= nsub) { te -= nsub; se++; }
-            } else {
-                se += 4;
-                while (se >= nsteps) { se -= nsteps; te++; }
-            }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         asm volatile("" :: "v"(warm));
@@ -392,10 +400,6 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int t = 0; t < 8; t++) abd[mt][t] = h8{};
-    // e / div as (e * inv) >> 16 (div = nsteps, or nsub segment-major): exact
-    // for e < 240, div <= 128
-    const uint32_t div = seg_major ? (uint32_t)nsub : (uint32_t)nsteps;
-    const uint32_t inv_div = (65536u + div - 1u) / div;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const int m = BD ? min(mt, M - 1) : min(mt * R + r / G, M - 1);   // padding rows reread row M-1
@@ -419,18 +423,16 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             e = __builtin_amdgcn_readfirstlane(e);
         }
         if (e >= S) break;
-        const int q_in = (int)(((uint32_t)e * inv_div) >> 16), r_in = e - q_in * (int)div;
-        const int t_in = seg_major ? r_in : q_in, s_in = seg_major ? q_in : r_in;
+        int t_in = 0, s_in = 0;
+        step_ts(e, t_in, s_in);
         if constexpr (!BD) {
             wait_flags(flags + kAMark + 4 * s_in, NL, lane);   // the step's activation segment
-            if constexpr (QT == QT_Q4_K) {
-                if (t_in == 0) {
-                    build_table(s_in * M * G * 4 + lane, (s_in + 1) * M * G * 4, 64);
-                    if (lane == 0)
-                        asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kTabFlag + s_in])), "v"(1) : "memory");
-                } else {
-                    wait_flag(&flags[kTabFlag + s_in]);
-                }
+            // the segment's block sums: tabulated by the wave of its first step;
+            // the others wait for them only after their codes' MFMAs
+            if (QT == QT_Q4_K && t_in == 0) {
+                build_table(s_in * M * G * 4 + lane, (s_in + 1) * M * G * 4, 64);
+                if (lane == 0)
+                    asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kTabFlag + s_in])), "v"(1) : "memory");
             }
         }
         Raw<QT> raw;
@@ -533,6 +535,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             }
             // sum_j m_j S_j: the mins {32m, m/64} of sub-blocks 2kg, 2kg+1 meet the
             // block sums {hi, lo} of the same sub-blocks (k slots 8kg .. 8kg+3)
+            if (t_in != 0) wait_flag(&flags[kTabFlag + s_in]);
             const h8 bm = __builtin_bit_cast(h8, u4{sk.min_hi, sk.min_lo, 0u, 0u});
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
@@ -555,7 +558,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         if constexpr (!BD) {
             // the step's activation reads are issued (a wave's LDS operations
             // complete in order): count it against its segment's slot
-            if (seg_major && lane == 0)
+            if (a_ring && lane == 0)
                 asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[kSegCount + s_in])), "v"(1) : "memory");
             // fold the G segments (lanes r = G*rowl + g) and park the partial sums
             // (slots in sub-tile-major order whatever the step order)
@@ -639,10 +642,11 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
 template <int QT, int G, int MT, int NC, int NL, bool BD>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
-                int nsub, int nslot, int na, const uint8_t* __restrict__ Waux, void* __restrict__ C, int ldc,
-                int out_f16) {
+                int nsub, int nslot, int na, int win, const uint8_t* __restrict__ Waux, void* __restrict__ C,
+                int ldc, int out_f16) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, Waux, C, ldc, out_f16);
+    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, win, Waux, C, ldc,
+                                    out_f16);
 }
 
 // Several independent GEMMs of one kernel shape in one launch (their grids
@@ -655,7 +659,7 @@ struct LdsJob {
     const uint8_t* Waux;
     const uint16_t* A;
     void* C;
-    int lda, ldc, M, N, K, nsub, nslot, na, grid0;
+    int lda, ldc, M, N, K, nsub, nslot, na, win, grid0;
 };
 struct LdsJobs {
     LdsJob job[kLdsMaxJobs];
@@ -671,15 +675,36 @@ void k_gemm_lds_batched(const LdsJobs jobs) {
     for (int i = 1; i < kLdsMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
     lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub, j.nslot,
-                                    j.na, j.Waux, j.C, j.ldc, jobs.out_f16);
+                                    j.na, j.win, j.Waux, j.C, j.ldc, jobs.out_f16);
 }
 
 constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 struct LdsPlan {
-    int G, MT, nsub, nslot, na, grid, lds;
+    int G, MT, nsub, nslot, na, win, grid, lds;
     bool BD;                           // sub-block rows form (Q4_K, one batch row per m-tile)
 };
+
+// Steps in windows of wn segments (each sub-tile in turn takes the window's
+// segments) with na activation slots: the fewest steps by which the loaders can
+// run ahead of the compute waves, or 0 when a loader would wait for a step of
+// its own group or a later one (deadlock) -- the slot of segment s is released
+// by the last step of segment s - na, and segment s is loaded in the group of
+// its first step.
+int ring_ahead(int nsteps, int nsub, int wn, int na) {
+    const int ew = nsub * wn;
+    auto first = [&](int sg) { return (sg / wn) * ew + sg % wn; };
+    auto last = [&](int sg) {
+        const int w = sg / wn, width = std::min(wn, nsteps - w * wn);
+        return w * ew + (nsub - 1) * width + sg % wn;
+    };
+    int ahead = 1 << 30;
+    for (int sg = na; sg < nsteps; sg++) {
+        if (last(sg - na) / 4 >= first(sg) / 4) return 0;
+        ahead = std::min(ahead, first(sg) - last(sg - na));
+    }
+    return ahead;
+}
 
 // Sub-tiles per workgroup: about one workgroup per CU when the LDS holds all of
 // its steps, otherwise the fewest rounds of 256 workgroups that fit.  With one
@@ -710,38 +735,44 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false, boo
             const int64_t f = base + na * seg;
             return f < kMaxLds ? (int)((kMaxLds - f) / kStep) & ~3 : 0;
         };
-        int na = nsteps, nslot = S;
+        int na = nsteps, nslot = S, win = nsteps;
         if (base + nsteps * seg + (int64_t)S * kStep > kMaxLds) {
             // a second round of workgroups costs more than a ring saves
             nslot = rounds == 1 ? ring(nsteps) : 0;
             if (nslot < kMinRing && rounds == 1 && aring && !BD) {
-                // both rings: the loaders run na * nsub steps at most ahead of the
-                // compute waves and nslot at most; the best of the two bounds.
-                // (na - 1) nsub >= 4: a segment's slot is released by steps of
-                // earlier groups of four (no loader waits for its own loads)
+                // both rings, steps in windows of wn segments (whole rows of
+                // 576 wn bytes per step run: wn = 4 when it keeps the loaders far
+                // enough ahead, else the farthest)
                 int best = 0;
-                for (int a = 2; a < nsteps; a++) {
-                    if ((a - 1) * nsub < 4) continue;
-                    const int rs = std::min(ring(a), S);
-                    if (rs < kMinRing && rs < S) continue;
-                    const int score = std::min(rs, a * nsub);
-                    if (score > best) {
-                        best = score;
-                        na = a;
-                        nslot = rs;
+                for (int wn : {4, 2, 1}) {
+                    if (wn > nsteps) continue;
+                    for (int a = wn + 1; a < nsteps; a++) {
+                        const int rs = std::min(ring(a), S);
+                        if (rs < kMinRing && rs < S) continue;
+                        const int ahead = ring_ahead(nsteps, nsub, wn, a);
+                        if (ahead <= 0) continue;
+                        const int score = std::min(rs, ahead);
+                        if (score > best) {
+                            best = score;
+                            na = a;
+                            nslot = rs;
+                            win = wn;
+                        }
                     }
+                    if (best >= kRingAhead) break;
                 }
                 if (best == 0) nslot = 0;
             }
             if (nslot < kMinRing && nslot < S) {
                 if (nsub == 1) return false;
-                na = nsteps;
+                na = win = nsteps;
                 continue;
             }
         }
         p.nsub = nsub;
         p.nslot = nslot;
         p.na = na;
+        p.win = win;
         p.grid = (T + nsub - 1) / nsub;
         p.lds = (int)(base + na * seg + (int64_t)nslot * kStep);
         return true;
@@ -763,7 +794,7 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
         attr_set.fetch_or(bit, std::memory_order_acq_rel);
     }
     hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kNC + kNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K, p.nsub,
-                       p.nslot, p.na, g.Waux, g.C, g.ldc, g.out_f16);
+                       p.nslot, p.na, p.win, g.Waux, g.C, g.ldc, g.out_f16);
     return hipGetLastError();
 }
 
@@ -807,7 +838,7 @@ hipError_t launch_lds_batched(const GemmArgs* gs, const LdsPlan* ps, int n, hipS
     for (int i = 0; i < n; i++) {
         const GemmArgs& g = gs[i];
         jobs.job[i] = LdsJob{g.W, g.Waux, g.A, g.C, g.lda, g.ldc, g.M, g.N, g.K, ps[i].nsub, ps[i].nslot,
-                             ps[i].na, grid};
+                             ps[i].na, ps[i].win, grid};
         grid += ps[i].grid;
         lds = std::max(lds, ps[i].lds);
     }
