@@ -98,8 +98,10 @@ constexpr int kASlots = 6;                        // activation instructions per
 constexpr int kMinRing = 16;                      // fewest steps in a ring of reused step slots
 constexpr int kRingAhead = 16;                    // steps of lead that keep the weight stream going
 
-// One GEMM's share of a launch: workgroup `bid` of its grid.
-template <int QT, int G, int MT, int NC, int NL, bool BD>
+// One GEMM's share of a launch: workgroup `bid` of its grid.  RG: steps in
+// windows of `win` segments and na activation slots (plans whose activations do
+// not all fit); otherwise sub-tile-major with all of A resident.
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                          const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
                                          int nslot, int na, int win, const uint8_t* __restrict__ Waux,
@@ -116,15 +118,21 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     // Step order: windows of Wn segments; in window w every sub-tile in turn
     // takes the window's segments in order (Wn = nsteps: sub-tile-major; the
     // last window may hold fewer, Wl).  na < nsteps: activation ring.
-    const int Wn = BD ? nsteps : win;
+    static_assert(!(BD && RG), "batch 1 keeps all of A");
+    const int Wn = RG ? win : nsteps;
     const int EW = nsub * Wn, nfull = nsteps / Wn, Wl = nsteps - nfull * Wn, E_full = nfull * EW;
-    const bool a_ring = na < nsteps;
+    const bool a_ring = RG && na < nsteps;
     // e / d as (e * inv) >> 16: exact for e < 240, d <= 240
     const uint32_t inv_EW = (65536u + EW - 1u) / (uint32_t)EW, inv_W = (65536u + Wn - 1u) / (uint32_t)Wn;
     const uint32_t inv_Wl = Wl ? (65536u + Wl - 1u) / (uint32_t)Wl : 0u;
+    const uint32_t inv_na = (65536u + na - 1u) / (uint32_t)na;
+    const uint32_t inv_nslot = (65536u + nslot - 1u) / (uint32_t)nslot;
     // step e -> (sub-tile t, segment s)
     auto step_ts = [&](int e, int& t, int& sg) {
-        if (e < E_full) {
+        if (!RG) {
+            t = (int)(((uint32_t)e * inv_W) >> 16);
+            sg = e - t * nsteps;
+        } else if (e < E_full) {
             const int w = (int)(((uint32_t)e * inv_EW) >> 16), e1 = e - w * EW;
             t = (int)(((uint32_t)e1 * inv_W) >> 16);
             sg = w * Wn + e1 - t * Wn;
@@ -135,6 +143,11 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         }
     };
     const int seg_bytes = M * G * 528, a_bytes = na * seg_bytes;
+    // activation segment s -> its byte offset (slot s mod na of the ring)
+    auto seg_off = [&](int sg) {
+        if (!RG) return sg * seg_bytes;
+        return (sg - (int)(((uint32_t)sg * inv_na) >> 16) * na) * seg_bytes;
+    };
     int* const flags = (int*)lds;
     uint8_t* const a_lds = lds + kFlagBytes;
     uint8_t* const w_lds = a_lds + a_bytes;            // ring of nslot steps (nslot = S: no reuse)
@@ -207,25 +220,32 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             aon[q] = P < (uint32_t)PA && c < 32;
             asrc[q] = (const uint8_t*)(A + (int64_t)min((int)m, M - 1) * lda + 256 * gg + 8 * min((int)c, 31));
         }
-        // the next activation segment to load, its window and place in it: its
-        // first step (sub-tile 0) is sw * EW + so
+        // RG: the next activation segment to load, its window and place in it
+        // (its first step, sub-tile 0, is sw * EW + so); otherwise the step
+        // e = te * nsteps + se
         int s_next = 0, sw = 0, so = 0;
+        int te = 0, se = j;
+        if (!RG)
+            while (se >= nsteps) { se -= nsteps; te++; }
         for (int g4 = 0, e = j; 4 * g4 < S; g4++, e += 4) {
-            // the activation segments first needed by this group's steps, then this
-            // loader's step of the group (batch 1: the compute waves load A)
-            const int s_lo = s_next;
-            while (!BD && s_next < nsteps && sw * EW + so <= 4 * g4 + 3) {
-                s_next++;
-                if (++so == Wn) { so = 0; sw++; }
+            // the activation segments first needed by this group's steps (RG:
+            // scanned; otherwise those of the first sub-tile, e < nsteps), then
+            // this loader's step of the group (batch 1: the compute waves load A)
+            int s_lo = 4 * g4, s_hi = BD ? 0 : min(4 * g4 + 4, nsteps);
+            if (RG) {
+                s_lo = s_next;
+                while (s_next < nsteps && sw * EW + so <= 4 * g4 + 3) {
+                    s_next++;
+                    if (++so == Wn) { so = 0; sw++; }
+                }
+                s_hi = s_next;
+                step_ts(e, te, se);
             }
-            const int s_hi = s_next;
-            int te = 0, se = 0;
-            step_ts(e, te, se);
             for (int s2 = s_lo; s2 < s_hi; s2++) {
                 // the segment's slot must be released by all nsub steps of its
                 // previous segment
-                if (s2 >= na) wait_flag_value(&flags[kSegCount + s2 - na], nsub);
-                const uint32_t dst = lds0 + (uint32_t)(kFlagBytes + (s2 % na) * seg_bytes);
+                if (RG && s2 >= na) wait_flag_value(&flags[kSegCount + s2 - na], nsub);
+                const uint32_t dst = lds0 + (uint32_t)(kFlagBytes + seg_off(s2));
 #pragma unroll
                 for (int q = 0; q < kASlots; q++) {
                     const int qa = j + 4 * q;
@@ -262,6 +282,10 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             for (int s2 = s_lo; s2 < s_hi; s2++)
                 dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kAMark + 4 * s2 + j)), lane);
             if (e < S) dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kStepMark + e)), lane);
+            if (!RG) {
+                se += 4;
+                while (se >= nsteps) { se -= nsteps; te++; }
+            }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         asm volatile("" :: "v"(warm));
@@ -313,7 +337,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         for (int u = u0; u < u_end; u += ustep) {
             const int kq = u & 3, rest = u >> 2, s_seg = rest / (M * G), mg4 = rest - s_seg * (M * G);
             const int m = mg4 / G, gg = mg4 - m * G;
-            uint8_t* src = a_lds + (s_seg % na) * seg_bytes + (m * G + gg) * 528 + 128 * kq;
+            uint8_t* src = a_lds + seg_off(s_seg) + (m * G + gg) * 528 + 128 * kq;
             u4 v[8];
 #pragma unroll
             for (int q = 0; q < 8; q++) v[q] = *(const u4*)(src + 16 * q);
@@ -426,17 +450,30 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         int t_in = 0, s_in = 0;
         step_ts(e, t_in, s_in);
         if constexpr (!BD) {
-            wait_flags(flags + kAMark + 4 * s_in, NL, lane);   // the step's activation segment
-            // the segment's block sums: tabulated by the wave of its first step;
-            // the others wait for them only after their codes' MFMAs
+            // the segment's block sums: tabulated by the wave of its first step
+            // once the segment has landed
+            // The step's flags in one LDS round trip (lanes 0-3 its segment's
+            // activation markers, lane 4 its own marker, lane 5 for Q4_K the
+            // segment's block-sum flag), or one after the other: Q4_K with two
+            // m-tiles or the rings measured faster with three round trips.
+            constexpr bool kMerged = !(QT == QT_Q4_K && (MT == 2 || RG));
+            if (!kMerged || (QT == QT_Q4_K && t_in == 0)) wait_flags(flags + kAMark + 4 * s_in, NL, lane);
             if (QT == QT_Q4_K && t_in == 0) {
                 build_table(s_in * M * G * 4 + lane, (s_in + 1) * M * G * 4, 64);
                 if (lane == 0)
                     asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kTabFlag + s_in])), "v"(1) : "memory");
             }
+            if (kMerged) {
+                const int* f = lane < NL ? flags + kAMark + 4 * s_in + lane
+                                         : lane == NL ? flags + kStepMark + e : flags + kTabFlag + s_in;
+                wait_lanes(f, lane <= NL || (QT == QT_Q4_K && lane == NL + 1));
+            } else {
+                if (t_in != 0) wait_flag(&flags[kTabFlag + s_in]);
+                wait_flag(&flags[kStepMark + e]);
+            }
         }
         Raw<QT> raw;
-        const uint8_t* const aseg = a_lds + (s_in % na) * seg_bytes;
+        const uint8_t* const aseg = a_lds + seg_off(s_in);
         if constexpr (BD) {
             // the step's marker with the step's weight and activation reads right
             // behind it: a wave's LDS reads complete in order, so a nonzero marker
@@ -444,7 +481,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             for (int it = 0;; it++) {
                 int mark;
                 asm volatile("ds_read_b32 %0, %1" : "=v"(mark) : "v"(lds_addr(&flags[kStepMark + e])) : "memory");
-                lds_raw<QT>(raw, w_lds + (e % nslot) * kStep + r * 144, kg);
+                lds_raw<QT>(raw, w_lds + (e - (int)(((uint32_t)e * inv_nslot) >> 16) * nslot) * kStep + r * 144, kg);
                 if (bd_on) {
 #pragma unroll
                     for (int mt = 0; mt < MT; mt++)
@@ -458,8 +495,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             // the step's slot is free again (its reads have completed)
             if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kStepMark + e])), "v"(2) : "memory");
         } else {
-            wait_flag(&flags[kStepMark + e]);
-            lds_raw<QT>(raw, w_lds + (e % nslot) * kStep + r * 144, kg);
+            lds_raw<QT>(raw, w_lds + (e - (int)(((uint32_t)e * inv_nslot) >> 16) * nslot) * kStep + r * 144, kg);
             // a wave's LDS operations complete in order: the slot is free once this
             // write is visible
             if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kStepMark + e])), "v"(2) : "memory");
@@ -535,7 +571,6 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             }
             // sum_j m_j S_j: the mins {32m, m/64} of sub-blocks 2kg, 2kg+1 meet the
             // block sums {hi, lo} of the same sub-blocks (k slots 8kg .. 8kg+3)
-            if (t_in != 0) wait_flag(&flags[kTabFlag + s_in]);
             const h8 bm = __builtin_bit_cast(h8, u4{sk.min_hi, sk.min_lo, 0u, 0u});
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
@@ -639,13 +674,13 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     }
 }
 
-template <int QT, int G, int MT, int NC, int NL, bool BD>
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
                 int nsub, int nslot, int na, int win, const uint8_t* __restrict__ Waux, void* __restrict__ C,
                 int ldc, int out_f16) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, win, Waux, C, ldc,
+    lds_body<QT, G, MT, NC, NL, BD, RG>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, win, Waux, C, ldc,
                                     out_f16);
 }
 
@@ -666,7 +701,7 @@ struct LdsJobs {
     int n, out_f16;
 };
 
-template <int QT, int G, int MT, int NC, int NL, bool BD>
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds_batched(const LdsJobs jobs) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
@@ -674,7 +709,7 @@ void k_gemm_lds_batched(const LdsJobs jobs) {
 #pragma unroll
     for (int i = 1; i < kLdsMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
-    lds_body<QT, G, MT, NC, NL, BD>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub, j.nslot,
+    lds_body<QT, G, MT, NC, NL, BD, RG>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub, j.nslot,
                                     j.na, j.win, j.Waux, j.C, j.ldc, jobs.out_f16);
 }
 
@@ -682,6 +717,7 @@ constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 struct LdsPlan {
     int G, MT, nsub, nslot, na, win, grid, lds;
+    bool RG;                           // window order and activation ring (win or na < steps per sub-tile)
     bool BD;                           // sub-block rows form (Q4_K, one batch row per m-tile)
 };
 
@@ -773,6 +809,7 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false, boo
         p.nslot = nslot;
         p.na = na;
         p.win = win;
+        p.RG = na < nsteps || win < nsteps;
         p.grid = (T + nsub - 1) / nsub;
         p.lds = (int)(base + na * seg + (int64_t)nslot * kStep);
         return true;
@@ -780,9 +817,9 @@ bool plan_lds(const GemmArgs& g, int G, int MT, LdsPlan& p, bool BD = false, boo
     return false;
 }
 
-template <int QT, int G, int MT, bool BD = false>
+template <int QT, int G, int MT, bool BD = false, bool RG = false>
 hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
-    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD>;
+    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -801,6 +838,12 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
 template <int QT>
 hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
     if (p.BD) return launch_lds<QT, 4, 1, true>(g, p, st);
+    if (p.RG) {
+        if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1, false, true>(g, p, st);
+        if (p.G == 4 && p.MT == 2) return launch_lds<QT, 4, 2, false, true>(g, p, st);
+        if (p.G == 2 && p.MT == 1) return launch_lds<QT, 2, 1, false, true>(g, p, st);
+        return hipErrorInvalidValue;                    // no ring kernel of this shape
+    }
     if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1>(g, p, st);
     if (p.G == 4 && p.MT == 2) return launch_lds<QT, 4, 2>(g, p, st);
     if (p.G == 2 && p.MT == 1) return launch_lds<QT, 2, 1>(g, p, st);
@@ -818,9 +861,9 @@ bool choose_lds(const GemmArgs& g, LdsPlan& p) {
     return false;
 }
 
-template <int QT, int G, int MT, bool BD>
+template <int QT, int G, int MT, bool BD, bool RG>
 hipError_t launch_lds_batched(const GemmArgs* gs, const LdsPlan* ps, int n, hipStream_t st) {
-    auto k = k_gemm_lds_batched<QT, G, MT, kNC, kNL, BD>;
+    auto k = k_gemm_lds_batched<QT, G, MT, kNC, kNL, BD, RG>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -852,9 +895,13 @@ bool lds_batchable(const LdsPlan& p) { return p.G == 4 && (p.BD || p.MT <= 2); }
 
 template <int QT>
 hipError_t dispatch_lds_batched(const GemmArgs* gs, const LdsPlan* ps, int n, hipStream_t st) {
-    if (ps[0].BD) return launch_lds_batched<QT, 4, 1, true>(gs, ps, n, st);
-    if (ps[0].MT == 1) return launch_lds_batched<QT, 4, 1, false>(gs, ps, n, st);
-    return launch_lds_batched<QT, 4, 2, false>(gs, ps, n, st);
+    if (ps[0].BD) return launch_lds_batched<QT, 4, 1, true, false>(gs, ps, n, st);
+    if (ps[0].RG) {
+        if (ps[0].MT == 1) return launch_lds_batched<QT, 4, 1, false, true>(gs, ps, n, st);
+        return launch_lds_batched<QT, 4, 2, false, true>(gs, ps, n, st);
+    }
+    if (ps[0].MT == 1) return launch_lds_batched<QT, 4, 1, false, false>(gs, ps, n, st);
+    return launch_lds_batched<QT, 4, 2, false, false>(gs, ps, n, st);
 }
 
 }  // namespace
@@ -868,7 +915,7 @@ bool lds_batched_supports(const GemmArgs* gs, int n) {
         if (gs[i].qtype == QT_PLANES && ((uintptr_t)gs[i].Waux & 15)) return false;
         if (!choose_lds(gs[i], p) || !lds_batchable(p)) return false;
         if (i == 0) p0 = p;
-        else if (p.G != p0.G || p.MT != p0.MT || p.BD != p0.BD) return false;
+        else if (p.G != p0.G || p.MT != p0.MT || p.BD != p0.BD || p.RG != p0.RG) return false;
     }
     return true;
 }

@@ -125,6 +125,18 @@ __device__ __forceinline__ void wait_flags(const int* flags, int n, int lane, in
     }
 }
 
+// Spin until the LDS word each lane names is nonzero in every lane with
+// `need`: one LDS read per round for up to 64 flags anywhere in LDS.
+__device__ __forceinline__ void wait_lanes(const int* flag, bool need) {
+    const uint32_t a = lds_addr(flag);
+    for (int it = 0; it < (1 << 20); it++) {
+        int v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+        if (__builtin_amdgcn_ballot_w64(need && v == 0) == 0) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // Sets the LDS word at `flag` to 1 once every load this wave has issued has
 // completed; for direct-to-LDS loads completion includes the LDS write.
 __device__ __forceinline__ void signal_own_loads(int* flag, int lane) {
