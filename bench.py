@@ -100,9 +100,11 @@ def bench_lib():
     L.bfb_time_sequence.argtypes = [i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, d]
     L.bfb_time_sequence_batched.argtypes = [i, i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, vp, d]
     L.bfb_read_peak.argtypes = [vp, ctypes.c_size_t, i, vp, vp, d]
+    L.bfb_read_slices.argtypes = [vp, i, ctypes.c_size_t, i, i, i, i, vp, vp, d]
     L.bfb_copy.argtypes = [vp, vp, ctypes.c_size_t, i, vp, d]
     L.bfb_last_error.restype = ctypes.c_char_p
-    for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_time_sequence_batched", "bfb_read_peak", "bfb_copy"):
+    for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_time_sequence_batched", "bfb_read_peak", "bfb_read_slices",
+              "bfb_copy"):
         getattr(L, f).restype = i
     return L
 
@@ -167,6 +169,30 @@ def read_peak(L, rot):
     if rc != 0:
         raise RuntimeError("bench host: " + L.bfb_last_error().decode())
     return 5 * nbytes / (ms.value / 1e3) / 1e9
+
+
+READ_GRIDS = ((256, 1024), (512, 512), (1024, 256), (2048, 256), (4096, 256))
+
+
+def read_floor(L, rot, steps, warmup):
+    """A plain streaming read of one matrix's bytes per launch, cycling through
+    the rotation like the GEMM: the time a launch of that size needs to read
+    its bytes with no other work (best of a few grid shapes)."""
+    import torch
+    sink = torch.zeros(1, dtype=torch.int32, device=rot.W.device)
+    W, _ = rot.ptr_arrays()
+    best_us, best_grid = None, None
+    for blocks, threads in READ_GRIDS:
+        ms = ctypes.c_double()
+        rc = L.bfb_read_slices(P(W), rot.count, rot.wbytes // 16 * 16, blocks, threads, warmup, steps,
+                               sink.data_ptr(), stream_handle(), ctypes.byref(ms))
+        if rc != 0:
+            raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+        us = ms.value * 1e3 / steps
+        if best_us is None or us < best_us:
+            best_us, best_grid = us, (blocks, threads)
+    return {"us_per_launch": round(best_us, 4), "GBps": round(rot.wbytes / (best_us / 1e6) / 1e9, 1),
+            "bytes": rot.wbytes, "grid": list(best_grid)}
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -241,6 +267,9 @@ def run_gemm_workload(L, fmt, N, K, batches, args, dev):
             recs.append(r)
     peak = read_peak(L, rot)
     log(f"[bench] streaming-read over the rotation buffer: {peak:.1f} GB/s")
+    rot.floor = read_floor(L, rot, args.steps, args.warmup)
+    log(f"[bench] streaming-read of one matrix's {rot.wbytes} bytes per launch: {rot.floor['us_per_launch']:.3f} us "
+        f"({rot.floor['GBps']:.1f} GB/s, grid {rot.floor['grid']})")
     return rot, recs, peak
 
 
@@ -391,6 +420,7 @@ def main():
             "per_batch": [best(recs, M) for M in batches],
             "all_runs": recs,
             "hbm_read_measured_GBps": round(peak, 1),
+            "same_bytes_read_per_launch": rot.floor,
             "roofline": {"bound": "hbm", "achieved": round(alg_bytes / t / 1e9, 2), "peak": HBM_PEAK_GBPS,
                          "unit": "GB/s", "frac": round(alg_bytes / t / 1e9 / HBM_PEAK_GBPS, 4),
                          "traffic": traffic_from_profiles(f"{fmt}_5120_m{head['M']}"),

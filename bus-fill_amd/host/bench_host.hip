@@ -125,7 +125,7 @@ int time_seq(const std::vector<Launch>& seq, int otype, int algo, int warmup, in
     return 0;
 }
 
-__global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ src, size_t n16,
+__global__ __launch_bounds__(1024) void k_stream_read(const uint4* __restrict__ src, size_t n16,
                                                      unsigned* __restrict__ sink) {
     unsigned acc = 0;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x) {
@@ -195,6 +195,39 @@ int bfb_read_peak(const void* src, size_t bytes, int reps, void* sink, void* str
     HCK(hipEventRecord(e0, st));
     for (int r = 0; r < reps; r++)
         hipLaunchKernelGGL(k_stream_read, dim3(2048), dim3(256), 0, st, (const uint4*)src, n16, (unsigned*)sink);
+    HCK(hipGetLastError());
+    HCK(hipEventRecord(e1, st));
+    HCK(hipEventSynchronize(e1));
+    float ms;
+    HCK(hipEventElapsedTime(&ms, e0, e1));
+    *ms_out = ms;
+    HCK(hipEventDestroy(e0));
+    HCK(hipEventDestroy(e1));
+    return 0;
+}
+
+// Streaming reads of `bytes` per launch cycling through `count` buffers src[i]
+// (the weight rotation): the time one launch of that size takes to read its
+// bytes from HBM with nothing else to do.  Grid blocks x threads.
+int bfb_read_slices(const void* const* src, int count, size_t bytes, int blocks, int threads, int warmup,
+                    int steps, void* sink, void* stream, double* ms_out) {
+    hipStream_t st = (hipStream_t)stream;
+    const size_t n16 = bytes / 16;
+    if (count < 1 || blocks < 1 || threads < 64 || threads > 1024 || threads % 64) {
+        g_err = hipErrorInvalidValue;
+        return -1;
+    }
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    for (int r = 0; r < warmup; r++)
+        hipLaunchKernelGGL(k_stream_read, dim3(blocks), dim3(threads), 0, st, (const uint4*)src[r % count], n16,
+                           (unsigned*)sink);
+    HCK(hipGetLastError());
+    HCK(hipEventRecord(e0, st));
+    for (int r = 0; r < steps; r++)
+        hipLaunchKernelGGL(k_stream_read, dim3(blocks), dim3(threads), 0, st, (const uint4*)src[r % count], n16,
+                           (unsigned*)sink);
     HCK(hipGetLastError());
     HCK(hipEventRecord(e1, st));
     HCK(hipEventSynchronize(e1));
