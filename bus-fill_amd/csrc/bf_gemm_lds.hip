@@ -896,7 +896,11 @@ bool lds_batchable(const LdsPlan& p) { return p.G == 4 && (p.BD || p.MT <= 2); }
 template <int QT>
 hipError_t dispatch_lds_batched(const GemmArgs* gs, const LdsPlan* ps, int n, hipStream_t st) {
     if (ps[0].BD) return launch_lds_batched<QT, 4, 1, true, false>(gs, ps, n, st);
-    if (ps[0].RG) {
+    // one job with the rings: all take the ring kernel (which runs the others'
+    // plans, win = na = all segments, in the plain order)
+    bool rg = false;
+    for (int i = 0; i < n; i++) rg = rg || ps[i].RG;
+    if (rg) {
         if (ps[0].MT == 1) return launch_lds_batched<QT, 4, 1, false, true>(gs, ps, n, st);
         return launch_lds_batched<QT, 4, 2, false, true>(gs, ps, n, st);
     }
@@ -915,7 +919,7 @@ bool lds_batched_supports(const GemmArgs* gs, int n) {
         if (gs[i].qtype == QT_PLANES && ((uintptr_t)gs[i].Waux & 15)) return false;
         if (!choose_lds(gs[i], p) || !lds_batchable(p)) return false;
         if (i == 0) p0 = p;
-        else if (p.G != p0.G || p.MT != p0.MT || p.BD != p0.BD || p.RG != p0.RG) return false;
+        else if (p.G != p0.G || p.MT != p0.MT || p.BD != p0.BD) return false;
     }
     return true;
 }
