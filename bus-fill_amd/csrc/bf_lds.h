@@ -4,13 +4,12 @@
 #pragma once
 
 #include "bf_formats.h"
+#include "bf_lds_plan.h"
 
 namespace bf {
 namespace {
 
-constexpr int kStep = 16 * 144;          // bytes of one step
 constexpr int kASg = 528;                // LDS bytes of one super-group of one activation row (512 + 16)
-constexpr int kMaxLds = 160 * 1024;      // LDS per workgroup on gfx950
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
