@@ -546,3 +546,37 @@ def test_lds_step_ring_parity(dev, qt, N, K):
         bd = M == 1 and (K // 256) % 4 == 0
         ref.check(C, f"ring {QT_NAME[qt]} N={N} K={K} M={M}", rows=M, form="f32" if qt == O.Q4_K or bd else "f16")
         assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_LDS, dw=dw) == C).all()
+
+
+def random_case(seed):
+    """A seeded shape: format, batch rows, rows and K (multiples of 256, often
+    large enough that the LDS-staged kernel needs its step and activation rings)."""
+    rng = np.random.default_rng(1000 + seed)
+    qt = QTS[seed % 3]
+    K = int(rng.choice([256 * int(rng.integers(1, 40)), 13824, 17408, 24576, 27648]))
+    N = int(rng.integers(1, 2600))
+    M = int(rng.integers(1, 17)) if seed % 4 else int(rng.integers(17, 41))
+    return qt, M, N, K
+
+
+@pytest.mark.parametrize("seed", range(24), ids=lambda s: f"case{s}")
+def test_random_shapes_every_kernel(dev, seed):
+    """Seeded random shapes through every kernel that takes them (automatic
+    choice, LDS-staged, K-split), each within the oracle's bounds and
+    reproducible bit for bit."""
+    qt, M, N, K = random_case(seed)
+    w = O.gen_weights(qt, N, K, seed=seed)
+    dw = upload(w, dev)
+    A = O.gen_act(M, K, seed=seed + 77)
+    ref = Ref(w, A)
+    ran = 0
+    for algo in (bf.ALGO_AUTO, bf.ALGO_LDS, bf.ALGO_SPLIT):
+        try:
+            C = gpu_gemm(w, A, dev, algo=algo, dw=dw)
+        except bf.BusfillError:
+            assert algo != bf.ALGO_AUTO
+            continue
+        ran += 1
+        ref.check(C, f"{QT_NAME[qt]} M={M} N={N} K={K} algo={algo}")
+        assert (gpu_gemm(w, A, dev, algo=algo, dw=dw) == C).all()
+    assert ran >= 1
