@@ -56,7 +56,9 @@ typedef enum {
     BF_ALGO_MFMA = 1,    /* v_mfma_f32_16x16x32_f16 over 16-row batch tiles            */
     BF_ALGO_DOT2 = 2,    /* v_dot2_f32_f16 lanes + cross-lane reduction (small M)      */
     BF_ALGO_SIMPLE = 3,  /* one thread per output; any legal shape (slow, for odd K)   */
-    BF_ALGO_LDS = 4,     /* direct-to-LDS staged weights + MFMA (M <= 16, A fits in LDS) */
+    BF_ALGO_LDS = 4,     /* direct-to-LDS staged weights + MFMA (M <= 8; M <= 16 when A
+                            fits in LDS; weight steps and A segments cycle through
+                            rings when they do not fit)                               */
     BF_ALGO_SLAB = 5,    /* weights and activation slabs through an LDS ring (M <= 32) */
     BF_ALGO_SPLIT = 6    /* K split over workgroups, all operands resident in LDS (M <= 32);
                             uses a per-stream workspace allocated on first use          */
