@@ -76,8 +76,9 @@ namespace {
 
 // One GEMM's share of a launch: workgroup `bid` of its grid.  RG: steps in
 // windows of `win` segments and na activation slots (plans whose activations do
-// not all fit); otherwise sub-tile-major with all of A resident.
-template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG>
+// not all fit); otherwise sub-tile-major with all of A resident.  AC: the
+// compute waves load all of A before the barrier (small A).
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                          const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
                                          int nslot, int na, int win, const uint8_t* __restrict__ Waux,
@@ -207,7 +208,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             // the activation segments first needed by this group's steps (RG:
             // scanned; otherwise those of the first sub-tile, e < nsteps), then
             // this loader's step of the group (batch 1: the compute waves load A)
-            int s_lo = 4 * g4, s_hi = BD ? 0 : min(4 * g4 + 4, nsteps);
+            int s_lo = 4 * g4, s_hi = BD || AC ? 0 : min(4 * g4 + 4, nsteps);
             if (RG) {
                 s_lo = s_next;
                 while (s_next < nsteps && sw * EW + so <= 4 * g4 + 3) {
@@ -298,6 +299,23 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             const int P = 64 * i + lane;
             const int sg = min(P / 33, nsg - 1), c = min(P - 33 * (P / 33), 31);
             if (P < nsg * 33) dma16(A + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + 1024 * i));
+        }
+        clear_flags_and_meet();
+        signal_own_loads(&flags[cw], lane);
+        wait_flags(flags, NC, lane);
+    } else if constexpr (AC) {
+        // small A, all of it resident: the compute waves load it (instruction
+        // f = s * IA + i: piece 64 i + lane of segment s; wave c issues c, c + NC,
+        // ...) so that the loaders stream weights only, then wait for all of it
+        const int cw = wave - NL;
+        const int PA = M * G * 33, IA = (PA + 63) >> 6;
+        for (int f = cw; f < nsteps * IA; f += NC) {
+            const int sg = f / IA, i = f - sg * IA;
+            const uint32_t P = 64u * i + lane;
+            const uint32_t m = P / (33u * G), rem = P - 33u * G * m, gg = rem / 33u, c = rem - 33u * gg;
+            const uint8_t* src =
+                (const uint8_t*)(A + (int64_t)min((int)m, M - 1) * lda + 256 * (G * sg + gg) + 8 * min((int)c, 31));
+            if (P < (uint32_t)PA && c < 32) dma16(src, lds0 + (uint32_t)(kFlagBytes + sg * seg_bytes + (i << 10)));
         }
         clear_flags_and_meet();
         signal_own_loads(&flags[cw], lane);
@@ -433,7 +451,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             // segment's block-sum flag), or one after the other: Q4_K with two
             // m-tiles or the rings measured faster with three round trips.
             constexpr bool kMerged = !(QT == QT_Q4_K && (MT == 2 || RG));
-            if (!kMerged || (QT == QT_Q4_K && t_in == 0)) wait_flags(flags + kAMark + 4 * s_in, NL, lane);
+            if (!AC && (!kMerged || (QT == QT_Q4_K && t_in == 0))) wait_flags(flags + kAMark + 4 * s_in, NL, lane);
             if (QT == QT_Q4_K && t_in == 0) {
                 build_table(s_in * M * G * 4 + lane, (s_in + 1) * M * G * 4, 64);
                 if (lane == 0)
@@ -442,7 +460,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             if (kMerged) {
                 const int* f = lane < NL ? flags + kAMark + 4 * s_in + lane
                                          : lane == NL ? flags + kStepMark + e : flags + kTabFlag + s_in;
-                wait_lanes(f, lane <= NL || (QT == QT_Q4_K && lane == NL + 1));
+                wait_lanes(f, (lane <= NL && (!AC || lane == NL)) || (QT == QT_Q4_K && lane == NL + 1));
             } else {
                 if (t_in != 0) wait_flag(&flags[kTabFlag + s_in]);
                 wait_flag(&flags[kStepMark + e]);
@@ -650,13 +668,13 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     }
 }
 
-template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG>
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC = false>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
                 int nsub, int nslot, int na, int win, const uint8_t* __restrict__ Waux, void* __restrict__ C,
                 int ldc, int out_f16) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    lds_body<QT, G, MT, NC, NL, BD, RG>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, win, Waux, C, ldc,
+    lds_body<QT, G, MT, NC, NL, BD, RG, AC>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, win, Waux, C, ldc,
                                     out_f16);
 }
 
@@ -685,7 +703,7 @@ void k_gemm_lds_batched(const LdsJobs jobs) {
 #pragma unroll
     for (int i = 1; i < kLdsMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
-    lds_body<QT, G, MT, NC, NL, BD, RG>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub, j.nslot,
+    lds_body<QT, G, MT, NC, NL, BD, RG, false>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub, j.nslot,
                                     j.na, j.win, j.Waux, j.C, j.ldc, jobs.out_f16);
 }
 
@@ -693,9 +711,9 @@ constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 LdsShape lds_shape(const GemmArgs& g) { return LdsShape{g.M, g.N, g.K, g.qtype == QT_Q4_K}; }
 
-template <int QT, int G, int MT, bool BD = false, bool RG = false>
+template <int QT, int G, int MT, bool BD = false, bool RG = false, bool AC = false>
 hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
-    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG>;
+    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG, AC>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -720,6 +738,7 @@ hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
         if (p.G == 2 && p.MT == 1) return launch_lds<QT, 2, 1, false, true>(g, p, st);
         return hipErrorInvalidValue;                    // no ring kernel of this shape
     }
+    if (p.AC) return launch_lds<QT, 4, 1, false, false, true>(g, p, st);
     if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1>(g, p, st);
     if (p.G == 4 && p.MT == 2) return launch_lds<QT, 4, 2>(g, p, st);
     if (p.G == 2 && p.MT == 1) return launch_lds<QT, 2, 1>(g, p, st);

@@ -38,6 +38,7 @@ inline constexpr int kStepCounter = 15;                  // flags[15]: next step
 inline constexpr int kASlots = 6;                        // activation instructions per loader and segment
 inline constexpr int kMinRing = 16;                      // fewest steps in a ring of reused step slots
 inline constexpr int kRingAhead = 16;                    // steps of lead that keep the weight stream going
+inline constexpr int kAcMaxBytes = 20480;                // A per workgroup that the compute waves load (AC)
 
 // A GEMM as the planner sees it.
 struct LdsShape {
@@ -48,6 +49,7 @@ struct LdsShape {
 struct LdsPlan {
     int G, MT, nsub, nslot, na, win, grid, lds;
     bool RG;                           // window order and activation ring (win or na < steps per sub-tile)
+    bool AC;                           // the compute waves load all of A up front (loaders: weights only)
     bool BD;                           // sub-block rows form (Q4_K, one batch row per m-tile)
 };
 
@@ -140,6 +142,10 @@ inline bool plan_lds(const LdsShape& g, int G, int MT, LdsPlan& p, bool BD = fal
         p.na = na;
         p.win = win;
         p.RG = na < nsteps || win < nsteps;
+        // small A (batch 2 at K = 5120): loaded by the compute waves before the
+        // barrier, as at batch 1, so that the loaders' weight stream starts alone
+        // (measured faster there; from about 40 KB on, slower)
+        p.AC = !BD && !p.RG && G == 4 && MT == 1 && (int64_t)g.M * g.K * 2 <= kAcMaxBytes;
         p.grid = (T + nsub - 1) / nsub;
         p.lds = (int)(base + na * seg + (int64_t)nslot * kStep);
         return true;

@@ -17,6 +17,8 @@
 //     release the step, compute, count the step against its segment (ring) and
 //     sub-tile; the last of a sub-tile reduces it (batch 1: the wave that took
 //     the sub-tile's last step, after its own steps).
+//   AC plans (small A): the compute waves load all of A before the barrier and
+//     wait for it (no dependence on the loaders), the loaders stream weights only.
 // Exit status 0 and a summary line on success; the first violation otherwise.
 // With --self-test it instead runs the model on plans with planted mistakes (an
 // activation ring too small for the loaders' lead, a step ring that is not
@@ -129,6 +131,13 @@ struct Model {
         aslot.assign(p.na, -1);
         for (int j = 0; j < kNL; j++) L.push_back(Loader{j});
         for (int c = 0; c < kNC; c++) W.push_back(Wave{c});
+        if (p.AC) {
+            if (p.na != nsteps || p.RG || p.BD) fail("AC plan without all of A resident", g, p);
+            for (int sg = 0; sg < nsteps; sg++) {
+                aslot[sg] = sg;
+                for (int j = 0; j < kNL; j++) amark[sg * kNL + j] = 1;
+            }
+        }
     }
     int wslot_of(int e) const { return ((e >> 2) % G4R) * 4 + (e & 3); }
 
@@ -146,7 +155,7 @@ struct Model {
                     l.s_hi = l.s_next;
                 } else {
                     l.s_lo = 4 * l.g4;
-                    l.s_hi = p.BD ? 0 : std::min(4 * l.g4 + 4, nsteps);
+                    l.s_hi = p.BD || p.AC ? l.s_lo : std::min(4 * l.g4 + 4, nsteps);
                 }
                 l.s2 = l.s_lo;
                 l.phase = 1;
@@ -381,7 +390,7 @@ int main(int argc, char** argv) {
     if (argc > 1 && std::strcmp(argv[1], "--self-test") == 0) return self_test();
     const int Ns[] = {1, 77, 512, 600, 1024, 3072, 4096, 5120, 7168, 13824, 17408, 27648};
     const int Ks[] = {256, 1024, 2048, 3072, 4096, 5120, 8192, 13824, 17408, 24576, 27648};
-    int plans = 0, rings = 0, aring = 0, runs = 0;
+    int plans = 0, rings = 0, aring = 0, ac = 0, runs = 0;
     for (int q = 0; q < 2; q++)
         for (int M = 1; M <= 16; M++)
             for (int N : Ns)
@@ -396,6 +405,7 @@ int main(int argc, char** argv) {
                     const bool ring = p.nslot < p.nsub * nsteps;
                     rings += ring;
                     aring += p.RG;
+                    ac += p.AC;
                     // the model runs each shape's first workgroup: every workgroup runs
                     // the same protocol on its own rows
                     const int seeds = ring || p.RG ? 3 : 1;
@@ -410,7 +420,7 @@ int main(int argc, char** argv) {
                         return 1;
                     }
                 }
-    std::printf("ok: %d plans (%d with a step ring, %d with windows / activation ring), %d model runs\n", plans,
-                rings, aring, runs);
+    std::printf("ok: %d plans (%d with a step ring, %d with windows / activation ring), %d model runs, %d AC\n",
+                plans, rings, aring, runs, ac);
     return 0;
 }
