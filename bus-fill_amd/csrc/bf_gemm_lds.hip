@@ -205,9 +205,11 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         if (!RG)
             while (se >= nsteps) { se -= nsteps; te++; }
         for (int g4 = 0, e = j; 4 * g4 < S; g4++, e += 4) {
-            // the activation segments first needed by this group's steps (RG:
-            // scanned; otherwise those of the first sub-tile, e < nsteps), then
-            // this loader's step of the group (batch 1: the compute waves load A)
+            // this loader's step of the group and its marker, then the activation
+            // segments first needed by the group's steps (RG: scanned; otherwise
+            // those of the first sub-tile, e < nsteps) and their markers, so that
+            // no step marker waits for activation loads (batch 1, small A: the
+            // compute waves load A)
             int s_lo = 4 * g4, s_hi = BD || AC ? 0 : min(4 * g4 + 4, nsteps);
             if (RG) {
                 s_lo = s_next;
@@ -217,18 +219,6 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                 }
                 s_hi = s_next;
                 step_ts(e, te, se);
-            }
-            for (int s2 = s_lo; s2 < s_hi; s2++) {
-                // the segment's slot must be released by all nsub steps of its
-                // previous segment
-                if (RG && s2 >= na) wait_flag_value(&flags[kSegCount + s2 - na], nsub);
-                const uint32_t dst = lds0 + (uint32_t)(kFlagBytes + seg_off(s2));
-#pragma unroll
-                for (int q = 0; q < kASlots; q++) {
-                    const int qa = j + 4 * q;
-                    if (qa >= IA) break;
-                    if (aon[q]) dma16(asrc[q] + (uint32_t)(512 * G * s2), dst + (uint32_t)(qa << 10));
-                }
             }
             if (e < S) {
                 // the slot's previous step must be consumed (its marker set to 2
@@ -256,9 +246,21 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                 }
             }
             if (g4 == 0) clear_flags_and_meet();
+            if (e < S) dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kStepMark + e)), lane);
+            for (int s2 = s_lo; s2 < s_hi; s2++) {
+                // the segment's slot must be released by all nsub steps of its
+                // previous segment
+                if (RG && s2 >= na) wait_flag_value(&flags[kSegCount + s2 - na], nsub);
+                const uint32_t dst = lds0 + (uint32_t)(kFlagBytes + seg_off(s2));
+#pragma unroll
+                for (int q = 0; q < kASlots; q++) {
+                    const int qa = j + 4 * q;
+                    if (qa >= IA) break;
+                    if (aon[q]) dma16(asrc[q] + (uint32_t)(512 * G * s2), dst + (uint32_t)(qa << 10));
+                }
+            }
             for (int s2 = s_lo; s2 < s_hi; s2++)
                 dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kAMark + 4 * s2 + j)), lane);
-            if (e < S) dma_marker(g_marker_src + lane, lds0 + (uint32_t)(4 * (kStepMark + e)), lane);
             if (!RG) {
                 se += 4;
                 while (se >= nsteps) { se -= nsteps; te++; }

@@ -55,10 +55,12 @@ struct LdsPlan {
 
 // Steps in windows of wn segments (each sub-tile in turn takes the window's
 // segments) with na activation slots: the fewest steps by which the loaders can
-// run ahead of the compute waves, or 0 when a loader would wait for a step of
-// its own group or a later one (deadlock) -- the slot of segment s is released
-// by the last step of segment s - na, and segment s is loaded in the group of
-// its first step.
+// run ahead of the compute waves, or 0 unless every slot is released by a step
+// of an earlier group of four -- the slot of segment s is released by the last
+// step of segment s - na, and segment s is loaded in the group of its first
+// step, after that group's steps.  (A release in a later group would deadlock;
+// one in the same group would not, each loader issuing its step before it
+// waits, but leaves the loaders no lead.)
 inline int ring_ahead(int nsteps, int nsub, int wn, int na) {
     const int ew = nsub * wn;
     auto first = [&](int sg) { return (sg / wn) * ew + sg % wn; };

@@ -6,11 +6,11 @@
 // done, and with every (sub-tile, segment) partial parked exactly once.
 //
 // The model follows the kernel's protocol action by action:
-//   loader j, group g4 (steps 4 g4 .. 4 g4 + 3; it owns step 4 g4 + j):
-//     the activation segments whose first step lies in the group (ring: wait
-//     until segment s - na has been counted by all nsub of its steps), then its
+//   loader j, group g4 (steps 4 g4 .. 4 g4 + 3; it owns step 4 g4 + j): its
 //     step (ring: wait until step e - nslot is released), the barrier after
-//     group 0, then the segments' markers and the step's marker;
+//     group 0, the step's marker, then the activation segments whose first
+//     step lies in the group (ring: wait until segment s - na has been counted
+//     by all nsub of its steps) and their markers;
 //   compute wave: after the barrier, take the next step (batch 1: steps
 //     c, c + 12, ...), tabulate a segment's block sums on its first step (Q4_K,
 //     MFMA form), wait for the step's markers (and block sums), read and
@@ -20,9 +20,9 @@
 //   AC plans (small A): the compute waves load all of A before the barrier and
 //     wait for it (no dependence on the loaders), the loaders stream weights only.
 // Exit status 0 and a summary line on success; the first violation otherwise.
-// With --self-test it instead runs the model on plans with planted mistakes (an
-// activation ring too small for the loaders' lead, a step ring that is not
-// whole groups of four) and succeeds only if every one is caught.
+// With --self-test it instead runs the model on plans with planted mistakes
+// (activation rings whose slots wait for steps of later groups, a step ring
+// that is not whole groups of four) and succeeds only if every one is caught.
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -158,11 +158,11 @@ struct Model {
                     l.s_hi = p.BD || p.AC ? l.s_lo : std::min(4 * l.g4 + 4, nsteps);
                 }
                 l.s2 = l.s_lo;
-                l.phase = 1;
+                l.phase = 2;
                 return true;
             }
             case 1: {                                          // load segment s2
-                if (l.s2 >= l.s_hi) { l.phase = 2; return true; }
+                if (l.s2 >= l.s_hi) { l.phase = 4; return true; }
                 const int s2 = l.s2;
                 if (a_ring && s2 >= p.na) {
                     if (!cleared) fail("loader waits before the barrier", g, p, s2);
@@ -189,13 +189,17 @@ struct Model {
                 l.phase = 3;
                 return true;
             }
-            case 3: {                                          // the barrier after group 0
+            case 3: {                                          // the barrier after group 0, the step's marker
                 if (l.g4 == 0) {
                     if (!l.at_bar) { l.at_bar = true; at_barrier++; }
                     if (!cleared) return false;
                 }
-                for (int s2 = l.s_lo; s2 < l.s_hi; s2++) amark[s2 * kNL + l.j] = 1;
                 if (e < S) stepmark[e] = 1;
+                l.phase = 1;
+                return true;
+            }
+            case 4: {                                          // the segments' markers
+                for (int s2 = l.s_lo; s2 < l.s_hi; s2++) amark[s2 * kNL + l.j] = 1;
                 l.g4++;
                 l.phase = 0;
                 if (4 * l.g4 >= S) l.done = true;
@@ -366,10 +370,10 @@ int self_test() {
         std::printf("no ring plan for the self-test shape\n");
         return 1;
     }
-    LdsPlan a = p;                     // one activation slot, segment-major: a loader waits for its own group
-    a.win = 1;
+    LdsPlan a = p;                     // windows of two with one slot: a segment's slot waits for the
+    a.win = 2;                         // previous segment's last step, in a later group of four
     a.na = 1;
-    expect_failure("activation ring of one slot", g, a);
+    expect_failure("activation ring of one slot, windows of two", g, a);
     LdsPlan b = p;                     // windows of four with three slots: the window's fourth segment
     b.win = 4;                         // waits for its first, whose last step is in a later group
     b.na = 3;
