@@ -29,7 +29,8 @@ OUT_F32, OUT_F16 = 0, 1
 # bf_algo
 ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT = 0, 1, 2, 3, 4, 5, 6
 
-EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16",
+EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
+           "bf_swiglu_f16",
            "bf_gguf_open", "bf_gguf_close", "bf_gguf_tensor_count", "bf_gguf_tensor_at", "bf_gguf_find",
            "bf_gguf_get_u64", "bf_gguf_get_str", "bf_gguf_upload",
            "bf_status_str", "bf_last_error", "bf_version")
@@ -76,6 +77,8 @@ def lib() -> ctypes.CDLL:
         L.bf_gemm_ex.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, i, vp]
         L.bf_dequant_f16.argtypes = [i, vp, vp, vp, i, i, vp]
         L.bf_gemm_batched.argtypes = [i, i, i, ctypes.POINTER(GemmDesc), vp]
+        L.bf_gemm_swiglu.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
+        L.bf_swiglu_f16.argtypes = [vp, i, vp, i, i, i, vp]
         L.bf_gguf_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(vp)]
         L.bf_gguf_close.argtypes = [vp]
         L.bf_gguf_close.restype = None
@@ -90,7 +93,8 @@ def lib() -> ctypes.CDLL:
         for f in ("bf_gguf_open", "bf_gguf_tensor_at", "bf_gguf_find", "bf_gguf_get_u64", "bf_gguf_get_str",
                   "bf_gguf_upload"):
             getattr(L, f).restype = i
-        for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16"):
+        for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
+                  "bf_swiglu_f16"):
             getattr(L, f).restype = i
         L.bf_status_str.argtypes = [i]
         L.bf_status_str.restype = ctypes.c_char_p
@@ -131,6 +135,23 @@ def gemm(qtype: int, W, W_aux, A, C, M: int, N: int, K: int, *, lda: int | None 
     st = lib().bf_gemm_ex(qtype, _ptr(W), _ptr(W_aux), _ptr(A), K if lda is None else lda,
                           _ptr(C), N if ldc is None else ldc, otype, M, N, K, algo, _stream(stream))
     _check(st, "bf_gemm_ex")
+
+
+def gemm_swiglu(qtype: int, W, W_aux, gate_up, C, M: int, N: int, K: int, *, ld: int | None = None,
+                ldc: int | None = None, otype: int = OUT_F32, stream=None) -> None:
+    """C[M][N] = (SiLU(G) * U) . dequant(W)^T with G, U = columns [0, K) and
+    [K, 2K) of gate_up[M][ld] (batch 1-2; BusfillError BF_ERR_UNSUPPORTED
+    otherwise)."""
+    st = lib().bf_gemm_swiglu(qtype, _ptr(W), _ptr(W_aux), _ptr(gate_up), 2 * K if ld is None else ld, _ptr(C),
+                              N if ldc is None else ldc, otype, M, N, K, _stream(stream))
+    _check(st, "bf_gemm_swiglu")
+
+
+def swiglu_f16(gate_up, out, M: int, K: int, *, ld: int | None = None, ldo: int | None = None,
+               stream=None) -> None:
+    """out[M][K] (fp16 bits) = RN_fp16(SiLU(G) * U), G and U as for gemm_swiglu."""
+    _check(lib().bf_swiglu_f16(_ptr(gate_up), 2 * K if ld is None else ld, _ptr(out), K if ldo is None else ldo,
+                               M, K, _stream(stream)), "bf_swiglu_f16")
 
 
 def gemm_batched(qtype: int, gemms, *, otype: int = OUT_F32, stream=None) -> None:

@@ -222,6 +222,41 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
     return BF_OK;
 }
 
+bf_status bf_gemm_swiglu(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* gate_up, int ld,
+                         void* C, int ldc, bf_otype otype, int M, int N, int K, void* stream) {
+    g_last_error[0] = '\0';
+    if (ld < 2 * (int64_t)K) return fail(BF_ERR_INVALID, "ld=%d < 2K=%lld", ld, 2 * (long long)K);
+    bf_status st = check_gemm(qtype, W, W_aux, gate_up, ld, C, ldc, otype, M, N, K);
+    if (st != BF_OK) return st;
+    if (!aligned(gate_up, 16) || ld % 8) return fail(BF_ERR_INVALID, "gate_up rows must be 16-byte aligned (ld %% 8 == 0)");
+    bf::GemmArgs g;
+    g.qtype = (int)qtype;
+    g.W = (const uint8_t*)W;
+    g.Waux = (const uint8_t*)W_aux;
+    g.A = gate_up;
+    g.lda = ld;
+    g.C = C;
+    g.ldc = ldc;
+    g.out_f16 = otype == BF_OUT_F16;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    if (!fast_eligible(g) || !bf::lds_swiglu_supports(g))
+        return fail(BF_ERR_UNSUPPORTED, "fused SiLU*up GEMM: batch 1-2 with the activations resident in LDS "
+                                        "(M=%d N=%d K=%d); use bf_swiglu_f16 then bf_gemm", M, N, K);
+    return from_hip(bf::gemm_lds_swiglu(g, (hipStream_t)stream), "kernel launch");
+}
+
+bf_status bf_swiglu_f16(const uint16_t* gate_up, int ld, uint16_t* out, int ldo, int M, int K, void* stream) {
+    g_last_error[0] = '\0';
+    if (!gate_up || !out) return fail(BF_ERR_INVALID, "gate_up or out is NULL");
+    if (M < 1 || K < 8 || K % 8) return fail(BF_ERR_INVALID, "M=%d must be >= 1 and K=%d a multiple of 8", M, K);
+    if (ld < 2 * (int64_t)K || ldo < K) return fail(BF_ERR_INVALID, "ld=%d < 2K or ldo=%d < K=%d", ld, ldo, K);
+    if (!aligned(gate_up, 16) || !aligned(out, 16) || ld % 8 || ldo % 8)
+        return fail(BF_ERR_INVALID, "gate_up and out rows must be 16-byte aligned");
+    return from_hip(bf::swiglu_f16(gate_up, ld, out, ldo, M, K, (hipStream_t)stream), "kernel launch");
+}
+
 bf_status bf_busfill_q4(const uint16_t* A, const uint8_t* Wq, const uint16_t* Ws, float* C, int Bsz, int K, int N,
                         void* stream) {
     return run_gemm(BF_Q4_0_PLANES, Wq, Ws, A, K, C, N, BF_OUT_F32, Bsz, N, K, BF_ALGO_AUTO, stream);

@@ -178,4 +178,28 @@ __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// SiLU(g) * u rounded to fp16 (computed in fp32: g / (1 + e^-g) * u), the one
+// formula of the fused down-projection GEMM and of the standalone kernel, so
+// that the two give the same bits.
+__device__ __forceinline__ _Float16 swiglu_f16(_Float16 g, _Float16 u) {
+    const float gf = (float)g;
+    return (_Float16)(gf / (1.0f + expf(-gf)) * (float)u);
+}
+
+// Eight fp16 pairs (16 bytes of gate at g, 16 of up at u) -> eight fp16 swiglu values.
+__device__ __forceinline__ u4 swiglu8(const uint16_t* g, const uint16_t* u) {
+    const u4 gv = *(const u4*)g, uv = *(const u4*)u;
+    u4 r;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t gw = gv[w], uw = uv[w];
+        const _Float16 lo = swiglu_f16(__builtin_bit_cast(_Float16, (uint16_t)(gw & 0xFFFF)),
+                                       __builtin_bit_cast(_Float16, (uint16_t)(uw & 0xFFFF)));
+        const _Float16 hi = swiglu_f16(__builtin_bit_cast(_Float16, (uint16_t)(gw >> 16)),
+                                       __builtin_bit_cast(_Float16, (uint16_t)(uw >> 16)));
+        r[w] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+    return r;
+}
+
 }  // namespace bf

@@ -77,8 +77,10 @@ namespace {
 // One GEMM's share of a launch: workgroup `bid` of its grid.  RG: steps in
 // windows of `win` segments and na activation slots (plans whose activations do
 // not all fit); otherwise sub-tile-major with all of A resident.  AC: the
-// compute waves load all of A before the barrier (small A).
-template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC>
+// compute waves load all of A before the barrier (small A).  SW (batch 1 or
+// AC): A[m][k] = SiLU(A[m][k]) * A[m][K + k], formed as the compute waves load
+// it (the fused gate|up projection's output in, the down projection out).
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC, bool SW = false>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                          const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
                                          int nslot, int na, int win, const uint8_t* __restrict__ Waux,
@@ -300,7 +302,12 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             const int i = i0 + rot < nA ? i0 + rot : i0 + rot - nA;
             const int P = 64 * i + lane;
             const int sg = min(P / 33, nsg - 1), c = min(P - 33 * (P / 33), 31);
-            if (P < nsg * 33) dma16(A + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + 1024 * i));
+            if constexpr (SW) {
+                if (P < nsg * 33)
+                    *(u4*)(lds + kFlagBytes + 1024 * i + 16 * lane) = swiglu8(A + 256 * sg + 8 * c, A + K + 256 * sg + 8 * c);
+            } else {
+                if (P < nsg * 33) dma16(A + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + 1024 * i));
+            }
         }
         clear_flags_and_meet();
         signal_own_loads(&flags[cw], lane);
@@ -315,9 +322,13 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             const int sg = f / IA, i = f - sg * IA;
             const uint32_t P = 64u * i + lane;
             const uint32_t m = P / (33u * G), rem = P - 33u * G * m, gg = rem / 33u, c = rem - 33u * gg;
-            const uint8_t* src =
-                (const uint8_t*)(A + (int64_t)min((int)m, M - 1) * lda + 256 * (G * sg + gg) + 8 * min((int)c, 31));
-            if (P < (uint32_t)PA && c < 32) dma16(src, lds0 + (uint32_t)(kFlagBytes + sg * seg_bytes + (i << 10)));
+            const uint16_t* src = A + (int64_t)min((int)m, M - 1) * lda + 256 * (G * sg + gg) + 8 * min((int)c, 31);
+            if constexpr (SW) {
+                if (P < (uint32_t)PA && c < 32)
+                    *(u4*)(lds + kFlagBytes + sg * seg_bytes + (i << 10) + 16 * lane) = swiglu8(src, src + K);
+            } else {
+                if (P < (uint32_t)PA && c < 32) dma16(src, lds0 + (uint32_t)(kFlagBytes + sg * seg_bytes + (i << 10)));
+            }
         }
         clear_flags_and_meet();
         signal_own_loads(&flags[cw], lane);
@@ -670,13 +681,13 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     }
 }
 
-template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC = false>
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC = false, bool SW = false>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
                 int nsub, int nslot, int na, int win, const uint8_t* __restrict__ Waux, void* __restrict__ C,
                 int ldc, int out_f16) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    lds_body<QT, G, MT, NC, NL, BD, RG, AC>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, win, Waux, C, ldc,
+    lds_body<QT, G, MT, NC, NL, BD, RG, AC, SW>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, win, Waux, C, ldc,
                                     out_f16);
 }
 
@@ -713,9 +724,9 @@ constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 LdsShape lds_shape(const GemmArgs& g) { return LdsShape{g.M, g.N, g.K, g.qtype == QT_Q4_K}; }
 
-template <int QT, int G, int MT, bool BD = false, bool RG = false, bool AC = false>
+template <int QT, int G, int MT, bool BD = false, bool RG = false, bool AC = false, bool SW = false>
 hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
-    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG, AC>;
+    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG, AC, SW>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -825,6 +836,36 @@ hipError_t gemm_lds_batched(const GemmArgs* gs, int n, hipStream_t st) {
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+// The fused SiLU-times-up GEMM (A = the gate|up output, K columns each): the
+// batch-1 kernel or the one whose compute waves load all of A (the only ones
+// that read A through the compute waves, where it can be transformed).
+bool lds_swiglu_plan(const GemmArgs& g, LdsPlan& p) {
+    if (g.M > 2 || !choose_lds(lds_shape(g), p)) return false;
+    return p.BD || (!p.RG && p.G == 4 && p.MT == 1 && p.na == g.K / 1024);
+}
+
+bool lds_swiglu_supports(const GemmArgs& g) {
+    LdsPlan p;
+    if (g.qtype == QT_PLANES && ((uintptr_t)g.Waux & 15)) return false;
+    return lds_swiglu_plan(g, p);
+}
+
+template <int QT>
+hipError_t dispatch_lds_swiglu(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
+    if (p.BD) return launch_lds<QT, 4, 1, true, false, false, true>(g, p, st);
+    return launch_lds<QT, 4, 1, false, false, true, true>(g, p, st);
+}
+
+hipError_t gemm_lds_swiglu(const GemmArgs& g, hipStream_t st) {
+    LdsPlan p;
+    if (!lds_swiglu_plan(g, p)) return hipErrorInvalidValue;
+    switch (g.qtype) {
+        case QT_Q4_K: return dispatch_lds_swiglu<QT_Q4_K>(g, p, st);
+        case QT_PLANES: return dispatch_lds_swiglu<QT_PLANES>(g, p, st);
+        default: return dispatch_lds_swiglu<QT_Q4_0>(g, p, st);
+    }
 }
 
 bool lds_supports(const GemmArgs& g) {

@@ -42,5 +42,10 @@ void set_last_error(const char* text);
 
 hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
                        int N, int K, hipStream_t st);
+// A = SiLU(A[:, 0:K]) * A[:, K:2K] formed while loading (batch 1-2 plans that
+// load A through the compute waves), and the standalone elementwise kernel.
+hipError_t gemm_lds_swiglu(const GemmArgs& g, hipStream_t st);
+bool lds_swiglu_supports(const GemmArgs& g);
+hipError_t swiglu_f16(const uint16_t* gu, int ld, uint16_t* out, int ldo, int M, int K, hipStream_t st);
 
 }  // namespace bf

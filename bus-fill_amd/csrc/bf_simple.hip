@@ -98,4 +98,22 @@ hipError_t gemm_simple(const GemmArgs& g, hipStream_t st) {
     return hipGetLastError();
 }
 
+// out[m][k] = SiLU(gu[m][k]) * gu[m][K + k] in fp16 (the formula the fused
+// down-projection GEMM applies while loading A), eight elements per thread.
+__global__ __launch_bounds__(256) void k_swiglu_f16(const uint16_t* __restrict__ gu, int ld,
+                                                    uint16_t* __restrict__ out, int ldo, int M, int K) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;   // group of eight in a row
+    const int per_row = K >> 3;
+    if (i >= (int64_t)M * per_row) return;
+    const int m = (int)(i / per_row), k = (int)(i - (int64_t)m * per_row) * 8;
+    const uint16_t* g = gu + (int64_t)m * ld + k;
+    *(u4*)(out + (int64_t)m * ldo + k) = swiglu8(g, g + K);
+}
+
+hipError_t swiglu_f16(const uint16_t* gu, int ld, uint16_t* out, int ldo, int M, int K, hipStream_t st) {
+    const int64_t groups = (int64_t)M * (K >> 3);
+    hipLaunchKernelGGL(k_swiglu_f16, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st, gu, ld, out, ldo, M, K);
+    return hipGetLastError();
+}
+
 }  // namespace bf

@@ -117,6 +117,25 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
 bf_status bf_dequant_f16(bf_qtype qtype, const void* W, const void* W_aux,
                          uint16_t* W_f16, int N, int K, void* stream);
 
+/* The down projection of a SwiGLU feed-forward block with the activation
+ * fused in: C = (SiLU(G) * U) . dequant(W)^T, where gate_up[M][ld] holds the
+ * fused gate|up projection's output, G = columns 0..K-1 and U = K..2K-1 (ld >=
+ * 2K, rows 16-byte aligned).  Each product is rounded to fp16 as
+ * bf_swiglu_f16 rounds it, so the result is bit-identical to bf_swiglu_f16
+ * followed by bf_gemm, without the second launch or the intermediate
+ * buffer.  Batch 1-2 (decode), with the activations resident in LDS
+ * (K <= 17408 at batch 2); other shapes return BF_ERR_UNSUPPORTED.  No
+ * counterpart in the reference, whose survey lists the fusion as a next step
+ * after the GEMM (fusing SiLU-mul between the gate/up and down projections). */
+bf_status bf_gemm_swiglu(bf_qtype qtype, const void* W, const void* W_aux,
+                         const uint16_t* gate_up, int ld, void* C, int ldc, bf_otype otype,
+                         int M, int N, int K, void* stream);
+
+/* out[m][k] = RN_fp16(SiLU(g) * u) for g = gate_up[m][k], u = gate_up[m][K + k],
+ * computed in fp32 as g / (1 + e^-g) * u.  K % 8 == 0; rows 16-byte aligned. */
+bf_status bf_swiglu_f16(const uint16_t* gate_up, int ld, uint16_t* out, int ldo,
+                        int M, int K, void* stream);
+
 /* ---------------------------------------------------------------- GGUF files
  * A reader of llama.cpp's model files (GGUF versions 2 and 3, public
  * specification), memory-mapped.  Q4_0 and Q4_K tensors are stored in the

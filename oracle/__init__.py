@@ -143,6 +143,19 @@ def gen_act(M: int, K: int, seed: int) -> np.ndarray:
     return A
 
 
+def swiglu_f16(gate_up: np.ndarray, K: int) -> np.ndarray:
+    """RN_fp16(SiLU(g) * u) for g = gate_up[:, :K], u = gate_up[:, K:2K] (fp16
+    bits), evaluated in fp32 as g / (1 + e^-g) * u.  No counterpart in the
+    reference (its survey lists the fused SiLU-mul down projection as a next
+    step); pinned by closed forms and a float64 evaluation in
+    tests/test_oracle.py."""
+    g = gate_up[:, :K].view(np.float16).astype(np.float32)
+    u = gate_up[:, K:2 * K].view(np.float16).astype(np.float32)
+    with np.errstate(over="ignore"):
+        s = g / (np.float32(1) + np.exp(-g))
+    return (s * u).astype(np.float16).view(np.uint16)
+
+
 def planes_to_blocks(w: QWeights) -> QWeights:
     assert w.qtype == Q4_0_PLANES
     B = np.empty((w.N, w.K // 32 * 18), np.uint8)

@@ -122,3 +122,23 @@ def test_gemm_desc_layout_matches_header():
     assert ctypes.sizeof(bf.GemmDesc) == 56
     assert bf.GemmDesc.C.offset == 32 and bf.GemmDesc.K.offset == 52
     assert "bf_gemm_desc" in HDR
+
+
+def test_swiglu_entries_reject_before_any_launch():
+    """bf_gemm_swiglu / bf_swiglu_f16 argument checks (no GPU needed: every
+    case returns before a launch)."""
+    L = bf.lib()
+    K, N = 1024, 256
+    # batch 3: not fused
+    assert L.bf_gemm_swiglu(bf.Q4_K, FAKE, None, FAKE, 2 * K, FAKE, N, bf.OUT_F32, 3, N, K, None) == bf.ERR_UNSUPPORTED
+    assert "bf_swiglu_f16 then bf_gemm" in L.bf_last_error().decode()
+    # ld must cover gate and up
+    assert L.bf_gemm_swiglu(bf.Q4_K, FAKE, None, FAKE, K, FAKE, N, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
+    # rows 16-byte aligned
+    assert L.bf_gemm_swiglu(bf.Q4_K, FAKE, None, FAKE + 2, 2 * K, FAKE, N, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
+    assert L.bf_gemm_swiglu(bf.Q4_K, FAKE, None, FAKE, 2 * K + 4, FAKE, N, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
+    assert L.bf_gemm_swiglu(bf.Q4_K, None, None, FAKE, 2 * K, FAKE, N, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
+    assert L.bf_swiglu_f16(None, 2 * K, FAKE, K, 1, K, None) == bf.ERR_INVALID
+    assert L.bf_swiglu_f16(FAKE, 2 * K, FAKE, K, 1, 12, None) == bf.ERR_INVALID
+    assert L.bf_swiglu_f16(FAKE, K, FAKE, K, 1, K, None) == bf.ERR_INVALID
+    assert L.bf_swiglu_f16(FAKE, 2 * K, FAKE + 8, K, 1, K, None) == bf.ERR_INVALID

@@ -584,3 +584,63 @@ def test_random_shapes_every_kernel(dev, seed):
         ref.check(C, f"{QT_NAME[qt]} M={M} N={N} K={K} algo={algo}")
         assert (gpu_gemm(w, A, dev, algo=algo, dw=dw) == C).all()
     assert ran >= 1
+
+
+def gen_gate_up(M, K, seed):
+    """gate|up rows (fp16 bits [M][2K]): gate ~ N(0, 2^2) with a few extreme
+    values, up ~ N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    g = (rng.normal(size=(M, K)) * 2).astype(np.float16)
+    g[:, :4] = np.array([0, 30, -30, -65504], np.float16)
+    u = rng.normal(size=(M, K)).astype(np.float16)
+    return np.concatenate([g, u], axis=1).view(np.uint16)
+
+
+@pytest.mark.parametrize("K", [1024, 5120, 17408])
+def test_swiglu_f16_matches_oracle(dev, K):
+    """The elementwise SiLU(g) * u against the oracle's fp32 restatement: at
+    most one fp16 ulp apart (the device exp and numpy's may round differently)."""
+    M = 3
+    gu = gen_gate_up(M, K, seed=K)
+    out = torch.empty((M, K), dtype=torch.int16, device=dev)
+    bf.swiglu_f16(to_dev(gu, dev), out, M, K)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.float16).astype(np.float64)
+    ref = O.swiglu_f16(gu, K).view(np.float16).astype(np.float64)
+    assert np.isfinite(got).all()
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert (np.abs(got - ref) <= ulp).all()
+
+
+@pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
+@pytest.mark.parametrize("N,K", [(5120, 17408), (1000, 5120), (300, 2048)])
+def test_gemm_swiglu_equals_swiglu_then_gemm(dev, qt, N, K):
+    """bf_gemm_swiglu (SiLU * up formed while the activations are loaded) is
+    bit-identical to bf_swiglu_f16 followed by bf_gemm, at batch 1 (sub-block
+    rows form) and 2 (activations loaded by the compute waves), and within the
+    oracle's bounds for the activations it used."""
+    w = O.gen_weights(qt, N, K, seed=N + K + qt)
+    dw = upload(w, dev)
+    for M in (1, 2):
+        gu = gen_gate_up(M, K, seed=M + N)
+        gud = to_dev(gu, dev)
+        C = torch.full((M, N), float("nan"), device=dev)
+        bf.gemm_swiglu(qt, dw[0], dw[1], gud, C, M, N, K)
+        a = torch.empty((M, K), dtype=torch.int16, device=dev)
+        bf.swiglu_f16(gud, a, M, K)
+        torch.cuda.synchronize()
+        A = a.cpu().numpy().view(np.uint16)
+        C2 = gpu_gemm(w, A, dev, dw=dw)
+        got = C.cpu().numpy().astype(np.float64)
+        assert (got == C2).all(), (QT_NAME[qt], N, K, M)
+        Ref(w, A).check(got, f"swiglu {QT_NAME[qt]} N={N} K={K} M={M}")
+
+
+def test_gemm_swiglu_refuses_shapes_it_does_not_fuse(dev):
+    w = O.gen_weights(O.Q4_K, 256, 1024, seed=3)
+    dw = upload(w, dev)
+    gud = to_dev(gen_gate_up(3, 1024, seed=3), dev)
+    C = torch.empty((3, 256), device=dev)
+    with pytest.raises(bf.BusfillError) as err:
+        bf.gemm_swiglu(O.Q4_K, dw[0], None, gud, C, 3, 256, 1024)
+    assert err.value.status == bf.ERR_UNSUPPORTED

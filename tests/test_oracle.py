@@ -333,3 +333,28 @@ def test_shape_rejection():
     w.K = 200
     with pytest.raises(ValueError):
         O.dequant_f16(w)
+
+
+def test_swiglu_closed_forms_and_float64():
+    """SiLU(g) * u: SiLU(0) = 0, SiLU(g) -> g for large g and -> -0 for very
+    negative g, u scales linearly; and within one fp16 ulp of the same
+    formula in float64 over a sweep of every fp16 exponent."""
+    def pack(g, u):
+        return np.concatenate([np.asarray(g, np.float16).reshape(1, -1),
+                               np.asarray(u, np.float16).reshape(1, -1)], axis=1).view(np.uint16)
+    K = 6
+    out = O.swiglu_f16(pack([0, 30, -30, 65504, -65504, 2.0], [1, 1, 1, 1, 1, 3.0]), K).view(np.float16)[0]
+    assert out[0] == 0 and out[1] == np.float16(30) and out[3] == np.float16(65504)
+    assert out[2] <= 0 and abs(float(out[2])) < 1e-10 and out[4] == 0
+    assert out[5] == np.float16(3 * 2 / (1 + np.exp(-2.0)))
+    # sweep: magnitudes over all fp16 binades, both signs, random u
+    rng = np.random.default_rng(4)
+    g = (rng.choice([-1, 1], 4096) * 2.0 ** rng.uniform(-14, 15.9, 4096)).astype(np.float16)
+    u = rng.normal(size=4096).astype(np.float16)
+    got = O.swiglu_f16(pack(g, u), 4096).view(np.float16)[0].astype(np.float64)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    ref = (g64 / (1 + np.exp(-g64)) * u64).astype(np.float16).astype(np.float64)
+    fin = np.isfinite(ref)
+    assert (got[~fin] == ref[~fin]).all()                 # products beyond fp16: the same infinity
+    ulp = np.spacing(np.abs(ref[fin]).astype(np.float16)).astype(np.float64)
+    assert (np.abs(got[fin] - ref[fin]) <= ulp).all()
