@@ -101,10 +101,11 @@ def bench_lib():
     L.bfb_time_sequence_batched.argtypes = [i, i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, vp, d]
     L.bfb_read_peak.argtypes = [vp, ctypes.c_size_t, i, vp, vp, d]
     L.bfb_read_slices.argtypes = [vp, i, ctypes.c_size_t, i, i, i, i, vp, vp, d]
+    L.bfb_time_swiglu.argtypes = [i, vp, vp, i, vp, i, vp, vp, i, i, i, i, i, i, vp, d]
     L.bfb_copy.argtypes = [vp, vp, ctypes.c_size_t, i, vp, d]
     L.bfb_last_error.restype = ctypes.c_char_p
     for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_time_sequence_batched", "bfb_read_peak", "bfb_read_slices",
-              "bfb_copy"):
+              "bfb_copy", "bfb_time_swiglu"):
         getattr(L, f).restype = i
     return L
 
@@ -356,6 +357,36 @@ def run_copy(L, args, dev):
                        "bytes_written": COPY_BYTES}}
 
 
+def run_swiglu(L, args, dev):
+    """The down projection of a 27B-class SwiGLU block (K = 17408 -> N = 5120)
+    fed by the gate|up output: SiLU*up fused into the GEMM's activation load
+    against bf_swiglu_f16 + bf_gemm (two launches and an fp16 intermediate)."""
+    import torch
+    N, K = 5120, 17408
+    rot = Rotation("q4_k", N, K, ROTATION_BYTES, seed=N, dev=dev)
+    W, aux = rot.ptr_arrays()
+    res = []
+    for M in (1, 2):
+        gu = torch.randn((M, 2 * K), device=dev).half()
+        a = torch.empty((M, K), device=dev, dtype=torch.float16)
+        C = torch.empty((M, N), device=dev, dtype=torch.float32)
+        r = {"M": M, "N": N, "K": K}
+        for fused in (1, 0):
+            ms = ctypes.c_double()
+            torch.cuda.synchronize()
+            rc = L.bfb_time_swiglu(QT["q4_k"], P(W), P(aux), rot.count, gu.data_ptr(), 2 * K, a.data_ptr(),
+                                   C.data_ptr(), M, N, K, fused, args.warmup, args.steps, stream_handle(),
+                                   ctypes.byref(ms))
+            torch.cuda.synchronize()
+            if rc != 0:
+                raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+            r["fused_us" if fused else "unfused_us"] = round(ms.value * 1e3 / args.steps, 3)
+        log(f"[bench] swiglu down projection M={M}: fused {r['fused_us']:.2f} us, "
+            f"swiglu + gemm {r['unfused_us']:.2f} us")
+        res.append(r)
+    return res
+
+
 def run_sweep(L, args, dev):
     res = []
     for (N, K) in ((17408, 5120), (5120, 17408)):
@@ -376,7 +407,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000, help="timed GEMMs per configuration")
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", default="q4_k", choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy"])
+    ap.add_argument("--workload", default="q4_k",
+                    choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy", "swiglu"])
     ap.add_argument("--batches", default="1,8,32")
     ap.add_argument("--graph", default="both", choices=["0", "1", "both"],
                     help="issue launches on the stream (0), replay a HIP graph (1), or time both")
@@ -445,6 +477,16 @@ def main():
                   "layer_tok_s": b["layer_tok_s"], "runs": recs}
     elif args.workload == "copy":
         record = run_copy(L, args, dev)
+    elif args.workload == "swiglu":
+        recs = run_swiglu(L, args, dev)
+        head = recs[0]
+        record = {"metric": "down projection with SiLU*up (Q4_K 17408->5120): us per call, fused vs swiglu + gemm",
+                  "value": head["fused_us"], "unit": "us", "n_gpus": 1, "steps": args.steps,
+                  "warmup": args.warmup, "ms_per_step": round(head["fused_us"] / 1e3, 6),
+                  "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+                  "data": "synthetic",
+                  "config": {"workload": "q4_k down projection N=5120 K=17408 fed by gate|up [M][2K], M=1 and 2"},
+                  "runs": recs}
     else:
         recs = run_sweep(L, args, dev)
         record = {"metric": "Q4_K GEMM batch sweep: weight-stream GB/s and MFMA utilisation",

@@ -178,12 +178,17 @@ __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// SiLU(g) * u rounded to fp16 (computed in fp32: g / (1 + e^-g) * u), the one
-// formula of the fused down-projection GEMM and of the standalone kernel, so
-// that the two give the same bits.
+// SiLU(g) * u rounded to fp16, computed in fp32 as g * (1 / (1 + e^-g)) * u
+// with e^-g = 2^(-g log2 e) on the hardware exp2 and the hardware reciprocal
+// (each within about one fp32 ulp; the fused GEMM evaluates this in every
+// workgroup, where a correctly rounded exp and division cost several
+// microseconds at K = 17408).  The one formula of the fused down-projection
+// GEMM and of the standalone kernel, so the two give the same bits.  Very
+// negative g: e^-g = inf, reciprocal 0, result -0 or 0; very positive g: g * u.
 __device__ __forceinline__ _Float16 swiglu_f16(_Float16 g, _Float16 u) {
     const float gf = (float)g;
-    return (_Float16)(gf / (1.0f + expf(-gf)) * (float)u);
+    const float e = __builtin_amdgcn_exp2f(gf * -1.44269504088896341f);
+    return (_Float16)(gf * __builtin_amdgcn_rcpf(1.0f + e) * (float)u);
 }
 
 // Eight fp16 pairs (16 bytes of gate at g, 16 of up at u) -> eight fp16 swiglu values.

@@ -206,6 +206,39 @@ int bfb_read_peak(const void* src, size_t bytes, int reps, void* sink, void* str
     return 0;
 }
 
+// The down projection of a SwiGLU block, cycling through `count` weight
+// matrices: fused (bf_gemm_swiglu) or SiLU*up by bf_swiglu_f16 into a_tmp
+// then bf_gemm; `steps` calls timed after `warmup`.
+int bfb_time_swiglu(int qtype, const void* const* W, const void* const* W_aux, int count, const uint16_t* gate_up,
+                    int ld, uint16_t* a_tmp, void* C, int M, int N, int K, int fused, int warmup, int steps,
+                    void* stream, double* ms_out) {
+    hipStream_t st = (hipStream_t)stream;
+    auto call = [&](int r) -> bf_status {
+        const void* w = W[r % count];
+        const void* aux = W_aux ? W_aux[r % count] : nullptr;
+        if (fused) return bf_gemm_swiglu((bf_qtype)qtype, w, aux, gate_up, ld, C, N, BF_OUT_F32, M, N, K, st);
+        bf_status s2 = bf_swiglu_f16(gate_up, ld, a_tmp, K, M, K, st);
+        if (s2 != BF_OK) return s2;
+        return bf_gemm((bf_qtype)qtype, w, aux, a_tmp, K, C, N, BF_OUT_F32, M, N, K, st);
+    };
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    for (int r = 0; r < warmup; r++)
+        if ((g_bf = call(r)) != BF_OK) return -1;
+    HCK(hipEventRecord(e0, st));
+    for (int r = 0; r < steps; r++)
+        if ((g_bf = call(r)) != BF_OK) return -1;
+    HCK(hipEventRecord(e1, st));
+    HCK(hipEventSynchronize(e1));
+    float ms;
+    HCK(hipEventElapsedTime(&ms, e0, e1));
+    *ms_out = ms;
+    HCK(hipEventDestroy(e0));
+    HCK(hipEventDestroy(e1));
+    return 0;
+}
+
 // Streaming reads of `bytes` per launch cycling through `count` buffers src[i]
 // (the weight rotation): the time one launch of that size takes to read its
 // bytes from HBM with nothing else to do.  Grid blocks x threads.

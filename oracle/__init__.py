@@ -145,7 +145,9 @@ def gen_act(M: int, K: int, seed: int) -> np.ndarray:
 
 def swiglu_f16(gate_up: np.ndarray, K: int) -> np.ndarray:
     """RN_fp16(SiLU(g) * u) for g = gate_up[:, :K], u = gate_up[:, K:2K] (fp16
-    bits), evaluated in fp32 as g / (1 + e^-g) * u.  No counterpart in the
+    bits), evaluated in fp32 as g / (1 + e^-g) * u (the device evaluates the
+    exponential and reciprocal to about one fp32 ulp: results may differ by one
+    fp16 ulp near a rounding boundary).  No counterpart in the
     reference (its survey lists the fused SiLU-mul down projection as a next
     step); pinned by closed forms and a float64 evaluation in
     tests/test_oracle.py."""
