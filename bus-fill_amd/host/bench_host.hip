@@ -221,14 +221,18 @@ int bfb_time_swiglu(int qtype, const void* const* W, const void* const* W_aux, i
         if (s2 != BF_OK) return s2;
         return bf_gemm((bf_qtype)qtype, w, aux, a_tmp, K, C, N, BF_OUT_F32, M, N, K, st);
     };
+    for (int r = 0; r < warmup; r++)
+        if ((g_bf = call(r)) != BF_OK) return -1;
     hipEvent_t e0, e1;
     HCK(hipEventCreate(&e0));
     HCK(hipEventCreate(&e1));
-    for (int r = 0; r < warmup; r++)
-        if ((g_bf = call(r)) != BF_OK) return -1;
     HCK(hipEventRecord(e0, st));
     for (int r = 0; r < steps; r++)
-        if ((g_bf = call(r)) != BF_OK) return -1;
+        if ((g_bf = call(r)) != BF_OK) {
+            (void)hipEventDestroy(e0);
+            (void)hipEventDestroy(e1);
+            return -1;
+        }
     HCK(hipEventRecord(e1, st));
     HCK(hipEventSynchronize(e1));
     float ms;
