@@ -103,9 +103,10 @@ def bench_lib():
     L.bfb_read_slices.argtypes = [vp, i, ctypes.c_size_t, i, i, i, i, vp, vp, d]
     L.bfb_time_swiglu.argtypes = [i, vp, vp, i, vp, i, vp, vp, i, i, i, i, i, i, vp, d]
     L.bfb_copy.argtypes = [vp, vp, ctypes.c_size_t, i, vp, d]
+    L.bfb_time_q8.argtypes = [i, vp, vp, i, vp, vp, vp, i, i, i, i, i, i, vp, d]
     L.bfb_last_error.restype = ctypes.c_char_p
     for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_time_sequence_batched", "bfb_read_peak", "bfb_read_slices",
-              "bfb_copy", "bfb_time_swiglu"):
+              "bfb_copy", "bfb_time_swiglu", "bfb_time_q8"):
         getattr(L, f).restype = i
     return L
 
@@ -387,6 +388,35 @@ def run_swiglu(L, args, dev):
     return res
 
 
+def run_q8(L, args, dev):
+    """The integer-dot activation path (int8 activations per 32 values,
+    v_dot4_i32_i8) against the fp16 GEMM, Q4_K 5120x5120, M = 1-16: the q8
+    GEMM alone, and quantize + GEMM per call."""
+    import torch
+    N = K = 5120
+    rot = Rotation("q4_k", N, K, ROTATION_BYTES, seed=N, dev=dev)
+    W, aux = rot.ptr_arrays()
+    res = []
+    for M in (1, 2, 4, 8, 16):
+        A = torch.randn((M, K), device=dev).half()
+        Aq = torch.empty((M * K + 8 * M * (K // 32),), device=dev, dtype=torch.uint8)
+        C = torch.empty((M, N), device=dev, dtype=torch.float32)
+        r = {"M": M, "N": N, "K": K}
+        for mode, key in ((0, "fp16_us"), (2, "q8_gemm_us"), (1, "q8_quant_gemm_us")):
+            ms = ctypes.c_double()
+            torch.cuda.synchronize()
+            rc = L.bfb_time_q8(QT["q4_k"], P(W), P(aux), rot.count, A.data_ptr(), Aq.data_ptr(), C.data_ptr(),
+                               M, N, K, mode, args.warmup, args.steps, stream_handle(), ctypes.byref(ms))
+            torch.cuda.synchronize()
+            if rc != 0:
+                raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+            r[key] = round(ms.value * 1e3 / args.steps, 3)
+        log(f"[bench] q8 path M={M:2d}: fp16 GEMM {r['fp16_us']:.2f} us, q8 GEMM {r['q8_gemm_us']:.2f} us, "
+            f"quantize + q8 GEMM {r['q8_quant_gemm_us']:.2f} us")
+        res.append(r)
+    return res
+
+
 def run_sweep(L, args, dev):
     res = []
     for (N, K) in ((17408, 5120), (5120, 17408)):
@@ -408,7 +438,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2000, help="timed GEMMs per configuration")
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="q4_k",
-                    choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy", "swiglu"])
+                    choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy", "swiglu", "q8"])
     ap.add_argument("--batches", default="1,8,32")
     ap.add_argument("--graph", default="both", choices=["0", "1", "both"],
                     help="issue launches on the stream (0), replay a HIP graph (1), or time both")
@@ -487,6 +517,15 @@ def main():
                   "data": "synthetic",
                   "config": {"workload": "q4_k down projection N=5120 K=17408 fed by gate|up [M][2K], M=1 and 2"},
                   "runs": recs}
+    elif args.workload == "q8":
+        recs = run_q8(L, args, dev)
+        head = next(r for r in recs if r["M"] == 8)
+        record = {"metric": "integer-dot (int8 activation) path vs fp16 GEMM, Q4_K 5120x5120: us per GEMM",
+                  "value": head["q8_gemm_us"], "unit": "us", "n_gpus": 1, "steps": args.steps,
+                  "warmup": args.warmup, "ms_per_step": round(head["q8_gemm_us"] / 1e3, 6),
+                  "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+                  "data": "synthetic",
+                  "config": {"workload": "q4_k N=5120 K=5120, M=1-16, value at M=8"}, "runs": recs}
     else:
         recs = run_sweep(L, args, dev)
         record = {"metric": "Q4_K GEMM batch sweep: weight-stream GB/s and MFMA utilisation",

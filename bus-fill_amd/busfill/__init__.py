@@ -30,7 +30,7 @@ OUT_F32, OUT_F16 = 0, 1
 ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT = 0, 1, 2, 3, 4, 5, 6
 
 EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
-           "bf_swiglu_f16",
+           "bf_swiglu_f16", "bf_q8_bytes", "bf_quantize_q8", "bf_gemm_q8",
            "bf_gguf_open", "bf_gguf_close", "bf_gguf_tensor_count", "bf_gguf_tensor_at", "bf_gguf_find",
            "bf_gguf_get_u64", "bf_gguf_get_str", "bf_gguf_upload",
            "bf_status_str", "bf_last_error", "bf_version")
@@ -79,6 +79,10 @@ def lib() -> ctypes.CDLL:
         L.bf_gemm_batched.argtypes = [i, i, i, ctypes.POINTER(GemmDesc), vp]
         L.bf_gemm_swiglu.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
         L.bf_swiglu_f16.argtypes = [vp, i, vp, i, i, i, vp]
+        L.bf_q8_bytes.argtypes = [i, i]
+        L.bf_q8_bytes.restype = ctypes.c_size_t
+        L.bf_quantize_q8.argtypes = [vp, i, vp, i, i, vp]
+        L.bf_gemm_q8.argtypes = [i, vp, vp, vp, vp, i, i, i, i, i, vp]
         L.bf_gguf_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(vp)]
         L.bf_gguf_close.argtypes = [vp]
         L.bf_gguf_close.restype = None
@@ -94,7 +98,7 @@ def lib() -> ctypes.CDLL:
                   "bf_gguf_upload"):
             getattr(L, f).restype = i
         for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
-                  "bf_swiglu_f16"):
+                  "bf_swiglu_f16", "bf_quantize_q8", "bf_gemm_q8"):
             getattr(L, f).restype = i
         L.bf_status_str.argtypes = [i]
         L.bf_status_str.restype = ctypes.c_char_p
@@ -152,6 +156,24 @@ def swiglu_f16(gate_up, out, M: int, K: int, *, ld: int | None = None, ldo: int 
     """out[M][K] (fp16 bits) = RN_fp16(SiLU(G) * U), G and U as for gemm_swiglu."""
     _check(lib().bf_swiglu_f16(_ptr(gate_up), 2 * K if ld is None else ld, _ptr(out), K if ldo is None else ldo,
                                M, K, _stream(stream)), "bf_swiglu_f16")
+
+
+def q8_bytes(M: int, K: int) -> int:
+    """Bytes of the int8 activation buffer for M rows of K (0 for a bad shape)."""
+    return int(lib().bf_q8_bytes(M, K))
+
+
+def quantize_q8(A, Aq, M: int, K: int, *, lda: int | None = None, stream=None) -> None:
+    """Aq (q8_bytes(M, K) bytes) = A[M][K] fp16 quantized to int8 per 32 values."""
+    _check(lib().bf_quantize_q8(_ptr(A), K if lda is None else lda, _ptr(Aq), M, K, _stream(stream)),
+           "bf_quantize_q8")
+
+
+def gemm_q8(qtype: int, W, W_aux, Aq, C, M: int, N: int, K: int, *, ldc: int | None = None,
+            otype: int = OUT_F32, stream=None) -> None:
+    """C[M][N] from quantize_q8's activations and the weights in place (M <= 16)."""
+    _check(lib().bf_gemm_q8(qtype, _ptr(W), _ptr(W_aux), _ptr(Aq), _ptr(C), N if ldc is None else ldc, otype,
+                            M, N, K, _stream(stream)), "bf_gemm_q8")
 
 
 def gemm_batched(qtype: int, gemms, *, otype: int = OUT_F32, stream=None) -> None:

@@ -257,6 +257,46 @@ bf_status bf_swiglu_f16(const uint16_t* gate_up, int ld, uint16_t* out, int ldo,
     return from_hip(bf::swiglu_f16(gate_up, ld, out, ldo, M, K, (hipStream_t)stream), "kernel launch");
 }
 
+size_t bf_q8_bytes(int M, int K) { return M < 1 || K < 32 || K % 32 ? 0 : bf::q8_bytes(M, K); }
+
+bf_status bf_quantize_q8(const uint16_t* A, int lda, void* Aq, int M, int K, void* stream) {
+    g_last_error[0] = '\0';
+    if (!A || !Aq) return fail(BF_ERR_INVALID, "A or Aq is NULL");
+    if (M < 1 || K < 32 || K % 32) return fail(BF_ERR_INVALID, "M=%d must be >= 1 and K=%d a multiple of 32", M, K);
+    if (lda < K) return fail(BF_ERR_INVALID, "lda=%d < K=%d", lda, K);
+    if (!aligned(A, 16) || lda % 8 || !aligned(Aq, 16))
+        return fail(BF_ERR_INVALID, "A rows and Aq must be 16-byte aligned (lda %% 8 == 0)");
+    return from_hip(bf::quantize_q8(A, lda, Aq, M, K, (hipStream_t)stream), "kernel launch");
+}
+
+bf_status bf_gemm_q8(bf_qtype qtype, const void* W, const void* W_aux, const void* Aq, void* C, int ldc,
+                     bf_otype otype, int M, int N, int K, void* stream) {
+    g_last_error[0] = '\0';
+    bf_status st = check_weights(qtype, W, W_aux, N, K);
+    if (st != BF_OK) return st;
+    if (!Aq || !C) return fail(BF_ERR_INVALID, "Aq or C is NULL");
+    if (otype != BF_OUT_F32 && otype != BF_OUT_F16) return fail(BF_ERR_INVALID, "unknown otype %d", (int)otype);
+    if (M < 1) return fail(BF_ERR_INVALID, "M=%d must be >= 1", M);
+    if (ldc < N) return fail(BF_ERR_INVALID, "ldc=%d < N=%d", ldc, N);
+    if (!aligned(C, otype == BF_OUT_F32 ? 4 : 2)) return fail(BF_ERR_INVALID, "C is not aligned to its element");
+    if (!aligned(Aq, 16) || !aligned(W, 16) || (W_aux && !aligned(W_aux, 4)))
+        return fail(BF_ERR_INVALID, "Aq and W must be 16-byte aligned, W_aux 4-byte aligned");
+    if (!bf::q8_supports(M, K))
+        return fail(BF_ERR_UNSUPPORTED, "integer-dot GEMM: batch 1-16 and K %% 64 == 0 (M=%d K=%d)", M, K);
+    bf::Q8Args g;
+    g.qtype = (int)qtype;
+    g.W = (const uint8_t*)W;
+    g.Waux = (const uint8_t*)W_aux;
+    g.Aq = Aq;
+    g.C = C;
+    g.ldc = ldc;
+    g.out_f16 = otype == BF_OUT_F16;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    return from_hip(bf::gemm_q8(g, (hipStream_t)stream), "kernel launch");
+}
+
 bf_status bf_busfill_q4(const uint16_t* A, const uint8_t* Wq, const uint16_t* Ws, float* C, int Bsz, int K, int N,
                         void* stream) {
     return run_gemm(BF_Q4_0_PLANES, Wq, Ws, A, K, C, N, BF_OUT_F32, Bsz, N, K, BF_ALGO_AUTO, stream);

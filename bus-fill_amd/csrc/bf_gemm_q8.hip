@@ -1,0 +1,334 @@
+// Integer-dot activation path: activations quantized to int8 per 32 values
+// (bf_quantize_q8), weights multiplied in with v_dot4_i32_i8.
+//
+// No counterpart in the reference's kernels (kernels/busfill_v1a.cu:41-104
+// multiplies fp16 activations by dequantized fp16 weights); its results credit
+// llama.cpp's quantized GEMM, which packs activations as int8 per 32 values and
+// spends one integer 4-way dot per four weights (RESULTS.md:72-77, 93-96).
+//
+// Quantized activations (one device buffer, regions contiguous):
+//   q [M][K] int8 | d [M][K/32] fp32 | s [M][K/32] int32
+// with d = amax/127 over the 32 values, q = round(x/d) (half away from zero,
+// 0 for an all-zero block) and s = sum of the block's q.
+//
+// GEMM: a lane owns one 64-weight unit (two 32-weight blocks; for Q4_K the two
+// sub-blocks sharing 32 code bytes) of four weight rows, and reuses each batch
+// row's 64 activation bytes over those four rows.  16 lanes (units) x 4 row
+// groups = 16 rows per workgroup; the workgroup's waves split the row's units.
+// The 4-bit codes enter the dot as bytes 0..15 (two masks per four code bytes),
+// so per 32-weight block b the exact integer dot_b = sum code*q, and
+//   C += d8_b * (scale_b * dot_b - offset_b * s_b)
+// in fp32 (Q4_0 and planes: scale = d, offset = 8d; Q4_K: scale = d*sc,
+// offset = dmin*m).  Lane sums reduce over the 16 unit lanes by butterfly and
+// over the waves through LDS, in a fixed order: results are deterministic.
+#include "bf_device.h"
+#include "bf_formats.h"
+#include "bf_launch.h"
+
+namespace bf {
+
+namespace {
+
+constexpr int kQ8Rows = 16;       // weight rows per workgroup
+constexpr int kQ8MaxWaves = 8;
+constexpr int kQ8MaxM = 16;
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+constexpr uint32_t kNib = 0x0F0F0F0Fu;
+
+// One unit of one row: wl[i] holds the four codes (bytes 0..15) that multiply
+// activation word a[i] (a[0..7] = block a, a[8..15] = block b), masked once per
+// unit and reused for every batch row.
+struct Q8Row {
+    uint32_t wl[16];
+    float sa, oa, sb, ob;
+    __device__ __forceinline__ void dots(const uint32_t a[16], int& da, int& db) const {
+        int x = 0, y = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            x = dot4(wl[i], a[i], x);
+            y = dot4(wl[8 + i], a[8 + i], y);
+        }
+        da = x; db = y;
+    }
+    // Q4_0 order within one 16-byte block: byte i = weights i (low), i+16 (high)
+    __device__ __forceinline__ void set_q40(const uint32_t* cw, uint32_t* out) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            out[t] = cw[t] & kNib;
+            out[4 + t] = (cw[t] >> 4) & kNib;
+        }
+    }
+};
+
+template <int QT>
+__device__ __forceinline__ void load_q8row(Q8Row& r, const uint8_t* W, const uint8_t* Waux, int64_t n, int j,
+                                           int K);
+
+// Q4_K: 32 code bytes (sub-block a = low nibbles, b = high nibbles) + header
+template <>
+__device__ __forceinline__ void load_q8row<QT_Q4_K>(Q8Row& r, const uint8_t* W, const uint8_t*, int64_t n, int j,
+                                                    int K) {
+    const uint8_t* base = W + n * ((int64_t)(K >> 8) * 144) + (int64_t)(j >> 2) * 144;
+    const int c = j & 3;
+    const u4 h = ld16(base), q0 = ld16(base + 16 + 32 * c), q1 = ld16(base + 32 + 32 * c);
+    const uint32_t cw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        r.wl[t] = cw[t] & kNib;
+        r.wl[8 + t] = (cw[t] >> 4) & kNib;
+    }
+    const float d = half_bits_to_float(h.x & 0xFFFFu), dmin = half_bits_to_float(h.x >> 16);
+    const uint32_t s3[3] = {h.y, h.z, h.w};
+    uint32_t sca, ma, scb, mb;
+    q4k_scale_min(s3, 2 * c, sca, ma);
+    q4k_scale_min(s3, 2 * c + 1, scb, mb);
+    r.sa = d * (float)sca; r.oa = dmin * (float)ma;
+    r.sb = d * (float)scb; r.ob = dmin * (float)mb;
+}
+
+// Q4_0: blocks 2j, 2j+1 = 36 bytes, 4-byte aligned: [d0][16 codes][d1][16 codes]
+template <>
+__device__ __forceinline__ void load_q8row<QT_Q4_0>(Q8Row& r, const uint8_t* W, const uint8_t*, int64_t n, int j,
+                                                    int K) {
+    const uint8_t* base = W + n * ((int64_t)(K >> 5) * 18) + (int64_t)j * 36;
+    const u4 a = ld16_a4(base), b = ld16_a4(base + 16);
+    const uint32_t c = *(const uint32_t*)(base + 32);
+    const uint32_t w[9] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c};
+    uint32_t cw[8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) cw[t] = __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2);   // bytes 2..17
+#pragma unroll
+    for (int t = 0; t < 4; t++) cw[4 + t] = w[5 + t];                                     // bytes 20..35
+    r.set_q40(cw, r.wl);
+    r.set_q40(cw + 4, r.wl + 8);
+    r.sa = half_bits_to_float(a.x & 0xFFFFu);
+    r.sb = half_bits_to_float(b.x >> 16);
+    r.oa = 8.f * r.sa; r.ob = 8.f * r.sb;
+}
+
+// planes: 32 code bytes, byte i = weights 2i (low) and 2i+1 (high); the
+// activation words of each block are regrouped as [even elements | odd elements]
+// (see k_gemm_q8), so the low nibbles meet words 0-3 and the high ones 4-7
+template <>
+__device__ __forceinline__ void load_q8row<QT_PLANES>(Q8Row& r, const uint8_t* W, const uint8_t* Waux, int64_t n,
+                                                      int j, int K) {
+    const uint8_t* base = W + n * (int64_t)(K >> 1) + (int64_t)j * 32;
+    const u4 q0 = ld16(base), q1 = ld16(base + 16);
+    const uint32_t cw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    r.set_q40(cw, r.wl);
+    r.set_q40(cw + 4, r.wl + 8);
+    const uint32_t sc = *(const uint32_t*)(Waux + 2 * (n * (int64_t)(K >> 5) + 2 * j));
+    r.sa = half_bits_to_float(sc & 0xFFFFu);
+    r.sb = half_bits_to_float(sc >> 16);
+    r.oa = 8.f * r.sa; r.ob = 8.f * r.sb;
+}
+
+}  // namespace
+
+// One thread per 8 activations, four threads per 32-value block.
+__global__ __launch_bounds__(256) void k_quantize_q8(const uint16_t* __restrict__ A, int lda,
+                                                     int8_t* __restrict__ q, float* __restrict__ d,
+                                                     int* __restrict__ s, int M, int K) {
+    const int64_t per_row = K >> 3, total = (int64_t)M * per_row;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool live = t < total;
+    const int64_t tt = live ? t : total - 1;    // total % 4 == 0: a block's four threads are all live or all not
+    const int64_t m = tt / per_row;
+    const int k = (int)(tt - m * per_row) << 3;
+    const h8 v = ld_act(A + m * lda + k);
+    float x[8], amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        x[i] = (float)v[i];
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
+    }
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 2, 64));
+    const float dd = amax / 127.0f;
+    int qi[8], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        qi[i] = amax == 0.f ? 0 : (int)__builtin_roundf(x[i] / dd);
+        sum += qi[i];
+    }
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if (live) {
+        uint32_t p0 = 0, p1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            p0 |= ((uint32_t)qi[i] & 0xFFu) << (8 * i);
+            p1 |= ((uint32_t)qi[4 + i] & 0xFFu) << (8 * i);
+        }
+        *(uint2*)(q + m * K + k) = make_uint2(p0, p1);
+        if ((k & 31) == 0) {
+            d[m * (K >> 5) + (k >> 5)] = dd;
+            s[m * (K >> 5) + (k >> 5)] = sum;
+        }
+    }
+}
+
+template <int QT, int MB>
+__global__ __launch_bounds__(64 * kQ8MaxWaves)
+void k_gemm_q8(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux, const int8_t* __restrict__ q,
+               const float* __restrict__ d8, const int* __restrict__ s8, void* __restrict__ C, int ldc, int out_f16,
+               int M, int N, int K) {
+    __shared__ float red[kQ8MaxWaves][kQ8Rows][MB];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int rg = lane >> 4, u = lane & 15;
+    const int nunits = K >> 6, nblk = K >> 5;
+    const int64_t row0 = (int64_t)blockIdx.x * kQ8Rows + 4 * rg;
+
+    float acc[4][MB];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int m = 0; m < MB; m++) acc[r][m] = 0.f;
+
+    for (int j = wave * 16 + u; j < nunits; j += nwaves * 16) {
+        Q8Row wu[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int64_t n = row0 + r < N ? row0 + r : (int64_t)N - 1;
+            load_q8row<QT>(wu[r], W, Waux, n, j, K);
+        }
+        // batch row m's 64 activation bytes, scales and sums; row m+1's are in
+        // flight while row m computes
+        auto fetch = [&](int m, u4* av, float2& dm, int2& sm) {
+            const int mm = m < M ? m : M - 1;
+            const int8_t* qa = q + (int64_t)mm * K + 64 * j;
+            av[0] = *(const u4*)qa;
+            av[1] = *(const u4*)(qa + 16);
+            av[2] = *(const u4*)(qa + 32);
+            av[3] = *(const u4*)(qa + 48);
+            dm = *(const float2*)(d8 + (int64_t)mm * nblk + 2 * j);
+            sm = *(const int2*)(s8 + (int64_t)mm * nblk + 2 * j);
+        };
+        u4 nav[4];
+        float2 ndm;
+        int2 nsm;
+        fetch(0, nav, ndm, nsm);
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+            uint32_t a[16] = {nav[0].x, nav[0].y, nav[0].z, nav[0].w, nav[1].x, nav[1].y, nav[1].z, nav[1].w,
+                              nav[2].x, nav[2].y, nav[2].z, nav[2].w, nav[3].x, nav[3].y, nav[3].z, nav[3].w};
+            const float2 dm = ndm;
+            const int2 sm = nsm;
+            if (m + 1 < MB) fetch(m + 1, nav, ndm, nsm);
+            if constexpr (QT == QT_PLANES) {
+                // per block: words 0-7 natural order -> 4 words of even elements, 4 of odd
+                uint32_t e[16];
+#pragma unroll
+                for (int b = 0; b < 2; b++)
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const uint32_t lo = a[8 * b + 2 * t], hi = a[8 * b + 2 * t + 1];
+                        e[8 * b + t] = perm_b32(hi, lo, 0x06040200u);
+                        e[8 * b + 4 + t] = perm_b32(hi, lo, 0x07050301u);
+                    }
+#pragma unroll
+                for (int i = 0; i < 16; i++) a[i] = e[i];
+            }
+            const float sfa = (float)sm.x, sfb = (float)sm.y;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int da, db;
+                wu[r].dots(a, da, db);
+                const float ta = __builtin_fmaf(wu[r].sa, (float)da, -wu[r].oa * sfa);
+                const float tb = __builtin_fmaf(wu[r].sb, (float)db, -wu[r].ob * sfb);
+                acc[r][m] = __builtin_fmaf(dm.x, ta, acc[r][m]);
+                acc[r][m] = __builtin_fmaf(dm.y, tb, acc[r][m]);
+            }
+        }
+    }
+
+    // butterfly over the 16 unit lanes of each row group, then the waves' sums
+    // through LDS in wave order
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+            float v = acc[r][m];
+            v += __shfl_xor(v, 1, 64);
+            v += __shfl_xor(v, 2, 64);
+            v += __shfl_xor(v, 4, 64);
+            v += __shfl_xor(v, 8, 64);
+            acc[r][m] = v;
+        }
+    if (u == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int m = 0; m < MB; m++) red[wave][4 * rg + r][m] = acc[r][m];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < kQ8Rows * MB; i += blockDim.x) {
+        const int rr = i / MB, m = i - rr * MB;
+        const int64_t n = (int64_t)blockIdx.x * kQ8Rows + rr;
+        float v = 0.f;
+        for (int w = 0; w < nwaves; w++) v += red[w][rr][m];
+        if (m < M && n < N) {
+            if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + n] = (_Float16)v;
+            else ((float*)C)[(int64_t)m * ldc + n] = v;
+        }
+    }
+}
+
+namespace {
+
+template <int QT, int MB>
+hipError_t launch_q8(const Q8Args& g, hipStream_t st) {
+    // waves per workgroup: as few passes over the units as 8 waves allow, then
+    // the fewest waves that keep that many passes
+    const int n16 = (g.K / 64 + 15) / 16;
+    const int passes = (n16 + kQ8MaxWaves - 1) / kQ8MaxWaves;
+    const int waves = (n16 + passes - 1) / passes;
+    const int8_t* q = (const int8_t*)g.Aq;
+    const float* d = (const float*)(q + (int64_t)g.M * g.K);
+    const int* s = (const int*)(d + (int64_t)g.M * (g.K / 32));
+    dim3 grid((unsigned)((g.N + kQ8Rows - 1) / kQ8Rows));
+    hipLaunchKernelGGL((k_gemm_q8<QT, MB>), grid, dim3(64 * waves), 0, st, g.W, g.Waux, q, d, s, g.C, g.ldc,
+                       g.out_f16, g.M, g.N, g.K);
+    return hipGetLastError();
+}
+
+template <int QT>
+hipError_t dispatch_q8_m(const Q8Args& g, hipStream_t st) {
+    if (g.M <= 1) return launch_q8<QT, 1>(g, st);
+    if (g.M <= 2) return launch_q8<QT, 2>(g, st);
+    if (g.M <= 4) return launch_q8<QT, 4>(g, st);
+    if (g.M <= 8) return launch_q8<QT, 8>(g, st);
+    return launch_q8<QT, 16>(g, st);
+}
+
+}  // namespace
+
+size_t q8_bytes(int M, int K) { return (size_t)M * K + (size_t)8 * M * (K / 32); }
+
+hipError_t quantize_q8(const uint16_t* A, int lda, void* Aq, int M, int K, hipStream_t st) {
+    int8_t* q = (int8_t*)Aq;
+    float* d = (float*)(q + (int64_t)M * K);
+    int* s = (int*)(d + (int64_t)M * (K / 32));
+    const int64_t threads = (int64_t)M * (K / 8);
+    hipLaunchKernelGGL(k_quantize_q8, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, A, lda, q, d, s, M,
+                       K);
+    return hipGetLastError();
+}
+
+bool q8_supports(int M, int K) { return M >= 1 && M <= kQ8MaxM && K % 64 == 0; }
+
+hipError_t gemm_q8(const Q8Args& g, hipStream_t st) {
+    if (!q8_supports(g.M, g.K)) return hipErrorNotSupported;
+    switch (g.qtype) {
+        case QT_Q4_K: return dispatch_q8_m<QT_Q4_K>(g, st);
+        case QT_Q4_0: return dispatch_q8_m<QT_Q4_0>(g, st);
+        case QT_PLANES: return dispatch_q8_m<QT_PLANES>(g, st);
+        default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace bf

@@ -48,4 +48,21 @@ hipError_t gemm_lds_swiglu(const GemmArgs& g, hipStream_t st);
 bool lds_swiglu_supports(const GemmArgs& g);
 hipError_t swiglu_f16(const uint16_t* gu, int ld, uint16_t* out, int ldo, int M, int K, hipStream_t st);
 
+// Integer-dot activation path: int8 activations per 32 values (q | d | s
+// regions of one buffer of q8_bytes(M, K)) and the v_dot4_i32_i8 GEMM.
+struct Q8Args {
+    int qtype;
+    const uint8_t* W;
+    const uint8_t* Waux;
+    const void* Aq;            // q8_bytes(M, K) bytes from quantize_q8
+    void* C;
+    int ldc;
+    int out_f16;
+    int M, N, K;               // M <= 16, K % 64 == 0
+};
+size_t q8_bytes(int M, int K);
+hipError_t quantize_q8(const uint16_t* A, int lda, void* Aq, int M, int K, hipStream_t st);
+bool q8_supports(int M, int K);
+hipError_t gemm_q8(const Q8Args& g, hipStream_t st);
+
 }  // namespace bf

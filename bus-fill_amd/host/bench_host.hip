@@ -243,6 +243,46 @@ int bfb_time_swiglu(int qtype, const void* const* W, const void* const* W_aux, i
     return 0;
 }
 
+// The integer-dot path against the fp16 GEMM over the same weight rotation:
+// mode 0 = bf_gemm on fp16 A, 1 = bf_quantize_q8 + bf_gemm_q8 (the whole
+// q8 path per GEMM), 2 = bf_gemm_q8 alone on Aq quantized beforehand.
+int bfb_time_q8(int qtype, const void* const* W, const void* const* W_aux, int count, const uint16_t* A,
+                void* Aq, void* C, int M, int N, int K, int mode, int warmup, int steps, void* stream,
+                double* ms_out) {
+    hipStream_t st = (hipStream_t)stream;
+    auto call = [&](int r) -> bf_status {
+        const void* w = W[r % count];
+        const void* aux = W_aux ? W_aux[r % count] : nullptr;
+        if (mode == 0) return bf_gemm((bf_qtype)qtype, w, aux, A, K, C, N, BF_OUT_F32, M, N, K, st);
+        if (mode == 1) {
+            bf_status s2 = bf_quantize_q8(A, K, Aq, M, K, st);
+            if (s2 != BF_OK) return s2;
+        }
+        return bf_gemm_q8((bf_qtype)qtype, w, aux, Aq, C, N, BF_OUT_F32, M, N, K, st);
+    };
+    if (mode == 2 && (g_bf = bf_quantize_q8(A, K, Aq, M, K, st)) != BF_OK) return -1;
+    for (int r = 0; r < warmup; r++)
+        if ((g_bf = call(r)) != BF_OK) return -1;
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    HCK(hipEventRecord(e0, st));
+    for (int r = 0; r < steps; r++)
+        if ((g_bf = call(r)) != BF_OK) {
+            (void)hipEventDestroy(e0);
+            (void)hipEventDestroy(e1);
+            return -1;
+        }
+    HCK(hipEventRecord(e1, st));
+    HCK(hipEventSynchronize(e1));
+    float ms;
+    HCK(hipEventElapsedTime(&ms, e0, e1));
+    *ms_out = ms;
+    HCK(hipEventDestroy(e0));
+    HCK(hipEventDestroy(e1));
+    return 0;
+}
+
 // Streaming reads of `bytes` per launch cycling through `count` buffers src[i]
 // (the weight rotation): the time one launch of that size takes to read its
 // bytes from HBM with nothing else to do.  Grid blocks x threads.

@@ -125,8 +125,8 @@ bf_status bf_dequant_f16(bf_qtype qtype, const void* W, const void* W_aux,
  * followed by bf_gemm, without the second launch or the intermediate
  * buffer.  Batch 1-2 (decode), with the activations resident in LDS
  * (K <= 17408 at batch 2); other shapes return BF_ERR_UNSUPPORTED.  No
- * counterpart in the reference, whose survey lists the fusion as a next step
- * after the GEMM (fusing SiLU-mul between the gate/up and down projections). */
+ * counterpart in the reference, which launches only the GEMM
+ * (kernels/busfill_v1a.cu:41-46). */
 bf_status bf_gemm_swiglu(bf_qtype qtype, const void* W, const void* W_aux,
                          const uint16_t* gate_up, int ld, void* C, int ldc, bf_otype otype,
                          int M, int N, int K, void* stream);
@@ -135,6 +135,32 @@ bf_status bf_gemm_swiglu(bf_qtype qtype, const void* W, const void* W_aux,
  * computed in fp32 as g / (1 + e^-g) * u.  K % 8 == 0; rows 16-byte aligned. */
 bf_status bf_swiglu_f16(const uint16_t* gate_up, int ld, uint16_t* out, int ldo,
                         int M, int K, void* stream);
+
+/* ---------------------------------------------------------------- integer-dot path
+ * Activations quantized to int8 per 32 values, multiplied in with a 4-way
+ * integer dot per four weights.  No counterpart in the reference's kernels;
+ * its results (RESULTS.md:72-77, 93-96) credit llama.cpp's quantized GEMM
+ * (quantize_q8_1 + dp4a vec-dots) with this activation form.  Not bit-equal
+ * to bf_gemm: each activation moves by at most half its block's step d/2
+ * (d = amax/127), so |C_q8 - C_fp16| <= sum_k |W[n][k]| * d_blk(k) / 2. */
+
+/* Bytes of the quantized-activation buffer for M rows of K (K % 32 == 0):
+ * q[M][K] int8, then d[M][K/32] fp32, then s[M][K/32] int32, contiguous.
+ * Returns 0 for an invalid shape. */
+size_t bf_q8_bytes(int M, int K);
+
+/* Aq = quantize(A[M][lda] fp16) per 32-value block, as llama.cpp's
+ * quantize_q8_1: d = amax/127, q = round(x/d) half away from zero (all zero
+ * for an all-zero block), s = sum of the block's q (an exact integer; this
+ * build keeps d in fp32).  A rows and Aq 16-byte aligned. */
+bf_status bf_quantize_q8(const uint16_t* A, int lda, void* Aq, int M, int K, void* stream);
+
+/* C[M][N] = sum over 32-blocks b of d_b * (scale * dot_b - offset * s_b), the
+ * integer dots exact, over the weights in place (any of the three formats).
+ * M = 1..16, K % 64 == 0, W and Aq 16-byte aligned; other shapes return
+ * BF_ERR_UNSUPPORTED. */
+bf_status bf_gemm_q8(bf_qtype qtype, const void* W, const void* W_aux, const void* Aq, void* C, int ldc,
+                     bf_otype otype, int M, int N, int K, void* stream);
 
 /* ---------------------------------------------------------------- GGUF files
  * A reader of llama.cpp's model files (GGUF versions 2 and 3, public

@@ -247,3 +247,103 @@ def gate(C, C_ref, max_abs: float = 0.6, rel_frob: float = 1e-3):
     denom = float(np.linalg.norm(C_ref))
     rfe = float(np.linalg.norm(diff)) / denom if denom > 0 else float(np.linalg.norm(diff))
     return (mae <= max_abs and rfe <= rel_frob), mae, rfe, 0
+
+
+# ---------------------------------------------------------------- q8 activations
+# Integer-dot activation path.  No counterpart in the reference's own kernels:
+# its results credit llama.cpp's quantized-GEMM path (pinned clone
+# Ajay9o9/llama.cpp @ d493f84, RESULTS.md:244) with packing the activations as
+# int8 per 32 values and multiplying them with one integer 4-way dot per four
+# weights (RESULTS.md:72-77, 93-96).  Restated from llama.cpp's published
+# quantize_q8_1 (ggml-cuda quantize.cu): amax = max|x| over the block,
+# d = amax / 127, q = round(x / d) (half away from zero; 0 when amax = 0).  This
+# build keeps d in fp32 (llama.cpp stores it as fp16) and the block's sum as the
+# exact integer sum of q (llama.cpp keeps a float sum).  Pinned in
+# tests/test_oracle.py by closed forms: d = 1 blocks whose q are the rounded
+# inputs (ties away from zero), amax -> +-127, the error bound |x - d q| <= d/2,
+# the all-zero block, and integer dots against brute force.
+
+
+def quantize_q8(A: np.ndarray):
+    """A[M][K] fp16 bits -> (q int8 [M][K], d float32 [M][K/32], s int32 [M][K/32])."""
+    A = np.ascontiguousarray(A, np.uint16)
+    M, K = A.shape
+    assert K % 32 == 0
+    x = A.view(np.float16).astype(np.float32).reshape(M, K // 32, 32)
+    amax = np.abs(x).max(axis=-1)
+    d = (amax / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        y = (x / d[..., None]).astype(np.float64)     # fp32 quotient, then exact rounding in fp64
+    q = np.where(amax[..., None] == 0, 0.0, np.sign(y) * np.floor(np.abs(y) + 0.5)).astype(np.int8)
+    s = q.astype(np.int32).sum(axis=-1).astype(np.int32)
+    return q.reshape(M, K), d, s
+
+
+def q8_pack(q, d, s) -> np.ndarray:
+    """The device buffer of bf_quantize_q8: q [M][K] int8, then d [M][K/32]
+    float32, then s [M][K/32] int32, each region contiguous."""
+    return np.concatenate([np.ascontiguousarray(q).view(np.uint8).ravel(),
+                           np.ascontiguousarray(d, np.float32).view(np.uint8).ravel(),
+                           np.ascontiguousarray(s, np.int32).view(np.uint8).ravel()])
+
+
+def q8_unpack(buf: np.ndarray, M: int, K: int):
+    buf = np.ascontiguousarray(buf).view(np.uint8).ravel()
+    nq, nb = M * K, M * (K // 32)
+    q = buf[:nq].view(np.int8).reshape(M, K)
+    d = buf[nq:nq + 4 * nb].view(np.float32).reshape(M, K // 32)
+    s = buf[nq + 4 * nb:nq + 8 * nb].view(np.int32).reshape(M, K // 32)
+    return q, d, s
+
+
+def weight_codes(w: QWeights):
+    """(codes uint8 [N][K] in 0..15, scale f64 [N][K/32], offset f64 [N][K/32])
+    with dequant(W)[n][k] = scale * code - offset for the block of k: Q4_0 and
+    planes offset = 8 d, Q4_K scale = d sc and offset = dmin m of the
+    sub-block (byte layouts as in oracle.c's dequant_row_f32)."""
+    N, K = w.N, w.K
+    if w.qtype == Q4_0_PLANES:
+        b = w.W.reshape(N, K // 2)
+        codes = np.stack([b & 15, b >> 4], axis=-1).reshape(N, K)
+        dd = f16_bits_to_f32(w.W_aux.reshape(N, K // 32)).astype(np.float64)
+        return codes, dd, 8 * dd
+    if w.qtype == Q4_0:
+        blk = w.W.reshape(N, K // 32, 18)
+        qs = blk[:, :, 2:]
+        codes = np.concatenate([qs & 15, qs >> 4], axis=-1).reshape(N, K)
+        dd = f16_bits_to_f32(blk[:, :, 0].astype(np.uint16) | (blk[:, :, 1].astype(np.uint16) << 8))
+        dd = dd.astype(np.float64)
+        return codes, dd, 8 * dd
+    blk = w.W.reshape(N, K // 256, 144)
+    d = f16_bits_to_f32(blk[:, :, 0].astype(np.uint16) | (blk[:, :, 1].astype(np.uint16) << 8)).astype(np.float64)
+    dmin = f16_bits_to_f32(blk[:, :, 2].astype(np.uint16) | (blk[:, :, 3].astype(np.uint16) << 8)).astype(np.float64)
+    sb = blk[:, :, 4:16].astype(np.int32)
+    sc = np.empty((N, K // 256, 8), np.int32)
+    mn = np.empty((N, K // 256, 8), np.int32)
+    for j in range(8):     # ggml get_scale_min_k4
+        if j < 4:
+            sc[:, :, j] = sb[:, :, j] & 63
+            mn[:, :, j] = sb[:, :, j + 4] & 63
+        else:
+            sc[:, :, j] = (sb[:, :, j + 4] & 0xF) | ((sb[:, :, j - 4] >> 6) << 4)
+            mn[:, :, j] = (sb[:, :, j + 4] >> 4) | ((sb[:, :, j] >> 6) << 4)
+    qs = blk[:, :, 16:].reshape(N, K // 256, 4, 32)
+    codes = np.stack([qs & 15, qs >> 4], axis=3).reshape(N, K)
+    return codes, (d[..., None] * sc).reshape(N, K // 32), (dmin[..., None] * mn).reshape(N, K // 32)
+
+
+def gemm_q8(w: QWeights, q, d, s):
+    """C[M][N] of the integer-dot path in fp64, and the sum of the magnitudes of
+    its terms (for a forward-error bound):
+        C[m][n] = sum_b d8[m][b] * (scale[n][b] * dot_b - offset[n][b] * s[m][b]),
+        dot_b = sum_{k in b} code[n][k] * q[m][k]   (exact integers)."""
+    codes, scale, offset = weight_codes(w)
+    M, K = q.shape
+    nb = K // 32
+    qb = q.astype(np.int64).reshape(M, nb, 32)
+    cb = codes.astype(np.int64).reshape(w.N, nb, 32)
+    dots = np.einsum("mbk,nbk->mnb", qb, cb)                        # exact int64
+    d8 = d.astype(np.float64)[:, None, :]
+    t1 = d8 * scale[None] * dots
+    t2 = d8 * offset[None] * s.astype(np.float64)[:, None, :]
+    return (t1 - t2).sum(-1), (np.abs(t1) + np.abs(t2)).sum(-1)

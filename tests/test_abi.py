@@ -142,3 +142,27 @@ def test_swiglu_entries_reject_before_any_launch():
     assert L.bf_swiglu_f16(FAKE, 2 * K, FAKE, K, 1, 12, None) == bf.ERR_INVALID
     assert L.bf_swiglu_f16(FAKE, K, FAKE, K, 1, K, None) == bf.ERR_INVALID
     assert L.bf_swiglu_f16(FAKE, 2 * K, FAKE + 8, K, 1, K, None) == bf.ERR_INVALID
+
+
+def test_q8_entries_reject_before_any_launch():
+    """bf_q8_bytes / bf_quantize_q8 / bf_gemm_q8 argument checks (no GPU needed:
+    every call below is rejected before a launch)."""
+    L = bf.lib()
+    N, K = 64, 512
+    assert L.bf_q8_bytes(3, 512) == 3 * 512 + 8 * 3 * 16
+    assert L.bf_q8_bytes(0, 512) == 0 and L.bf_q8_bytes(1, 48) == 0
+    assert L.bf_quantize_q8(None, K, FAKE, 1, K, None) == bf.ERR_INVALID
+    assert L.bf_quantize_q8(FAKE, K, FAKE, 1, 48, None) == bf.ERR_INVALID
+    assert L.bf_quantize_q8(FAKE, K - 8, FAKE, 1, K, None) == bf.ERR_INVALID
+    assert L.bf_quantize_q8(FAKE + 8, K, FAKE, 1, K, None) == bf.ERR_INVALID
+    assert L.bf_quantize_q8(FAKE, K + 4, FAKE, 2, K, None) == bf.ERR_INVALID
+    assert L.bf_quantize_q8(FAKE, K, FAKE + 4, 1, K, None) == bf.ERR_INVALID
+    assert L.bf_gemm_q8(bf.Q4_K, FAKE, None, FAKE, FAKE, N, bf.OUT_F32, 17, N, K, None) == bf.ERR_UNSUPPORTED
+    assert "batch 1-16" in L.bf_last_error().decode()
+    assert L.bf_gemm_q8(bf.Q4_0, FAKE, None, FAKE, FAKE, N, bf.OUT_F32, 2, N, 96, None) == bf.ERR_UNSUPPORTED
+    assert L.bf_gemm_q8(bf.Q4_K, FAKE, None, None, FAKE, N, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
+    assert L.bf_gemm_q8(bf.Q4_K, FAKE, None, FAKE + 4, FAKE, N, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
+    assert L.bf_gemm_q8(bf.Q4_K, FAKE + 4, None, FAKE, FAKE, N, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
+    assert L.bf_gemm_q8(bf.Q4_K, FAKE, None, FAKE, FAKE, N - 1, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
+    assert L.bf_gemm_q8(bf.Q4_0_PLANES, FAKE, None, FAKE, FAKE, N, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
+    assert L.bf_gemm_q8(bf.Q4_K, FAKE, None, FAKE, FAKE, N, 7, 1, N, K, None) == bf.ERR_INVALID

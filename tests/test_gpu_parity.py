@@ -644,3 +644,80 @@ def test_gemm_swiglu_refuses_shapes_it_does_not_fuse(dev):
     with pytest.raises(bf.BusfillError) as err:
         bf.gemm_swiglu(O.Q4_K, dw[0], None, gud, C, 3, 256, 1024)
     assert err.value.status == bf.ERR_UNSUPPORTED
+
+
+# ---------------------------------------------------------------- integer-dot path
+def gpu_quantize_q8(A, dev):
+    M, K = A.shape
+    Ad = to_dev(A, dev)
+    Aq = torch.full((bf.q8_bytes(M, K),), 0xAB, dtype=torch.uint8, device=dev)
+    bf.quantize_q8(Ad, Aq, M, K)
+    torch.cuda.synchronize()
+    return Aq
+
+
+def q8_special_rows(K):
+    """Rows with an all-zero block, a d = 1 block of ties (x.5 values), and tiny values."""
+    rows = np.zeros((3, K), np.float16)
+    rows[1, :32] = np.array([127, -127, 0.5, -0.5, 1.5, 2.5, -2.5, 126.5] * 4, np.float16)
+    rows[2, :] = np.float16(6e-8) * np.arange(K).astype(np.float16) % 7
+    return rows.view(np.uint16)
+
+
+@pytest.mark.parametrize("M,K", [(1, 64), (5, 4096), (16, 5120)])
+def test_quantize_q8_bitexact(dev, M, K):
+    A = O.gen_act(M, K, 31 + M)
+    A[: min(M, 3)] = q8_special_rows(K)[: min(M, 3)]
+    Aq = gpu_quantize_q8(A, dev).cpu().numpy()
+    assert (Aq == O.q8_pack(*O.quantize_q8(A))).all()
+
+
+@pytest.mark.parametrize("qt", QTS)
+@pytest.mark.parametrize("M,N,K", [(1, 40, 1024), (2, 300, 1536), (3, 64, 5120), (5, 129, 2048),
+                                   (8, 512, 1024), (11, 200, 768), (16, 256, 2560)])
+def test_gemm_q8_parity(dev, qt, M, N, K):
+    """Integer-dot GEMM against the oracle's restatement: the integer dots are
+    exact, the fp32 scale terms and sums within (K/32 + 32) * 2^-24 of the sum
+    of the terms' magnitudes; and within half a quantization step of the fp16
+    activation GEMM (sum_k |W| d/2)."""
+    w = O.gen_weights(qt, N, K, 100 + M)
+    A = O.gen_act(M, K, 200 + N)
+    Aq = gpu_quantize_q8(A, dev)
+    Wd, auxd = upload(w, dev)
+    C = torch.full((M, N), float("nan"), device=dev)
+    bf.gemm_q8(qt, Wd, auxd, Aq, C, M, N, K)
+    torch.cuda.synchronize()
+    Cg = C.cpu().numpy().astype(np.float64)
+    q, d, s = O.quantize_q8(A)
+    ref, mag = O.gemm_q8(w, q, d, s)
+    assert np.isfinite(Cg).all()
+    tol = (K / 32 + 32) * 2.0 ** -24 * mag + 1e-30
+    assert (np.abs(Cg - ref) <= tol).all(), f"worst excess {float((np.abs(Cg - ref) / tol).max())}"
+    half_step = d.astype(np.float64).repeat(32, axis=1) / 2
+    bound = half_step @ np.abs(O.dequant_f32(w).astype(np.float64)).T
+    assert (np.abs(Cg - O.gemm_f64(w, A)) <= bound * (1 + 1e-4) + tol).all()
+
+
+def test_gemm_q8_full_size_strided_f16_and_deterministic(dev):
+    """Q4_K 5120 x 5120 at batch 16 into an fp16 output with ldc > N: rows
+    beyond M and columns beyond N untouched, values within the oracle's bound
+    plus one fp16 rounding, two runs bit-identical."""
+    M, N, K = 16, 5120, 5120
+    w = O.gen_weights(O.Q4_K, N, K, 77)
+    A = O.gen_act(M, K, 78)
+    Aq = gpu_quantize_q8(A, dev)
+    Wd, auxd = upload(w, dev)
+    ldc = N + 8
+    outs = []
+    for _ in range(2):
+        C = torch.full((M + 1, ldc), 7.0, device=dev, dtype=torch.float16)
+        bf.gemm_q8(O.Q4_K, Wd, auxd, Aq, C, M, N, K, ldc=ldc, otype=bf.OUT_F16)
+        torch.cuda.synchronize()
+        outs.append(C.cpu().numpy())
+    assert (outs[0].view(np.uint16) == outs[1].view(np.uint16)).all()
+    C = outs[0]
+    assert (C[M] == 7).all() and (C[:M, N:] == 7).all()
+    q, d, s = O.quantize_q8(A)
+    ref, mag = O.gemm_q8(w, q, d, s)
+    tol = (K / 32 + 32) * 2.0 ** -24 * mag + np.abs(ref) * 2.0 ** -11 + 6e-8
+    assert (np.abs(C[:M, :N].astype(np.float64) - ref) <= tol).all()

@@ -358,3 +358,80 @@ def test_swiglu_closed_forms_and_float64():
     assert (got[~fin] == ref[~fin]).all()                 # products beyond fp16: the same infinity
     ulp = np.spacing(np.abs(ref[fin]).astype(np.float16)).astype(np.float64)
     assert (np.abs(got[fin] - ref[fin]) <= ulp).all()
+
+
+# ---------------------------------------------------------------- q8 activations
+def _f16(vals):
+    return np.asarray(vals, np.float16).view(np.uint16)
+
+
+def test_quantize_q8_closed_forms():
+    """d = 1 blocks (amax = 127): q is the input rounded half away from zero --
+    2.5 -> 3 and -2.5 -> -3 (round-to-even would give 2), the largest fp16
+    below 0.5 -> 0 (a float32 |y| + 0.5 would round up to 1) -- and the
+    all-zero block gives q = d = s = 0."""
+    below_half = float(np.nextafter(np.float16(0.5), np.float16(0)))
+    vals = [127, -127, 0.5, -0.5, 1.5, 2.5, -2.5, below_half, -below_half, 126.5, -126.5, 3, -3, 0, 64.25, -0.75]
+    vals += [0.0] * (32 - len(vals))
+    expect = [127, -127, 1, -1, 2, 3, -3, 0, 0, 127, -127, 3, -3, 0, 64, -1] + [0] * 16
+    A = np.stack([_f16(vals), _f16(np.zeros(32))])
+    q, d, s = O.quantize_q8(A)
+    assert d[0, 0] == np.float32(1.0) and d[1, 0] == 0
+    assert q[0].tolist() == expect
+    assert s[0, 0] == sum(expect) and s[1, 0] == 0 and not q[1].any()
+
+
+def test_quantize_q8_invariants():
+    """Random blocks: the largest magnitude maps to +-127, every |x - d q| <=
+    d/2 (up to the fp32 quotient's rounding), |q| <= 127 and s = sum q."""
+    A = O.gen_act(7, 4096, 11)
+    A[3, 64:96] = _f16(np.linspace(-1e-3, 2e-3, 32))       # a small-scale block
+    q, d, s = O.quantize_q8(A)
+    x = A.view(np.float16).astype(np.float64).reshape(7, 128, 32)
+    qb = q.astype(np.int64).reshape(7, 128, 32)
+    imax = np.abs(x).argmax(-1)
+    assert (np.abs(np.take_along_axis(qb, imax[..., None], -1)) == 127).all()
+    err = np.abs(x - d[..., None].astype(np.float64) * qb)
+    assert (err <= d[..., None] * (0.5 + 1e-5)).all()
+    assert np.abs(qb).max() <= 127 and (s == qb.sum(-1)).all()
+    # pack / unpack round trip
+    q2, d2, s2 = O.q8_unpack(O.q8_pack(q, d, s), 7, 4096)
+    assert (q2 == q).all() and (d2 == d).all() and (s2 == s).all()
+
+
+@pytest.mark.parametrize("qt", [O.Q4_0_PLANES, O.Q4_0, O.Q4_K])
+def test_gemm_q8_equals_dequant_route(qt):
+    """The integer-dot restatement (codes, scale*dot - offset*s) equals the
+    float64 matmul of the quantized activations d*q with the C oracle's fp32
+    dequant (a different route to the same number), and differs from the fp16
+    activation GEMM by at most sum_k |W[n][k]| * d_blk(k) / 2."""
+    M, N, K = 3, 24, 512
+    w = O.gen_weights(qt, N, K, 5)
+    A = O.gen_act(M, K, 6)
+    q, d, s = O.quantize_q8(A)
+    C, mag = O.gemm_q8(w, q, d, s)
+    Wf = O.dequant_f32(w).astype(np.float64)
+    xq = (d.astype(np.float64).repeat(32, axis=1)) * q.astype(np.float64)
+    ref = xq @ Wf.T
+    assert np.abs(C - ref).max() <= 1e-12 * mag.max()
+    half_step = d.astype(np.float64).repeat(32, axis=1) / 2
+    bound = half_step @ np.abs(Wf).T
+    assert (np.abs(C - O.gemm_f64(w, A)) <= bound * (1 + 1e-5) + 1e-12).all()
+
+
+def test_gemm_q8_brute_force_tiny():
+    """One output by explicit loops over the byte layout of Q4_0 (block d,
+    code = nibble - 8) against gemm_q8."""
+    K = 64
+    w = O.gen_weights(O.Q4_0, 1, K, 9)
+    A = O.gen_act(1, K, 10)
+    q, d, s = O.quantize_q8(A)
+    blk = w.W.reshape(K // 32, 18)
+    total = 0.0
+    for b in range(K // 32):
+        db = float(np.frombuffer(blk[b, :2].tobytes(), np.float16)[0])
+        for i in range(16):
+            lo, hi = int(blk[b, 2 + i]) & 15, int(blk[b, 2 + i]) >> 4
+            total += float(d[0, b]) * db * ((lo - 8) * int(q[0, 32 * b + i]) + (hi - 8) * int(q[0, 32 * b + 16 + i]))
+    C, _ = O.gemm_q8(w, q, d, s)
+    assert abs(C[0, 0] - total) <= 1e-12 * max(1.0, abs(total))
