@@ -82,12 +82,17 @@ __device__ __forceinline__ void load_q8row<QT_Q4_K>(Q8Row& r, const uint8_t* W, 
         r.wl[8 + t] = (cw[t] >> 4) & kNib;
     }
     const float d = half_bits_to_float(h.x & 0xFFFFu), dmin = half_bits_to_float(h.x >> 16);
-    const uint32_t s3[3] = {h.y, h.z, h.w};
-    uint32_t sca, ma, scb, mb;
-    q4k_scale_min(s3, 2 * c, sca, ma);
-    q4k_scale_min(s3, 2 * c + 1, scb, mb);
-    r.sa = d * (float)sca; r.oa = dmin * (float)ma;
-    r.sb = d * (float)scb; r.ob = dmin * (float)mb;
+    // (scale, min) of sub-blocks 2c and 2c+1 without divergent branches (c
+    // differs between lanes): both forms of ggml get_scale_min_k4, then a select
+    const uint32_t s0 = h.y, s1 = h.z, s2 = h.w;
+    const uint32_t sh = 16u * (uint32_t)(c & 1);
+    const uint32_t lo_sc = (s0 >> sh) & 0x3F3Fu, lo_m = (s1 >> sh) & 0x3F3Fu;   // c < 2: bytes 2c, 2c+1
+    const uint32_t b2 = (s2 >> sh) & 0xFFFFu;
+    const uint32_t hi_sc = (b2 & 0x0F0Fu) | (((s0 >> sh) >> 2) & 0x3030u);       // c >= 2
+    const uint32_t hi_m = ((b2 >> 4) & 0x0F0Fu) | (((s1 >> sh) >> 2) & 0x3030u);
+    const uint32_t scp = c < 2 ? lo_sc : hi_sc, mp = c < 2 ? lo_m : hi_m;
+    r.sa = d * (float)(scp & 0xFFu); r.oa = dmin * (float)(mp & 0xFFu);
+    r.sb = d * (float)(scp >> 8); r.ob = dmin * (float)(mp >> 8);
 }
 
 // Q4_0: blocks 2j, 2j+1 = 36 bytes, 4-byte aligned: [d0][16 codes][d1][16 codes]
@@ -176,12 +181,22 @@ template <int QT, int MB>
 __global__ __launch_bounds__(64 * kQ8MaxWaves)
 void k_gemm_q8(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux, const int8_t* __restrict__ q,
                const float* __restrict__ d8, const int* __restrict__ s8, void* __restrict__ C, int ldc, int out_f16,
-               int M, int N, int K) {
+               int Mall, int N, int K, int nx, int ny) {
     __shared__ float red[kQ8MaxWaves][kQ8Rows][MB];
+    // block b -> (row block x, batch group y): the ny groups of one row block sit
+    // 8 blocks apart, i.e. on the same XCD, so its L2 serves the weights' reuse
+    const int b = blockIdx.x, per = 8 * ny;
+    const int y = (b % per) >> 3, x = (b / per) * 8 + (b & 7);
+    if (x >= nx) return;                                       // whole workgroup, before any barrier
+    const int m0 = y * MB, M = min(MB, Mall - m0);
+    q += (int64_t)m0 * K;
+    d8 += (int64_t)m0 * (K >> 5);
+    s8 += (int64_t)m0 * (K >> 5);
+    C = (uint8_t*)C + (int64_t)m0 * ldc * (out_f16 ? 2 : 4);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int rg = lane >> 4, u = lane & 15;
     const int nunits = K >> 6, nblk = K >> 5;
-    const int64_t row0 = (int64_t)blockIdx.x * kQ8Rows + 4 * rg;
+    const int64_t row0 = (int64_t)x * kQ8Rows + 4 * rg;
 
     float acc[4][MB];
 #pragma unroll
@@ -268,7 +283,7 @@ void k_gemm_q8(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux, 
     __syncthreads();
     for (int i = threadIdx.x; i < kQ8Rows * MB; i += blockDim.x) {
         const int rr = i / MB, m = i - rr * MB;
-        const int64_t n = (int64_t)blockIdx.x * kQ8Rows + rr;
+        const int64_t n = (int64_t)x * kQ8Rows + rr;
         float v = 0.f;
         for (int w = 0; w < nwaves; w++) v += red[w][rr][m];
         if (m < M && n < N) {
@@ -290,19 +305,20 @@ hipError_t launch_q8(const Q8Args& g, hipStream_t st) {
     const int8_t* q = (const int8_t*)g.Aq;
     const float* d = (const float*)(q + (int64_t)g.M * g.K);
     const int* s = (const int*)(d + (int64_t)g.M * (g.K / 32));
-    dim3 grid((unsigned)((g.N + kQ8Rows - 1) / kQ8Rows));
+    const int nx = (g.N + kQ8Rows - 1) / kQ8Rows, ny = (g.M + MB - 1) / MB;
+    dim3 grid((unsigned)(((nx + 7) / 8) * 8 * ny));
     hipLaunchKernelGGL((k_gemm_q8<QT, MB>), grid, dim3(64 * waves), 0, st, g.W, g.Waux, q, d, s, g.C, g.ldc,
-                       g.out_f16, g.M, g.N, g.K);
+                       g.out_f16, g.M, g.N, g.K, nx, ny);
     return hipGetLastError();
 }
 
 template <int QT>
 hipError_t dispatch_q8_m(const Q8Args& g, hipStream_t st) {
+    // batches above 4 run as groups of 4 rows (more batch rows per workgroup
+    // cost registers, and with them the second workgroup per CU)
     if (g.M <= 1) return launch_q8<QT, 1>(g, st);
     if (g.M <= 2) return launch_q8<QT, 2>(g, st);
-    if (g.M <= 4) return launch_q8<QT, 4>(g, st);
-    if (g.M <= 8) return launch_q8<QT, 8>(g, st);
-    return launch_q8<QT, 16>(g, st);
+    return launch_q8<QT, 4>(g, st);
 }
 
 }  // namespace
