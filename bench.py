@@ -453,8 +453,9 @@ def main():
     args.algo_id = {"auto": 0, "mfma": 1, "dot2": 2, "simple": 3, "lds": 4, "slab": 5, "split": 6}[args.algo]
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build runs the GEMM on a single MI355X and has no "
-              "multi-GPU path (see the sharding note in DESIGN.md); run it with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: the GEMM runs on a single MI355X and there is no "
+              "multi-GPU path (sharding would split N across GPUs, one independent GEMM each); "
+              "run it with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
