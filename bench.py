@@ -2,11 +2,14 @@
 """Benchmark of the batched int4-block GEMM on one MI355X.
 
 Default run (the headline metric): Q4_K weights, N = K = 5120, batch M = 1, 8
-and 32, one GEMM per step, cycling through >= 1 GB of distinct weight matrices
-already resident in HBM (so the 256 MB Infinity Cache cannot serve them).
-Timing is hipEvents recorded on the launch stream around exactly --steps GEMMs
-(after --warmup untimed ones), issued back to back by the C++ bench host
-(bus-fill_amd/host/bench_host.hip) through the libbusfill C-ABI.
+and 32.  A step is one pass over a rotation of >= 1 GB of distinct weight
+matrices already resident in HBM (72 matrices of 14.7 MB at 5120^2, so the
+256 MB Infinity Cache cannot serve them): one GEMM per matrix.  Timing is
+hipEvents recorded on the launch stream around exactly --steps passes (after
+--warmup untimed ones); the timed GEMMs continue the rotation where the warmup
+stopped, so no timed GEMM finds its matrix in a cache.  The GEMMs are issued
+back to back by the C++ bench host (bus-fill_amd/host/bench_host.hip) through
+the libbusfill C-ABI.
 
 Prints ONE JSON line.  `value` is the weight-stream GB/s at M = 1
 (N*K*9/16 bytes / time per GEMM); `per_batch` carries M = 8 and 32; `roofline`
@@ -130,6 +133,8 @@ def stream_handle():
 
 
 def time_gemm(L, rot, M, steps, warmup, graph, algo, dev, seed=7):
+    """ms for steps * rot.count GEMMs (steps passes over the rotation) after
+    warmup passes."""
     import torch
     torch.manual_seed(seed)
     A = torch.randn((M, rot.K), device=dev).half()
@@ -138,7 +143,8 @@ def time_gemm(L, rot, M, steps, warmup, graph, algo, dev, seed=7):
     ms = ctypes.c_double()
     torch.cuda.synchronize()
     rc = L.bfb_time_gemms(QT[rot.fmt], P(W), P(aux), rot.count, A.data_ptr(), rot.K, C.data_ptr(), rot.N, 0,
-                          M, rot.N, rot.K, algo, warmup, steps, int(graph), stream_handle(), ctypes.byref(ms))
+                          M, rot.N, rot.K, algo, warmup * rot.count, steps * rot.count, int(graph), stream_handle(),
+                          ctypes.byref(ms))
     torch.cuda.synchronize()
     if rc != 0:
         raise RuntimeError("bench host: " + L.bfb_last_error().decode())
@@ -148,11 +154,13 @@ def time_gemm(L, rot, M, steps, warmup, graph, algo, dev, seed=7):
 
 
 def gemm_record(rot, M, ms, steps, graph):
-    t = ms / 1e3 / steps
+    """Per-GEMM figures from ms for `steps` passes over the rotation."""
+    t = ms / 1e3 / (steps * rot.count)
     alg = rot.wbytes + M * rot.K * 2 + M * rot.N * 4
     flops = 2.0 * M * rot.N * rot.K
     return {
-        "M": M, "us_per_gemm": round(t * 1e6, 4),
+        "M": M, "us_per_gemm": round(t * 1e6, 4), "ms_per_pass": round(t * rot.count * 1e3, 5),
+        "gemms_timed": steps * rot.count,
         "weight_GBps": round(rot.wbytes / t / 1e9, 2),
         "tok_s": round(M / t, 1),
         "alg_GBps": round(alg / t / 1e9, 2),
@@ -186,11 +194,11 @@ def read_floor(L, rot, steps, warmup):
     best_us, best_grid = None, None
     for blocks, threads in READ_GRIDS:
         ms = ctypes.c_double()
-        rc = L.bfb_read_slices(P(W), rot.count, rot.wbytes // 16 * 16, blocks, threads, warmup, steps,
-                               sink.data_ptr(), stream_handle(), ctypes.byref(ms))
+        rc = L.bfb_read_slices(P(W), rot.count, rot.wbytes // 16 * 16, blocks, threads, warmup * rot.count,
+                               steps * rot.count, sink.data_ptr(), stream_handle(), ctypes.byref(ms))
         if rc != 0:
             raise RuntimeError("bench host: " + L.bfb_last_error().decode())
-        us = ms.value * 1e3 / steps
+        us = ms.value * 1e3 / (steps * rot.count)
         if best_us is None or us < best_us:
             best_us, best_grid = us, (blocks, threads)
     return {"us_per_launch": round(best_us, 4), "GBps": round(rot.wbytes / (best_us / 1e6) / 1e9, 1),
@@ -199,9 +207,17 @@ def read_floor(L, rot, steps, warmup):
 
 # ------------------------------------------------------------------ CPU baseline
 def cpu_threads():
-    n = os.cpu_count() or 1
-    cap = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
-    return max(1, min(n, cap))
+    """Host threads for the CPU baseline: every CPU this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets it (the CPU share a job
+    is granted on a shared host).  Returns (threads, cpus in the affinity mask,
+    the OMP_NUM_THREADS text or None)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    n = min(avail, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else avail
+    return max(1, n), avail, cap
 
 
 def cpu_model():
@@ -225,7 +241,8 @@ def cpu_baseline(fmt, N, K, M, seconds):
     A = O.gen_act(M, K, seed=2025)
     scratch = np.empty(N * K, np.float32)
     out = {}
-    for label, threads, budget in (("all", cpu_threads(), seconds), ("one", 1, max(2.0, seconds / 3))):
+    nthreads, avail, cap = cpu_threads()
+    for label, threads, budget in (("all", nthreads, seconds), ("one", 1, max(2.0, seconds / 3))):
         O.cpu_dequant_matmul(w, A, threads=threads, scratch=scratch)          # warm
         n, tdq, tmm = 0, 0.0, 0.0
         t0 = time.perf_counter()
@@ -244,7 +261,8 @@ def cpu_baseline(fmt, N, K, M, seconds):
             "sample": (f"{fmt} N={N} K={K} M={M}: {a['calls']} dequantize-then-matmul calls in "
                        f"{a['seconds']} s on {a['threads']} threads ({cpu_model()})"),
             "tok_s": a["tok_s"], "ms_per_call": a["ms_per_call"], "ms_dequant": a["ms_dequant"],
-            "ms_matmul": a["ms_matmul"], "one_thread": out["one"]}
+            "ms_matmul": a["ms_matmul"], "one_thread": out["one"],
+            "host_cpus": os.cpu_count(), "affinity_cpus": avail, "omp_num_threads": cap, "cpu_model": cpu_model()}
 
 
 def traffic_from_profiles(key):
@@ -298,8 +316,7 @@ def run_layer(L, args, dev):
     arr = lambda t, xs: P((t * cnt)(*xs))
     ms = ctypes.c_double()
     nlin = len(LAYER)
-    steps = (args.steps // nlin) * nlin or nlin
-    warmup = (args.warmup // nlin) * nlin
+    steps, warmup = args.steps * cnt, args.warmup * cnt      # passes over the nl layers, in GEMMs
     common = (arr(ctypes.c_int, [2] * cnt), arr(ctypes.c_void_p, [s[0] for s in seq]), None,
               arr(ctypes.c_void_p, [s[1] for s in seq]), arr(ctypes.c_int, [s[4] for s in seq]),
               arr(ctypes.c_void_p, [s[2] for s in seq]), arr(ctypes.c_int, [s[3] for s in seq]),
@@ -322,10 +339,12 @@ def run_layer(L, args, dev):
             if rc != 0:
                 raise RuntimeError("bench host: " + L.bfb_last_error().decode())
             t_layer = ms.value / 1e3 / (steps / nlin)
+            pass_ms = ms.value / args.steps
             rec = {"M": M, "us_per_layer": round(t_layer * 1e6, 3), "layer_tok_s": round(M / t_layer, 1),
                    "weight_GBps": round(layer_bytes / t_layer / 1e9, 2),
                    "hbm_frac": round(layer_bytes / t_layer / 1e9 / HBM_PEAK_GBPS, 4),
-                   "launch": "graph" if graph else "stream", "calls": mode, "layers_rotated": nl}
+                   "launch": "graph" if graph else "stream", "calls": mode, "layers_rotated": nl,
+                   "ms_per_pass": round(pass_ms, 5), "gemms_timed": steps}
             log(f"[bench] layer M={M} {mode} {rec['launch']}: {rec['us_per_layer']:.2f} us/layer "
                 f"{rec['weight_GBps']:.1f} GB/s {rec['layer_tok_s']:.0f} tok/s")
             out.append(rec)
@@ -371,17 +390,17 @@ def run_swiglu(L, args, dev):
         gu = torch.randn((M, 2 * K), device=dev).half()
         a = torch.empty((M, K), device=dev, dtype=torch.float16)
         C = torch.empty((M, N), device=dev, dtype=torch.float32)
-        r = {"M": M, "N": N, "K": K}
+        r = {"M": M, "N": N, "K": K, "calls_per_pass": rot.count}
         for fused in (1, 0):
             ms = ctypes.c_double()
             torch.cuda.synchronize()
             rc = L.bfb_time_swiglu(QT["q4_k"], P(W), P(aux), rot.count, gu.data_ptr(), 2 * K, a.data_ptr(),
-                                   C.data_ptr(), M, N, K, fused, args.warmup, args.steps, stream_handle(),
-                                   ctypes.byref(ms))
+                                   C.data_ptr(), M, N, K, fused, args.warmup * rot.count, args.steps * rot.count,
+                                   stream_handle(), ctypes.byref(ms))
             torch.cuda.synchronize()
             if rc != 0:
                 raise RuntimeError("bench host: " + L.bfb_last_error().decode())
-            r["fused_us" if fused else "unfused_us"] = round(ms.value * 1e3 / args.steps, 3)
+            r["fused_us" if fused else "unfused_us"] = round(ms.value * 1e3 / (args.steps * rot.count), 3)
         log(f"[bench] swiglu down projection M={M}: fused {r['fused_us']:.2f} us, "
             f"swiglu + gemm {r['unfused_us']:.2f} us")
         res.append(r)
@@ -401,16 +420,17 @@ def run_q8(L, args, dev):
         A = torch.randn((M, K), device=dev).half()
         Aq = torch.empty((M * K + 8 * M * (K // 32),), device=dev, dtype=torch.uint8)
         C = torch.empty((M, N), device=dev, dtype=torch.float32)
-        r = {"M": M, "N": N, "K": K}
+        r = {"M": M, "N": N, "K": K, "calls_per_pass": rot.count}
         for mode, key in ((0, "fp16_us"), (2, "q8_gemm_us"), (1, "q8_quant_gemm_us")):
             ms = ctypes.c_double()
             torch.cuda.synchronize()
             rc = L.bfb_time_q8(QT["q4_k"], P(W), P(aux), rot.count, A.data_ptr(), Aq.data_ptr(), C.data_ptr(),
-                               M, N, K, mode, args.warmup, args.steps, stream_handle(), ctypes.byref(ms))
+                               M, N, K, mode, args.warmup * rot.count, args.steps * rot.count, stream_handle(),
+                               ctypes.byref(ms))
             torch.cuda.synchronize()
             if rc != 0:
                 raise RuntimeError("bench host: " + L.bfb_last_error().decode())
-            r[key] = round(ms.value * 1e3 / args.steps, 3)
+            r[key] = round(ms.value * 1e3 / (args.steps * rot.count), 3)
         log(f"[bench] q8 path M={M:2d}: fp16 GEMM {r['fp16_us']:.2f} us, q8 GEMM {r['q8_gemm_us']:.2f} us, "
             f"quantize + q8 GEMM {r['q8_quant_gemm_us']:.2f} us")
         res.append(r)
@@ -435,8 +455,9 @@ def run_sweep(L, args, dev):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000, help="timed GEMMs per configuration")
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=30,
+                    help="timed passes over the >= 1 GB weight rotation per configuration (one GEMM per matrix)")
+    ap.add_argument("--warmup", type=int, default=3, help="untimed passes before the timed ones")
     ap.add_argument("--workload", default="q4_k",
                     choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy", "swiglu", "q8"])
     ap.add_argument("--batches", default="1,8,32")
@@ -472,14 +493,17 @@ def main():
         record = {
             "metric": METRIC if fmt == "q4_k" else METRIC.replace("Q4_K", fmt.upper()),
             "value": head["weight_GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": round(head["us_per_gemm"] / 1e3, 6),
+            "warmup": args.warmup, "ms_per_step": head["ms_per_pass"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
             "data": "synthetic",
             "config": {"workload": f"{fmt} GEMM N=K=5120, batch M={head['M']} (per_batch: M={batches})",
                        "format": QT_DESC[fmt], "N": 5120, "K": 5120, "batches": batches,
                        "rotation_matrices": rot.count, "rotation_bytes": rot.total_bytes,
                        "launch": head["launch"], "accumulate": "fp32", "algo": args.algo},
-            "tok_s": head["tok_s"],
+            "tok_s": head["tok_s"], "us_per_gemm": head["us_per_gemm"],
+            "step": (f"one pass over the rotation: {rot.count} GEMMs, one per distinct matrix, "
+                     f"{rot.total_bytes} weight bytes"),
+            "gemms_timed": head["gemms_timed"], "weight_bytes_timed": head["gemms_timed"] * rot.wbytes,
             "per_batch": [best(recs, M) for M in batches],
             "all_runs": recs,
             "hbm_read_measured_GBps": round(peak, 1),
@@ -494,13 +518,20 @@ def main():
         if not args.no_cpu:
             log("[bench] CPU baseline ...")
             record["cpu_baseline"] = cpu_baseline(fmt, 5120, 5120, batches[0], args.cpu_seconds)
+            # the reference's CPU-runnable case: Q4_0 blocks, M = 1, the same path
+            c0 = cpu_baseline("q4_0", 5120, 5120, 1, args.cpu_seconds / 2)
+            record["cpu_baseline"]["q4_0_m1"] = {k: c0[k] for k in ("value", "unit", "cores", "sample", "tok_s",
+                                                                    "ms_per_call", "ms_dequant", "ms_matmul",
+                                                                    "one_thread")}
     elif args.workload == "layer":
         recs = run_layer(L, args, dev)
         b = min(recs, key=lambda r: r["us_per_layer"])
         record = {"metric": "layer-sum weight-stream GB/s + tok/s, 27B-class decoder layer Q4_K linears at batch "
                             f"{args.layer_m}",
                   "value": b["weight_GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-                  "warmup": args.warmup, "ms_per_step": round(b["us_per_layer"] / 1e3 / len(LAYER), 6),
+                  "warmup": args.warmup, "ms_per_step": b["ms_per_pass"],
+                  "step": f"one pass over {b['layers_rotated']} distinct layers ({len(LAYER)} GEMMs each)",
+                  "us_per_layer": b["us_per_layer"],
                   "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
                   "data": "synthetic",
                   "config": {"workload": "q4_k qkv 5120->7168, o 5120->5120, gate/up 5120->17408, down 17408->5120",
@@ -513,7 +544,7 @@ def main():
         head = recs[0]
         record = {"metric": "down projection with SiLU*up (Q4_K 17408->5120): us per call, fused vs swiglu + gemm",
                   "value": head["fused_us"], "unit": "us", "n_gpus": 1, "steps": args.steps,
-                  "warmup": args.warmup, "ms_per_step": round(head["fused_us"] / 1e3, 6),
+                  "warmup": args.warmup, "ms_per_step": round(head["fused_us"] * head["calls_per_pass"] / 1e3, 6),
                   "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
                   "data": "synthetic",
                   "config": {"workload": "q4_k down projection N=5120 K=17408 fed by gate|up [M][2K], M=1 and 2"},
@@ -523,7 +554,7 @@ def main():
         head = next(r for r in recs if r["M"] == 8)
         record = {"metric": "integer-dot (int8 activation) path vs fp16 GEMM, Q4_K 5120x5120: us per GEMM",
                   "value": head["q8_gemm_us"], "unit": "us", "n_gpus": 1, "steps": args.steps,
-                  "warmup": args.warmup, "ms_per_step": round(head["q8_gemm_us"] / 1e3, 6),
+                  "warmup": args.warmup, "ms_per_step": round(head["q8_gemm_us"] * head["calls_per_pass"] / 1e3, 6),
                   "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
                   "data": "synthetic",
                   "config": {"workload": "q4_k N=5120 K=5120, M=1-16, value at M=8"}, "runs": recs}

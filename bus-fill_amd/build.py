@@ -7,6 +7,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -21,7 +22,7 @@ SOURCES = ["bf_api.hip", "bf_gemm_mfma.hip", "bf_gemm_dot2.hip", "bf_gemm_lds.hi
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 anywhere in the device code.
 HIP_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Wall", "-Wextra", "-Werror", "-Wno-unused-parameter",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # the first kernel arguments arrive in SGPRs at wave launch instead of through
@@ -31,9 +32,7 @@ HIP_FLAGS = [
 ]
 
 
-def _hipcc(sources, out, extra=(), verbose=False):
-    tmp = out + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, *sources, *extra, "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -43,6 +42,27 @@ def _hipcc(sources, out, extra=(), verbose=False):
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
     if verbose and err:
         print(err, file=sys.stderr)
+
+
+def _jobs():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    cap = os.environ.get("MAX_JOBS")
+    return max(1, min(n, int(cap) if cap and cap.isdigit() else 16))
+
+
+def _hipcc(sources, out, extra=(), verbose=False):
+    """Compiles each source to an object in parallel, then links the shared library."""
+    objdir = os.path.join(LIBDIR, "obj")
+    os.makedirs(objdir, exist_ok=True)
+    stem = os.path.splitext(os.path.basename(out))[0]
+    objs = [os.path.join(objdir, f"{stem}.{os.path.basename(s)}.o") for s in sources]
+    with ThreadPoolExecutor(max_workers=_jobs()) as ex:
+        list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, "-c", so[0], "-o", so[1]], verbose), zip(sources, objs)))
+    tmp = out + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, *extra, "-o", tmp], verbose)
     os.replace(tmp, out)
 
 

@@ -70,12 +70,16 @@ int issue_group(const std::vector<Launch>& seq, size_t first, int group, int oty
 
 // Runs `warmup` then `steps` GEMMs taken cyclically from seq, one launch call
 // per GEMM (group 1) or one bf_gemm_batched call per `group` GEMMs; returns ms.
+// The timed GEMMs continue the rotation where the warmup stopped (GEMM i of the
+// run uses seq[i % n], i counting from the first warmup GEMM), so with a
+// rotation larger than the caches no timed GEMM finds its weights left there
+// by the warmup.
 int time_seq(const std::vector<Launch>& seq, int otype, int algo, int warmup, int steps, int use_graph,
              hipStream_t st, double* ms_out, int group = 1) {
     const size_t n = seq.size();
-    auto issue = [&](const Launch&, int i) -> int {
+    auto issue = [&](int i) -> int {
         if (group > 1) return (i % group) ? 0 : issue_group(seq, (size_t)i, group, otype, st);
-        return ::issue(seq[i % n], otype, algo, st);
+        return ::issue(seq[(size_t)i % n], otype, algo, st);
     };
     hipEvent_t e0, e1;
     HCK(hipEventCreate(&e0));
@@ -83,20 +87,20 @@ int time_seq(const std::vector<Launch>& seq, int otype, int algo, int warmup, in
     float ms = 0.f;
     if (!use_graph) {
         for (int i = 0; i < warmup; i++)
-            if (issue(seq[i % n], i)) return -1;
+            if (issue(i)) return -1;
         HCK(hipStreamSynchronize(st));
         HCK(hipEventRecord(e0, st));
-        for (int i = 0; i < steps; i++)
-            if (issue(seq[i % n], i)) return -1;
+        for (int i = warmup; i < warmup + steps; i++)
+            if (issue(i)) return -1;
         HCK(hipEventRecord(e1, st));
         HCK(hipEventSynchronize(e1));
         HCK(hipEventElapsedTime(&ms, e0, e1));
     } else {
-        auto capture = [&](int count, hipGraphExec_t* exec) -> int {
+        auto capture = [&](int first, int count, hipGraphExec_t* exec) -> int {
             hipGraph_t g;
             HCK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-            for (int i = 0; i < count; i++)
-                if (issue(seq[i % n], i)) {
+            for (int i = first; i < first + count; i++)
+                if (issue(i)) {
                     hipGraph_t dead;
                     (void)hipStreamEndCapture(st, &dead);
                     return -1;
@@ -107,8 +111,8 @@ int time_seq(const std::vector<Launch>& seq, int otype, int algo, int warmup, in
             return 0;
         };
         hipGraphExec_t gw = nullptr, gs = nullptr;
-        if (warmup > 0 && capture(warmup, &gw)) return -1;
-        if (capture(steps, &gs)) return -1;
+        if (warmup > 0 && capture(0, warmup, &gw)) return -1;
+        if (capture(warmup, steps, &gs)) return -1;
         if (gw) HCK(hipGraphLaunch(gw, st));
         HCK(hipStreamSynchronize(st));
         HCK(hipEventRecord(e0, st));
@@ -227,7 +231,7 @@ int bfb_time_swiglu(int qtype, const void* const* W, const void* const* W_aux, i
     HCK(hipEventCreate(&e0));
     HCK(hipEventCreate(&e1));
     HCK(hipEventRecord(e0, st));
-    for (int r = 0; r < steps; r++)
+    for (int r = warmup; r < warmup + steps; r++)
         if ((g_bf = call(r)) != BF_OK) {
             (void)hipEventDestroy(e0);
             (void)hipEventDestroy(e1);
@@ -267,7 +271,7 @@ int bfb_time_q8(int qtype, const void* const* W, const void* const* W_aux, int c
     HCK(hipEventCreate(&e0));
     HCK(hipEventCreate(&e1));
     HCK(hipEventRecord(e0, st));
-    for (int r = 0; r < steps; r++)
+    for (int r = warmup; r < warmup + steps; r++)
         if ((g_bf = call(r)) != BF_OK) {
             (void)hipEventDestroy(e0);
             (void)hipEventDestroy(e1);
@@ -302,7 +306,7 @@ int bfb_read_slices(const void* const* src, int count, size_t bytes, int blocks,
                            (unsigned*)sink);
     HCK(hipGetLastError());
     HCK(hipEventRecord(e0, st));
-    for (int r = 0; r < steps; r++)
+    for (int r = warmup; r < warmup + steps; r++)
         hipLaunchKernelGGL(k_stream_read, dim3(blocks), dim3(threads), 0, st, (const uint4*)src[r % count], n16,
                            (unsigned*)sink);
     HCK(hipGetLastError());
