@@ -29,6 +29,16 @@ bf_status from_hip(hipError_t e, const char* what) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// A K-split launch: the one error of its own is a first use of a stream's
+// workspace while the stream is being captured.
+bf_status from_split(hipError_t e, const char* what) {
+    if (e == hipErrorStreamCaptureUnsupported)
+        return fail(BF_ERR_UNSUPPORTED, "%s: the K-split kernel's workspace for this stream is allocated on its first "
+                                        "use, which cannot happen during stream capture; make one uncaptured call of "
+                                        "this shape (or a larger one) on the stream first", what);
+    return from_hip(e, what);
+}
+
 constexpr int kMaxMPerLaunch = 128;   // MFMA kernels cover up to 8 batch tiles of 16
 constexpr int kDot2MaxM = 4;          // crossover dot2 -> MFMA (see the batch sweep)
 constexpr int kSplitMaxM = 32;        // batch rows of one K-split launch
@@ -145,7 +155,7 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
                 if (!fast || !bf::split_supports(g))
                     return fail(BF_ERR_UNSUPPORTED, "K-split path does not serve qtype %d M=%d N=%d K=%d",
                                 (int)qtype, g.M, N, K);
-                e = bf::gemm_split(g, hs);
+                e = bf::gemm_split(g, nullptr, hs);
                 break;
             case BF_ALGO_LDS:
                 if (!fast || !bf::lds_supports(g))
@@ -157,7 +167,7 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
                 e = bf::gemm_simple(g, hs);
                 break;
         }
-        st = from_hip(e, "kernel launch");
+        st = use == BF_ALGO_SPLIT ? from_split(e, "kernel launch") : from_hip(e, "kernel launch");
         if (st != BF_OK) return st;
     }
     return BF_OK;
@@ -212,7 +222,7 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
     if (all_lds && bf::lds_batched_supports(gs.data(), count))
         return from_hip(bf::gemm_lds_batched(gs.data(), count, (hipStream_t)stream), "batched launch");
     if (all_split && bf::split_batched_supports(gs.data(), count))
-        return from_hip(bf::gemm_split_batched(gs.data(), count, (hipStream_t)stream), "batched launch");
+        return from_split(bf::gemm_split_batched(gs.data(), count, nullptr, (hipStream_t)stream), "batched launch");
     for (int i = 0; i < count; i++) {
         const bf_gemm_desc& d = descs[i];
         const bf_status st =
@@ -330,6 +340,15 @@ const char* bf_last_error(void) { return g_last_error; }
 
 namespace bf {
 void set_last_error(const char* text) { snprintf(g_last_error, sizeof g_last_error, "%s", text); }
+
+bool copy_to_device(void* dst, const void* src, size_t n, void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    const hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, st);
+    const hipError_t e2 = e == hipSuccess ? hipStreamSynchronize(st) : e;
+    if (e2 == hipSuccess) return true;
+    snprintf(g_last_error, sizeof g_last_error, "copy of %zu bytes to the device failed: %s", n, hipGetErrorString(e2));
+    return false;
+}
 }  // namespace bf
 
 extern "C" {

@@ -92,26 +92,30 @@ __device__ __forceinline__ void q4k_scale_min(const uint32_t s[3], int j, uint32
 }
 
 // Eight fp16 weights from eight code bytes (w0 = bytes 0-3, w1 = bytes 4-7),
-// one nibble per byte (low nibbles when HI == false), in natural byte order.
-// Q4_K: out = RN16(fma32(bias + q, s, c)) with s = d*sc and c = -dmin*m - bias*s
-// in fp32 (v_fma_mix: fp16 operand, fp32 arithmetic, one rounding to fp16).
-// (bias + q) is exact in fp16 and (bias + q)*s is exact in the fused multiply-add,
-// so each weight is q*s - dmin*m rounded once, up to c's own fp32 rounding
-// (at most 2^-24 * bias * s).
+// one nibble per byte (low nibbles when HI == false), in natural byte order:
+// Q4_K, out = RN16(RN32(q*s - dm)), the oracle's (and ggml's) fp16 dequant of
+// scale s = d*sc and offset dm = dmin*m, bit for bit.  v_perm_b32 spreads two
+// code bytes into the halves of a word and one AND keeps one nibble per half,
+// which read as fp16 is an exact subnormal: q * 2^-24 (low nibble) or
+// 16 q * 2^-24 (high nibble, masked in place).  v_fma_mix_f32 takes that half
+// as its fp16 operand, times s24 = s * 2^24 (low) or s * 2^20 (high), plus
+// ndm = -dm, so it forms q*s - dm exactly and rounds it once to fp32;
+// v_cvt_pk_f16_f32 then rounds two results to fp16 (RNE).  (v_fma_mix{lo,hi}_f16
+// would round the exact value straight to fp16, which differs from the two
+// roundings of the dequant in double-rounding cases.)
 template <bool HI>
-__device__ __forceinline__ h8 decode8_mix(const Magic& mg, uint32_t w0, uint32_t w1, float s, float c) {
-    const uint32_t mask = HI ? mg.hi_mask : mg.lo_mask, bits = HI ? mg.hi_bits : mg.lo_bits;
-    uint32_t p[4] = {perm_b32(w0, w0, SEL_B01), perm_b32(w0, w0, SEL_B23),
-                     perm_b32(w1, w1, SEL_B01), perm_b32(w1, w1, SEL_B23)};
+__device__ __forceinline__ h8 decode8_mix(uint32_t w0, uint32_t w1, float s24, float ndm) {
+    const uint32_t mask = HI ? 0x00F000F0u : 0x000F000Fu;
+    const uint32_t p[4] = {perm_b32(w0, w0, SEL_B01), perm_b32(w0, w0, SEL_B23),
+                           perm_b32(w1, w1, SEL_B01), perm_b32(w1, w1, SEL_B23)};
     uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t x = and_or(p[i], mask, bits);              // {bias + q, bias + q'}
-        // v_fma_mix{lo,hi}_f16: op_sel_hi marks src0 as fp16 (op_sel picks its half),
-        // s and c are fp32; mixhi keeps the low half written by mixlo
-        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(o[i]) : "v"(x), "v"(s), "v"(c));
-        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-            : "+v"(o[i]) : "v"(x), "v"(s), "v"(c));
+        const uint32_t x = p[i] & mask;                           // {q, q'} as fp16 subnormals
+        float lo, hi;
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(lo) : "v"(x), "v"(s24), "v"(ndm));
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(hi) : "v"(x), "v"(s24), "v"(ndm));
+        asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(o[i]) : "v"(lo), "v"(hi));
     }
     return __builtin_bit_cast(h8, u4{o[0], o[1], o[2], o[3]});
 }

@@ -61,7 +61,9 @@ __device__ __forceinline__ void load_raw<QT_Q4_0>(Raw<QT_Q4_0>& raw, const uint8
 
 // Per-lane scale state derived once per super-group.
 template <int QT> struct Scl;
-template <> struct Scl<QT_Q4_K> { float sa, ca, sb, cb; };   // scale, offset of sub-blocks 2kg, 2kg+1
+// Q4_K: d*sc * 2^24 (sub-block 2kg, low nibbles) and d*sc * 2^20 (2kg+1, high
+// nibbles), and -dmin*m of each: the operands of decode8_mix
+template <> struct Scl<QT_Q4_K> { float sa, ca, sb, cb; };
 template <> struct Scl<QT_PLANES> { h2 da, db; };
 template <> struct Scl<QT_Q4_0> { h2 da, db; uint32_t qa[4]; };
 
@@ -84,11 +86,12 @@ __device__ __forceinline__ Scl<QT_Q4_K> scales(const Raw<QT_Q4_K>& raw, int kg) 
     const float d = half_bits_to_float(raw.hdr.x & 0xFFFFu);
     const float dmin = half_bits_to_float(raw.hdr.x >> 16);
     Scl<QT_Q4_K> o;
-    // sub-block 2kg uses the low nibbles (magic bias 1024), 2kg+1 the high ones (bias 64)
-    o.sa = d * (float)(sc & 0xFFu);
-    o.ca = __builtin_fmaf(-1024.0f, o.sa, -(dmin * (float)(mn & 0xFFu)));
-    o.sb = d * (float)(sc >> 8);
-    o.cb = __builtin_fmaf(-64.0f, o.sb, -(dmin * (float)(mn >> 8)));
+    // d*sc and dmin*m are exact in fp32 (at most 17 significant bits), and so
+    // are their power-of-two multiples (d*sc < 2^22: no overflow)
+    o.sa = d * (float)(sc & 0xFFu) * 16777216.0f;
+    o.ca = -(dmin * (float)(mn & 0xFFu));
+    o.sb = d * (float)(sc >> 8) * 1048576.0f;
+    o.cb = -(dmin * (float)(mn >> 8));
     return o;
 }
 
@@ -238,8 +241,8 @@ __device__ __forceinline__ Scl<QT_Q4_0> scales(const Raw<QT_Q4_0>& raw, int) {
 __device__ __forceinline__ h8 weights(const Magic& mg, const Raw<QT_Q4_K>& raw, const Scl<QT_Q4_K>& sc, int i) {
     const uint32_t w[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
     const int t = i & 3;
-    if (i < 4) return decode8_mix<false>(mg, w[2 * t], w[2 * t + 1], sc.sa, sc.ca);
-    return decode8_mix<true>(mg, w[2 * t], w[2 * t + 1], sc.sb, sc.cb);
+    if (i < 4) return decode8_mix<false>(w[2 * t], w[2 * t + 1], sc.sa, sc.ca);
+    return decode8_mix<true>(w[2 * t], w[2 * t + 1], sc.sb, sc.cb);
 }
 
 __device__ __forceinline__ h8 weights(const Magic& mg, const Raw<QT_PLANES>& raw, const Scl<QT_PLANES>& sc, int i) {

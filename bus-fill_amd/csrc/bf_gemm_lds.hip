@@ -225,7 +225,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             if (e < S) {
                 // the slot's previous step must be consumed (its marker set to 2
                 // by the compute wave that read it) before it is overwritten
-                if (e >= nslot) wait_flag_value(&flags[kStepMark + e - nslot], 2);
+                if (e >= nslot) wait_flag_value(&flags[kStepMark + e - nslot], 2, flags + kPoison);
                 const uint32_t gbase = m0 + (uint32_t)((g4 % G4R) * 4 * kStep);
                 const StepBase<QT> base = step_base<QT>((int64_t)(tile0 + te) * R, G * se, K);
 #pragma unroll
@@ -252,7 +252,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             for (int s2 = s_lo; s2 < s_hi; s2++) {
                 // the segment's slot must be released by all nsub steps of its
                 // previous segment
-                if (RG && s2 >= na) wait_flag_value(&flags[kSegCount + s2 - na], nsub);
+                if (RG && s2 >= na) wait_flag_value(&flags[kSegCount + s2 - na], nsub, flags + kPoison);
                 const uint32_t dst = lds0 + (uint32_t)(kFlagBytes + seg_off(s2));
 #pragma unroll
                 for (int q = 0; q < kASlots; q++) {
@@ -311,7 +311,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         }
         clear_flags_and_meet();
         signal_own_loads(&flags[cw], lane);
-        wait_flags(flags, NC, lane);
+        wait_flags(flags, NC, lane, flags + kPoison);
     } else if constexpr (AC) {
         // small A, all of it resident: the compute waves load it (instruction
         // f = s * IA + i: piece 64 i + lane of segment s; wave c issues c, c + NC,
@@ -332,7 +332,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         }
         clear_flags_and_meet();
         signal_own_loads(&flags[cw], lane);
-        wait_flags(flags, NC, lane);
+        wait_flags(flags, NC, lane, flags + kPoison);
     } else {
         clear_flags_and_meet();
     }
@@ -412,7 +412,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         // batch 1: all of A (10 KB at K = 5120) at once, tabulated before the first step
         build_table((wave - NL) * 64 + lane, nsteps * M * G * 4, NC * 64);
         if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[wave - NL])), "v"(2) : "memory");
-        wait_flags(flags, NC, lane, 2);
+        wait_flags(flags, NC, lane, flags + kPoison, 2);
     }
 
     const Magic mg = make_magic();
@@ -464,7 +464,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             // segment's block-sum flag), or one after the other: Q4_K with two
             // m-tiles or the rings measured faster with three round trips.
             constexpr bool kMerged = !(QT == QT_Q4_K && (MT == 2 || RG));
-            if (!AC && (!kMerged || (QT == QT_Q4_K && t_in == 0))) wait_flags(flags + kAMark + 4 * s_in, NL, lane);
+            if (!AC && (!kMerged || (QT == QT_Q4_K && t_in == 0))) wait_flags(flags + kAMark + 4 * s_in, NL, lane, flags + kPoison);
             if (QT == QT_Q4_K && t_in == 0) {
                 build_table(s_in * M * G * 4 + lane, (s_in + 1) * M * G * 4, 64);
                 if (lane == 0)
@@ -473,10 +473,10 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             if (kMerged) {
                 const int* f = lane < NL ? flags + kAMark + 4 * s_in + lane
                                          : lane == NL ? flags + kStepMark + e : flags + kTabFlag + s_in;
-                wait_lanes(f, (lane <= NL && (!AC || lane == NL)) || (QT == QT_Q4_K && lane == NL + 1));
+                wait_lanes(f, (lane <= NL && (!AC || lane == NL)) || (QT == QT_Q4_K && lane == NL + 1), flags + kPoison);
             } else {
-                if (t_in != 0) wait_flag(&flags[kTabFlag + s_in]);
-                wait_flag(&flags[kStepMark + e]);
+                if (t_in != 0) wait_flag(&flags[kTabFlag + s_in], flags + kPoison);
+                wait_flag(&flags[kStepMark + e], flags + kPoison);
             }
         }
         Raw<QT> raw;
@@ -496,7 +496,11 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                         for (int t = 0; t < 8; t++) abd[mt][t] = *(const h8*)(aseg + arow[mt] + 16 * t);
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(mark) :: "memory");
-                if (__builtin_amdgcn_readfirstlane(mark) != 0 || it >= (1 << 20)) break;
+                if (__builtin_amdgcn_readfirstlane(mark) != 0) break;
+                if (it >= kWaitBound) {
+                    mark_poison(flags + kPoison);
+                    break;
+                }
                 __builtin_amdgcn_s_sleep(1);
             }
             // the step's slot is free again (its reads have completed)
@@ -642,10 +646,12 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                          : "=v"(old) : "v"(lds_addr(&flags[kSubCount + t_in])), "v"(1) : "memory");
         if (__builtin_amdgcn_readfirstlane(old) == nsteps - 1) {
             const int64_t row0 = (int64_t)(tile0 + t_in) * R;
+            const bool bad = poisoned(flags + kPoison);
             for (int v = lane; v < SLOT; v += 64) {
                 const float* pp = parts + t_in * nsteps * SLOT + v;
                 float sum = 0.f;
                 for (int s2 = 0; s2 < nsteps; s2++) sum += pp[s2 * SLOT];
+                if (bad) sum = __builtin_nanf("");
                 const int m = v / R, rl = v - m * R;   // m = mt * R + m_loc
                 const int64_t row = row0 + rl;
                 if (m < M && row < N) {
@@ -661,7 +667,8 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         // groups (sub-block pairs) and the four segments are summed
         for (int t_in = 0; t_in < nsub; t_in++) {
             if ((t_in * nsteps + nsteps - 1) % NC != wave - NL) continue;
-            wait_count(&flags[kSubCount + t_in], nsteps);
+            wait_count(&flags[kSubCount + t_in], nsteps, flags + kPoison);
+            const bool bad = poisoned(flags + kPoison);
             const int64_t row = (int64_t)(tile0 + t_in) * R + rowl;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
@@ -672,6 +679,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                 y = sum_lane_xor32(y);
                 y += dpp_xor(y, 1);
                 y += dpp_xor(y, 2);
+                if (bad) y = __builtin_nanf("");
                 if (g == 0 && kg == 0 && mt < M && row < N) {
                     if (out_f16) ((_Float16*)C)[(int64_t)mt * ldc + row] = (_Float16)y;
                     else ((float*)C)[(int64_t)mt * ldc + row] = y;

@@ -32,6 +32,7 @@ namespace bf {
 namespace {
 
 constexpr int kSlabFlags = 2048;         // ready[e] at 64 + 4e, consumed[e] at 1024 + 4e, counter at 4
+constexpr int kSlabPoison = 3;           // flags[3]: a bounded wait gave up (results become NaN)
 constexpr int kSlabMaxSteps = (1024 - 64) / 4;
 
 template <int QT, int MT, int NTMAX, int NC, int NL, int D>
@@ -64,7 +65,7 @@ void k_gemm_slab(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux
         const int nIw = (nt * 144 + 63) >> 6;          // instructions of the weight part
         const int nIa = (M * 33 + 63) >> 6;            // instructions of the activation slab
         for (int e = j; e < nsg; e += NL) {
-            if (e >= D) wait_flag(&flags[256 + e - D]);   // the slot's previous step is consumed
+            if (e >= D) wait_flag(&flags[256 + e - D], flags + kSlabPoison);   // the slot's previous step is consumed
             const uint32_t slot = lds0 + (uint32_t)(kSlabFlags + (e % D) * slot_bytes);
             for (int i = 0; i < nIw; i++) {
                 const int P = 64 * i + lane;           // piece of the weight part: tile, row, part
@@ -100,7 +101,7 @@ void k_gemm_slab(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux
     for (int mt = 0; mt < MT; mt++) arow[mt] = min(16 * mt + r, M - 1) * 528 + 128 * kg;
 
     for (int e = c; e < nsg; e += NC) {
-        wait_flag(&flags[16 + e]);
+        wait_flag(&flags[16 + e], flags + kSlabPoison);
         const uint8_t* slot = ring + (e % D) * slot_bytes;
         Raw<QT> raw[NTMAX] = {};
 #pragma unroll
@@ -142,6 +143,7 @@ void k_gemm_slab(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux
         asm volatile("s_waitcnt lgkmcnt(0)\n\tds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
                      : "=v"(old) : "v"(lds_addr(&flags[1])), "v"(1) : "memory");
     if (__builtin_amdgcn_readfirstlane(old) != NC - 1) return;
+    const bool bad = poisoned(flags + kSlabPoison);
 #pragma unroll
     for (int tt = 0; tt < NTMAX; tt++) {
         if (tt >= nt) break;
@@ -151,6 +153,7 @@ void k_gemm_slab(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux
             for (int i = 0; i < 4; i++) {
                 float v = 0.f;
                 for (int w2 = 0; w2 < NC; w2++) v += parts[(w2 * 64 + lane) * PER + (tt * MT + mt) * 4 + i];
+                if (bad) v = __builtin_nanf("");
                 const int m = 16 * mt + 4 * kg + i;
                 const int64_t n = (int64_t)(t0 + tt) * 16 + r;
                 if (m < M && n < N) {

@@ -23,20 +23,30 @@
 //   (u = c / nt, U = number of waves on that tile), accumulating all batch rows
 //   (MT m-tiles of 16) in registers.  The other waves of a tile park their sums
 //   in LDS and the tile's first wave adds them in wave order.
-// * With S > 1 the tile sums are written to a per-stream workspace; the split
-//   that finishes last (a device-scope counter per row group) adds the S
-//   partials in split order and writes C.  The order never depends on timing,
-//   so results are deterministic; the last split resets the counter, so the
-//   workspace is ready for the next launch on the stream.  Partials are written
-//   and read with device-coherent (agent-scope) accesses, which reach the point
-//   of coherence of the XCDs' L2s: a writer's accesses are complete
+// * With S > 1 the tile sums are written to a workspace; the split that
+//   finishes last (a counter per row group) adds the S partials in split order
+//   and writes C.  The order never depends on timing, so results are
+//   deterministic; the last split resets the counter, so the workspace is
+//   ready for the next launch that uses it.  A writer's stores are complete
 //   (s_waitcnt vmcnt(0)) before its workgroup counts itself, and the last
-//   split reads only after its own count, so no whole-L2 write-back or
-//   invalidate (what a release/acquire fence costs) is needed.
+//   split reads only after its own count.
+// * XCD-local exchange (nx > 0): the dispatcher hands workgroup b to XCD
+//   b % nx, so the grid is laid out to put all S splits of a row group on one
+//   XCD, where they share one L2.  Partials are then plain (L2 write-back)
+//   stores that the last split's device-scope reads find in that L2 (those
+//   reads miss only the L1), instead of stores written through to memory.
+//   The counter stays a device-scope atomic.
+//   Each workgroup checks its XCC id against b % nx; a workgroup that finds
+//   itself elsewhere writes NaN over its rows of C, so a broken placement
+//   shows as a failed result rather than a silently wrong one.  With nx = 0
+//   the partials are written with device-scope (sc1) stores, which reach the
+//   point of coherence of all XCDs' L2s.
 #include <algorithm>
 #include <atomic>
 #include <map>
 #include <mutex>
+#include <thread>
+#include <tuple>
 #include <utility>
 
 #include "bf_launch.h"
@@ -45,16 +55,28 @@
 namespace bf {
 namespace {
 
-// LDS: [0, 2048) flags: owners-done counter at 4, is-last word at 8, unit
-// markers of loader j for unit i at 64 + 16 i + 4 j, park flag of compute wave c
-// at 1024 + 4 c; then the units; then the parked sums.
+// LDS: [0, 2048) flags: owners-done counter at 4, is-last word at 8, poison
+// word at 12 (a bounded wait gave up), unit markers of loader j for unit i at
+// 64 + 16 i + 4 j, park flag of compute wave c at 1024 + 4 c; then the units;
+// then the parked sums.
+constexpr int kSpPoison = 3;
+// A workgroup that counts itself with a poisoned result adds this to its row
+// group's counter too (on top of 1), so the split that finishes last writes NaN.
+constexpr unsigned kSpPoisonCount = 1u << 16;
 constexpr int kSpFlags = 2048;
 constexpr int kSpMaxUnits = (1024 - 64) / 16;
 constexpr int kSpNC = 12, kSpNL = 4;    // compute and loader waves per workgroup
 constexpr int kSpQS = 12;               // instruction slots per loader and unit
 constexpr int kSpMaxPieces = 64 * kSpNL * kSpQS;
 constexpr int kSpCounterStride = 64;    // one row-group counter per 256-byte line: no shared lines
-constexpr int kCoherent = 16;           // buffer access cache policy: sc1, coherent across the XCDs' L2s
+constexpr int kCoherent = 16;           // buffer access cache policy: sc1 (device scope: misses the L1)
+
+// The XCC (XCD) this wave runs on.
+__device__ __forceinline__ int xcc_id() {
+    int x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 0xF;
+}
 
 // Buffer resource over the split partials [S][N][Mp] (fp32).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t workspace_rsrc(float* ws, int S, int N, int Mp) {
@@ -67,11 +89,33 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
                                            const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nt,
                                            int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux,
                                            void* __restrict__ C, int ldc, int out_f16, float* __restrict__ ws,
-                                           unsigned* __restrict__ counters) {
+                                           unsigned* __restrict__ counters, int nx) {
     constexpr int NC = kSpNC, NL = kSpNL;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int rg = bid / S, s = bid - rg * S;
+    int rg, s;
+    if (nx > 0) {
+        // XCD x = bid % nx holds row groups x, x + nx, ..., each as S consecutive workgroups
+        const int x = bid % nx, jx = bid / nx, q = jx / S;
+        rg = x + nx * q;
+        s = jx - q * S;
+        if ((int64_t)rg * nt * 16 >= N) return;          // padding of the last XCD round
+        if (S > 1 && nx > 1 && xcc_id() != x) {
+            // not on the XCD the exchange assumes: poison this workgroup's rows
+            for (int v = threadIdx.x; v < nt * 16 * M; v += blockDim.x) {
+                const int m = v / (nt * 16);
+                const int64_t n = (int64_t)rg * nt * 16 + (v - m * nt * 16);
+                if (n < N) {
+                    if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + n] = (_Float16)__builtin_nanf("");
+                    else ((float*)C)[(int64_t)m * ldc + n] = __builtin_nanf("");
+                }
+            }
+            return;
+        }
+    } else {
+        rg = bid / S;
+        s = bid - rg * S;
+    }
     const int sg0 = s * nsgS;
     int* const flags = (int*)lds;
     const uint32_t lds0 = lds_addr(lds);
@@ -144,7 +188,7 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
     for (int mt = 0; mt < MT; mt++) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
 
     for (int i = u; i < nsgS; i += U) {
-        wait_flags(flags + 16 + 4 * i, NL, lane);
+        wait_flags(flags + 16 + 4 * i, NL, lane, flags + kSpPoison);
         const uint8_t* unit = lds + kSpFlags + i * unit_bytes;
         Raw<QT> raw;
         lds_raw<QT>(raw, unit + PA * 16 + t * 2304 + r * 144, kg);
@@ -170,7 +214,7 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
     } else {
         for (int u2 = 1; u2 < U; u2++) {
             const int c2 = t + nt * u2;
-            wait_flag(&flags[256 + c2]);
+            wait_flag(&flags[256 + c2], flags + kSpPoison);
             const float* theirs = park + (c2 - nt) * MT * 256;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
@@ -178,15 +222,21 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
                 for (int i = 0; i < 4; i++) acc[mt][i] += theirs[(mt * 4 + i) * 64 + lane];
         }
         const int64_t n = (int64_t)(rg * nt + t) * 16 + r;
+        if (poisoned(flags + kSpPoison)) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) acc[mt] = f4{1.f, 1.f, 1.f, 1.f} * __builtin_nanf("");
+        }
         if (S > 1) {
             // workspace [s][n][Mp]: this lane's four rows of an m-tile are one 16-byte store
             const __amdgpu_buffer_rsrc_t wr = workspace_rsrc(ws, S, N, Mp);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
                 const int m4 = mt * 16 + 4 * kg;
-                if (m4 < Mp && n < N)
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr,
-                                                           (int)((((int64_t)s * N + n) * Mp + m4) * 4), 0, kCoherent);
+                if (m4 < Mp && n < N) {
+                    const int off = (int)((((int64_t)s * N + n) * Mp + m4) * 4);
+                    if (nx > 0) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr, off, 0, 0);
+                    else __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr, off, 0, kCoherent);
+                }
             }
         } else {
 #pragma unroll
@@ -207,17 +257,24 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
 
     // --------------------------------------------------------- cross-split sum
     if (c == 0) {
-        wait_flags(&flags[1], 1, lane, min(nt, NC));
+        wait_flags(&flags[1], 1, lane, flags + kSpPoison, min(nt, NC));
+        // the count carries this workgroup's poison (a tile whose sums it did
+        // not see stored leaves a stale partial behind)
+        const unsigned add = poisoned(flags + kSpPoison) ? 1u + kSpPoisonCount : 1u;
         unsigned old = 0;
         unsigned* const cnt = counters + rg * kSpCounterStride;
-        if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) old = __hip_atomic_fetch_add(cnt, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         old = __builtin_amdgcn_readfirstlane(old);
-        const int last = old == (unsigned)(S - 1);
+        const int last = (old & (kSpPoisonCount - 1)) == (unsigned)(S - 1);
         if (last && lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[2])), "v"(last ? 1 : 2) : "memory");
+        // 1: last and clean, 3: last with a poisoned split, 2: not last
+        const int word = !last ? 2 : (old >= kSpPoisonCount || add > 1u) ? 3 : 1;
+        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[2])), "v"(word) : "memory");
     }
-    wait_flags(&flags[2], 1, lane);
-    if (flags[2] != 1) return;
+    wait_flags(&flags[2], 1, lane, flags + kSpPoison);
+    const int word = flags[2];
+    if (word != 1 && word != 3) return;
+    const bool bad = word == 3 || poisoned(flags + kSpPoison);
     // each lane takes up to four quads (one row n, rows m4 .. m4+3) at a time and
     // issues all of their partial loads (up to 16) before the first add
     const int rows = nt * 16, nq = rows * (Mp / 4);
@@ -262,8 +319,9 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 if (m4 + i >= M) break;
-                if (out_f16) ((_Float16*)C)[(int64_t)(m4 + i) * ldc + n] = (_Float16)sum[q][i];
-                else ((float*)C)[(int64_t)(m4 + i) * ldc + n] = sum[q][i];
+                const float y = bad ? __builtin_nanf("") : sum[q][i];
+                if (out_f16) ((_Float16*)C)[(int64_t)(m4 + i) * ldc + n] = (_Float16)y;
+                else ((float*)C)[(int64_t)(m4 + i) * ldc + n] = y;
             }
         }
     }
@@ -273,10 +331,10 @@ template <int QT, int MT>
 __global__ __launch_bounds__(64 * (kSpNC + kSpNL))
 void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
                   int nt, int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C,
-                  int ldc, int out_f16, float* __restrict__ ws, unsigned* __restrict__ counters) {
+                  int ldc, int out_f16, float* __restrict__ ws, unsigned* __restrict__ counters, int nx) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     split_body<QT, MT>((int)blockIdx.x, lds, W, A, lda, M, N, K, nt, S, nsgS, unit_bytes, Waux, C, ldc, out_f16, ws,
-                       counters);
+                       counters, nx);
 }
 
 // Several independent GEMMs in one launch (their grids back to back): a
@@ -295,7 +353,7 @@ struct SplitJob {
 };
 struct SplitJobs {
     SplitJob job[kSpMaxJobs];
-    int n, out_f16;
+    int n, out_f16, nx;                  // nx: XCD-local exchange (every job's grid0 a multiple of nx)
 };
 
 template <int QT, int MT>
@@ -309,7 +367,7 @@ void k_gemm_split_batched(const SplitJobs jobs) {
     for (int i = 1; i < kSpMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
     split_body<QT, MT>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nt, j.S, j.nsgS,
-                       j.unit_bytes, j.Waux, j.C, j.ldc, jobs.out_f16, j.ws, j.counters);
+                       j.unit_bytes, j.Waux, j.C, j.ldc, jobs.out_f16, j.ws, j.counters, jobs.nx);
 }
 
 __global__ void k_zero_u32(unsigned* p, int n) {
@@ -317,7 +375,7 @@ __global__ void k_zero_u32(unsigned* p, int n) {
 }
 
 struct SplitPlan {
-    int S, nt, nsgS, MT, grid, unit_bytes, lds;
+    int S, nt, nsgS, MT, grid, unit_bytes, lds, nx, rgs;
 };
 
 int split_lds_bytes(int M, int nt, int nsgS, int MT) {
@@ -326,10 +384,27 @@ int split_lds_bytes(int M, int nt, int nsgS, int MT) {
     return kSpFlags + nsgS * unit + parks;
 }
 
+// XCDs of the current device: the workgroup round robin the XCD-local exchange
+// lays its grid out for (1 on a device with one XCD per agent).
+int device_xcds() {
+    static std::atomic<int> cache[64];                 // 0: not queried yet
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || v < 1 || v > 16) v = -1;
+        cache[dev].store(v, std::memory_order_relaxed);
+        n = v;
+    }
+    return n > 0 ? n : 0;                                // unknown: device-scope exchange
+}
+
 // S divides the super-groups; nt tiles per workgroup (<= the compute waves);
 // the estimate is rounds of 256 workgroups times the bytes each one loads,
-// plus the partials' round trip when S > 1.
-bool plan_split(const GemmArgs& g, SplitPlan& p) {
+// plus the partials' round trip when S > 1.  With nx XCDs the grid holds
+// ceil(rgs / nx) * nx row groups (whole rounds of the XCD round robin).
+bool plan_split(const GemmArgs& g, SplitPlan& p, int nx) {
     if (g.M > 32 || g.K % 256) return false;
     if ((int64_t)g.K / 256 * g.N * 32 * 4 >= (1LL << 31)) return false;   // partials addressed by 32-bit offsets
     const int nsg = g.K / 256, T = (g.N + 15) / 16;
@@ -343,13 +418,16 @@ bool plan_split(const GemmArgs& g, SplitPlan& p) {
             const int nt = (int)(((int64_t)T * S + 256LL * rounds - 1) / (256LL * rounds));
             if (nt > kSpNC || g.M * 33 + nt * 144 > kSpMaxPieces) continue;
             if (split_lds_bytes(g.M, nt, nsgS, MT) > kMaxLds) continue;
-            const int grid = (T + nt - 1) / nt * S;
+            const int rgs = (T + nt - 1) / nt;
+            const int sx = S > 1 && nx > 0 ? nx : 0;
+            const int grid = (sx ? (rgs + sx - 1) / sx * sx : rgs) * S;
             const double per_wg = (double)nt * nsgS * 2304 + (double)g.M * nsgS * 512 +
                                   (S > 1 ? 3.0 * nt * 16 * g.M * 4 : 0.0);
             const double est = (double)((grid + 255) / 256) * per_wg;
             if (est < best) {
                 best = est;
-                p = SplitPlan{S, nt, nsgS, MT, grid, (g.M * 33 + nt * 144) * 16, split_lds_bytes(g.M, nt, nsgS, MT)};
+                p = SplitPlan{S, nt, nsgS, MT, grid, (g.M * 33 + nt * 144) * 16, split_lds_bytes(g.M, nt, nsgS, MT),
+                              sx, rgs};
             }
             break;                                       // fewer rounds fit first: more would only add rounds
         }
@@ -357,35 +435,79 @@ bool plan_split(const GemmArgs& g, SplitPlan& p) {
     return best < 1e300;
 }
 
-// Per-(device, stream) workspace: row-group counters (kept zero between
-// launches by the kernel) followed by the split partials.  Grown on demand and
-// kept until the process ends; launches on one stream are ordered, so they can
-// share it.
-hipError_t workspace(hipStream_t st, size_t counter_bytes, size_t part_bytes, unsigned** counters, float** parts) {
+// Workspace of one K-split GEMM: row-group counters (256 bytes each, kept zero
+// between launches by the kernel) then the partials [S][N][Mp], at 256-byte
+// offsets.  0 when the plan does not split K.
+size_t counter_bytes(const SplitPlan& p) { return p.S > 1 ? (size_t)p.rgs * kSpCounterStride * 4 : 0; }
+size_t partial_bytes(const GemmArgs& g, const SplitPlan& p) {
+    return p.S > 1 ? ((size_t)p.S * g.N * ((g.M + 3) & ~3) * 4 + 255) & ~(size_t)255 : 0;
+}
+
+// The library's own workspaces, one per (device, stream): launches on one
+// stream are ordered, so they can share it.  hipStreamPerThread names a
+// different stream in every host thread, so it is keyed by the thread too.
+// Grown on demand: the old buffer is freed once the stream has finished with
+// it.  Never allocated while the stream is being captured into a graph (an
+// allocation cannot be captured): such a call fails with
+// hipErrorStreamCaptureUnsupported unless a large enough workspace exists.
+hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t pbytes, unsigned** counters, float** parts) {
+    struct Slot {
+        uint8_t* p = nullptr;
+        size_t cb = 0, pb = 0;
+    };
     static std::mutex mu;
-    static std::map<std::pair<int, uintptr_t>, std::pair<uint8_t*, std::pair<size_t, size_t>>> cache;
+    static std::map<std::tuple<int, uintptr_t, std::thread::id>, Slot> cache;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
+    const std::thread::id tid = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
     std::lock_guard<std::mutex> lock(mu);
-    auto& slot = cache[{dev, (uintptr_t)st}];
-    if (!slot.first || slot.second.first < counter_bytes || slot.second.second < part_bytes) {
-        const size_t cb = std::max(counter_bytes, slot.second.first), pb = std::max(part_bytes, slot.second.second);
+    Slot& slot = cache[{dev, (uintptr_t)st, tid}];
+    if (!slot.p || slot.cb < cbytes || slot.pb < pbytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(st, &cs);
+        if (e != hipSuccess) return e;
+        if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+        const size_t cb = std::max(cbytes, slot.cb), pb = std::max(pbytes, slot.pb);
         uint8_t* p = nullptr;
         e = hipMalloc((void**)&p, cb + pb);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(k_zero_u32, dim3(64), dim3(256), 0, st, (unsigned*)p, (int)(cb / 4));
         e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        slot = {p, {cb, pb}};                            // a replaced buffer is kept: in-flight launches may use it
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return e;
+        }
+        if (slot.p) {
+            // launches already queued on the stream may still use the old buffer
+            e = hipStreamSynchronize(st);
+            if (e != hipSuccess) return e;
+            e = hipFree(slot.p);
+            if (e != hipSuccess) return e;
+        }
+        slot = Slot{p, cb, pb};
     }
-    *counters = (unsigned*)slot.first;
-    *parts = (float*)(slot.first + slot.second.first);
+    *counters = (unsigned*)slot.p;
+    *parts = (float*)(slot.p + slot.cb);
     return hipSuccess;
 }
 
+// Counters and partials for one launch: carved out of the caller's scratch
+// (bytes == 0: none given) or the library's workspace for the stream.
+hipError_t launch_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes, size_t pbytes,
+                            unsigned** counters, float** parts) {
+    if (!scratch) return library_workspace(st, cbytes, pbytes, counters, parts);
+    if (cbytes + pbytes > scratch->bytes) return hipErrorInvalidValue;
+    *counters = (unsigned*)scratch->base;
+    *parts = (float*)(scratch->base + cbytes);
+    // the counters must start at zero: cleared by a kernel on the stream
+    // (not a memset node, so a captured call replays correctly)
+    hipLaunchKernelGGL(k_zero_u32, dim3(16), dim3(256), 0, st, *counters, (int)(cbytes / 4));
+    return hipGetLastError();
+}
+
 template <int QT, int MT>
-hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, hipStream_t st) {
+hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
     auto k = k_gemm_split<QT, MT>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
@@ -400,24 +522,23 @@ hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, hipStream_t st) {
     unsigned* counters = nullptr;
     float* parts = nullptr;
     if (p.S > 1) {
-        const int T = (g.N + 15) / 16, rgs = (T + p.nt - 1) / p.nt;
-        e = workspace(st, (size_t)rgs * kSpCounterStride * 4, (size_t)p.S * g.N * ((g.M + 3) & ~3) * 4, &counters,
-                      &parts);
+        e = launch_workspace(scratch, st, counter_bytes(p), partial_bytes(g, p), &counters, &parts);
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kSpNC + kSpNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K,
-                       p.nt, p.S, p.nsgS, p.unit_bytes, g.Waux, g.C, g.ldc, g.out_f16, parts, counters);
+                       p.nt, p.S, p.nsgS, p.unit_bytes, g.Waux, g.C, g.ldc, g.out_f16, parts, counters, p.nx);
     return hipGetLastError();
 }
 
 template <int QT>
-hipError_t dispatch_split(const GemmArgs& g, const SplitPlan& p, hipStream_t st) {
-    return p.MT == 1 ? launch_split<QT, 1>(g, p, st) : launch_split<QT, 2>(g, p, st);
+hipError_t dispatch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
+    return p.MT == 1 ? launch_split<QT, 1>(g, p, scratch, st) : launch_split<QT, 2>(g, p, scratch, st);
 }
 
 // Up to kSpMaxJobs GEMMs of one format and one m-tile count in one launch.
 template <int QT, int MT>
-hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, hipStream_t st) {
+hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, int nx, const Scratch* scratch,
+                                hipStream_t st) {
     auto k = k_gemm_split_batched<QT, MT>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
@@ -433,22 +554,21 @@ hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, 
     // launches), then every job's partials, at 256-byte offsets
     size_t cb[kSpMaxJobs] = {}, pb[kSpMaxJobs] = {}, ctot = 0, ptot = 0;
     for (int i = 0; i < n; i++) {
-        if (ps[i].S == 1) continue;
-        const int T = (gs[i].N + 15) / 16, rgs = (T + ps[i].nt - 1) / ps[i].nt;
-        cb[i] = ((size_t)rgs * kSpCounterStride * 4 + 255) & ~(size_t)255;
-        pb[i] = ((size_t)ps[i].S * gs[i].N * ((gs[i].M + 3) & ~3) * 4 + 255) & ~(size_t)255;
+        cb[i] = counter_bytes(ps[i]);
+        pb[i] = partial_bytes(gs[i], ps[i]);
         ctot += cb[i];
         ptot += pb[i];
     }
     unsigned* counters = nullptr;
     float* parts = nullptr;
     if (ctot) {
-        e = workspace(st, ctot, ptot, &counters, &parts);
+        e = launch_workspace(scratch, st, ctot, ptot, &counters, &parts);
         if (e != hipSuccess) return e;
     }
     SplitJobs jobs = {};
     jobs.n = n;
     jobs.out_f16 = gs[0].out_f16;
+    jobs.nx = nx;
     int grid = 0, lds = 0;
     size_t co = 0, po = 0;
     for (int i = 0; i < n; i++) {
@@ -460,7 +580,10 @@ hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, 
                                g.lda, g.ldc, g.M, g.N, g.K, p.nt, p.S, p.nsgS, p.unit_bytes, grid};
         co += cb[i];
         po += pb[i];
-        grid += p.grid;
+        // with the XCD-local exchange every job starts on XCD 0 (its grid is
+        // padded to whole rounds of the XCD round robin; for S = 1 the padding
+        // workgroups exit at once)
+        grid += nx > 0 ? (p.grid + nx - 1) / nx * nx : p.grid;
         lds = std::max(lds, p.lds);
     }
     hipLaunchKernelGGL(k, dim3(grid), dim3(64 * (kSpNC + kSpNL)), lds, st, jobs);
@@ -472,41 +595,67 @@ hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, 
 bool split_supports(const GemmArgs& g) {
     SplitPlan p;
     if (g.qtype == QT_PLANES && ((uintptr_t)g.Waux & 15)) return false;
-    return plan_split(g, p);
+    return plan_split(g, p, device_xcds());
+}
+
+size_t split_scratch_bytes(const GemmArgs& g) {
+    SplitPlan p;
+    if (!plan_split(g, p, device_xcds())) return 0;
+    return counter_bytes(p) + partial_bytes(g, p);
 }
 
 bool split_batched_supports(const GemmArgs* gs, int n) {
     if (n < 1) return false;
+    const int nx = device_xcds();
     for (int i = 0; i < n; i++) {
         SplitPlan p;
         if (gs[i].qtype != gs[0].qtype || gs[i].out_f16 != gs[0].out_f16) return false;
         if ((gs[i].M <= 16) != (gs[0].M <= 16)) return false;      // one m-tile count per launch
         if (gs[i].qtype == QT_PLANES && ((uintptr_t)gs[i].Waux & 15)) return false;
-        if (!plan_split(gs[i], p)) return false;
+        if (!plan_split(gs[i], p, nx)) return false;
     }
     return true;
 }
 
-hipError_t gemm_split_batched(const GemmArgs* gs, int n, hipStream_t st) {
+size_t split_batched_scratch_bytes(const GemmArgs* gs, int n) {
+    const int nx = device_xcds();
+    size_t worst = 0;
+    for (int i0 = 0; i0 < n; i0 += kSpMaxJobs) {
+        size_t tot = 0;
+        for (int i = i0; i < std::min(n, i0 + kSpMaxJobs); i++) {
+            SplitPlan p;
+            if (plan_split(gs[i], p, nx)) tot += counter_bytes(p) + partial_bytes(gs[i], p);
+        }
+        worst = std::max(worst, tot);
+    }
+    return worst;
+}
+
+hipError_t gemm_split_batched(const GemmArgs* gs, int n, const Scratch* scratch, hipStream_t st) {
     if (!split_batched_supports(gs, n)) return hipErrorInvalidValue;
+    const int nx = device_xcds();
     for (int i0 = 0; i0 < n; i0 += kSpMaxJobs) {
         const int m = std::min(kSpMaxJobs, n - i0);
         SplitPlan ps[kSpMaxJobs];
-        for (int i = 0; i < m; i++) plan_split(gs[i0 + i], ps[i]);
+        int bnx = 0;                                     // XCD-local exchange if any job splits K
+        for (int i = 0; i < m; i++) {
+            plan_split(gs[i0 + i], ps[i], nx);
+            if (ps[i].nx) bnx = ps[i].nx;
+        }
         const bool mt1 = gs[0].M <= 16;
         hipError_t e;
         switch (gs[0].qtype) {
             case QT_Q4_K:
-                e = mt1 ? launch_split_batched<QT_Q4_K, 1>(gs + i0, ps, m, st)
-                        : launch_split_batched<QT_Q4_K, 2>(gs + i0, ps, m, st);
+                e = mt1 ? launch_split_batched<QT_Q4_K, 1>(gs + i0, ps, m, bnx, scratch, st)
+                        : launch_split_batched<QT_Q4_K, 2>(gs + i0, ps, m, bnx, scratch, st);
                 break;
             case QT_PLANES:
-                e = mt1 ? launch_split_batched<QT_PLANES, 1>(gs + i0, ps, m, st)
-                        : launch_split_batched<QT_PLANES, 2>(gs + i0, ps, m, st);
+                e = mt1 ? launch_split_batched<QT_PLANES, 1>(gs + i0, ps, m, bnx, scratch, st)
+                        : launch_split_batched<QT_PLANES, 2>(gs + i0, ps, m, bnx, scratch, st);
                 break;
             default:
-                e = mt1 ? launch_split_batched<QT_Q4_0, 1>(gs + i0, ps, m, st)
-                        : launch_split_batched<QT_Q4_0, 2>(gs + i0, ps, m, st);
+                e = mt1 ? launch_split_batched<QT_Q4_0, 1>(gs + i0, ps, m, bnx, scratch, st)
+                        : launch_split_batched<QT_Q4_0, 2>(gs + i0, ps, m, bnx, scratch, st);
                 break;
         }
         if (e != hipSuccess) return e;
@@ -514,13 +663,13 @@ hipError_t gemm_split_batched(const GemmArgs* gs, int n, hipStream_t st) {
     return hipSuccess;
 }
 
-hipError_t gemm_split(const GemmArgs& g, hipStream_t st) {
+hipError_t gemm_split(const GemmArgs& g, const Scratch* scratch, hipStream_t st) {
     SplitPlan p;
-    if (!plan_split(g, p)) return hipErrorInvalidValue;
+    if (!plan_split(g, p, device_xcds())) return hipErrorInvalidValue;
     switch (g.qtype) {
-        case QT_Q4_K: return dispatch_split<QT_Q4_K>(g, p, st);
-        case QT_PLANES: return dispatch_split<QT_PLANES>(g, p, st);
-        default: return dispatch_split<QT_Q4_0>(g, p, st);
+        case QT_Q4_K: return dispatch_split<QT_Q4_K>(g, p, scratch, st);
+        case QT_PLANES: return dispatch_split<QT_PLANES>(g, p, scratch, st);
+        default: return dispatch_split<QT_Q4_0>(g, p, scratch, st);
     }
 }
 

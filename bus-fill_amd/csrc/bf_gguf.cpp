@@ -21,8 +21,6 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
-#include <hip/hip_runtime.h>
-
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -30,7 +28,7 @@
 #include <vector>
 
 #include "busfill.h"
-#include "bf_launch.h"
+#include "bf_host.h"
 
 namespace {
 
@@ -327,15 +325,7 @@ bf_status bf_gguf_upload(const bf_gguf* g, const bf_gguf_tensor* t, void* dst, v
     if ((const uint8_t*)t->data < g->map || t->nbytes > g->size ||
         (const uint8_t*)t->data - g->map > (ptrdiff_t)(g->size - t->nbytes))
         return gguf_fail("tensor does not belong to this file");
-    hipStream_t st = (hipStream_t)stream;
-    if (hipMemcpyAsync(dst, t->data, t->nbytes, hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipStreamSynchronize(st) != hipSuccess) {
-        char text[96];
-        snprintf(text, sizeof text, "hipMemcpyAsync of %llu bytes failed", (unsigned long long)t->nbytes);
-        bf::set_last_error(text);
-        return BF_ERR_HIP;
-    }
-    return BF_OK;
+    return bf::copy_to_device(dst, t->data, t->nbytes, stream) ? BF_OK : BF_ERR_HIP;
 }
 
 }  // extern "C"

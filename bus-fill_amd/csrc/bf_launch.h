@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "bf_host.h"
+
 namespace bf {
 
 struct GemmArgs {
@@ -19,6 +21,14 @@ struct GemmArgs {
     int M, N, K;               // M <= 128 per launch (the front end slices larger M)
 };
 
+// Device memory a call may use for the K-split kernel's workspace instead of
+// the library's own (bytes == 0 never happens: a null Scratch* means "use the
+// library's workspace for the stream").
+struct Scratch {
+    uint8_t* base;             // 256-byte aligned
+    size_t bytes;
+};
+
 hipError_t gemm_mfma(const GemmArgs& g, hipStream_t st);
 hipError_t gemm_dot2(const GemmArgs& g, hipStream_t st);
 hipError_t gemm_simple(const GemmArgs& g, hipStream_t st);
@@ -30,15 +40,21 @@ hipError_t gemm_lds_batched(const GemmArgs* gs, int n, hipStream_t st);
 bool lds_batched_supports(const GemmArgs* gs, int n);
 hipError_t gemm_slab(const GemmArgs& g, hipStream_t st);
 bool slab_supports(const GemmArgs& g);
-hipError_t gemm_split(const GemmArgs& g, hipStream_t st);
+// The K-split kernel.  With S > 1 splits it needs a workspace (counters and
+// partials): from `scratch` when given (its counters are cleared by a kernel
+// on the stream first), else the library's per-stream workspace, allocated on
+// first use and never while the stream is capturing (then the call returns
+// hipErrorStreamCaptureUnsupported).  hipErrorInvalidValue when scratch is too
+// small.
+hipError_t gemm_split(const GemmArgs& g, const Scratch* scratch, hipStream_t st);
 bool split_supports(const GemmArgs& g);
+size_t split_scratch_bytes(const GemmArgs& g);      // 0 when the plan does not split K
 // Independent GEMMs of one format, one output type and one side of M = 16, in
 // launches of up to eight (their grids back to back).
-hipError_t gemm_split_batched(const GemmArgs* gs, int n, hipStream_t st);
+hipError_t gemm_split_batched(const GemmArgs* gs, int n, const Scratch* scratch, hipStream_t st);
 bool split_batched_supports(const GemmArgs* gs, int n);
+size_t split_batched_scratch_bytes(const GemmArgs* gs, int n);
 bool dot2_supports(const GemmArgs& g);
-// The calling thread's text for bf_last_error().
-void set_last_error(const char* text);
 
 hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
                        int N, int K, hipStream_t st);

@@ -78,62 +78,87 @@ __device__ __forceinline__ const uint8_t* w_piece(const uint8_t* W, const uint8_
     }
 }
 
-// Spin (with s_sleep) until the LDS word at `flag` is nonzero.  The bound only
-// guards against a hang if a producer were ever missing: no launch comes close.
-__device__ __forceinline__ void wait_flag(const int* flag) {
+// Bounded waits.  A wait ends when its producer signals; the bound only
+// guards against a hang if a producer were ever missing (a protocol bug: no
+// launch comes close to it).  A wait that reaches the bound marks the
+// workgroup poisoned before the wave goes on: it sets the LDS word `poison`
+// and waits for that write, so every LDS write the wave makes afterwards (and
+// every load it issues afterwards) is ordered behind it.  Each store of a
+// result first reads the poison word (poisoned()) and stores NaN instead of a
+// value if it is set, so a missing producer shows as a failed result, never as
+// a plausible wrong one.
+constexpr int kWaitBound = 1 << 20;
+
+__device__ __forceinline__ void mark_poison(int* poison) {
+    asm volatile("ds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" :: "v"(lds_addr(poison)), "v"(1) : "memory");
+}
+
+__device__ __forceinline__ bool poisoned(const int* poison) {
+    int v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(poison)) : "memory");
+    return __builtin_amdgcn_readfirstlane(v) != 0;
+}
+
+// Spin (with s_sleep) until the LDS word at `flag` is nonzero.
+__device__ __forceinline__ void wait_flag(const int* flag, int* poison) {
     const uint32_t a = lds_addr(flag);
-    for (int it = 0; it < (1 << 20); it++) {
+    for (int it = 0; it < kWaitBound; it++) {
         int v;
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
         if (__builtin_amdgcn_readfirstlane(v) != 0) return;
         __builtin_amdgcn_s_sleep(1);
     }
+    mark_poison(poison);
 }
 
 // Spin until the LDS word at `flag` equals v.
-__device__ __forceinline__ void wait_flag_value(const int* flag, int v) {
+__device__ __forceinline__ void wait_flag_value(const int* flag, int v, int* poison) {
     const uint32_t a = lds_addr(flag);
-    for (int it = 0; it < (1 << 20); it++) {
+    for (int it = 0; it < kWaitBound; it++) {
         int x;
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(x) : "v"(a) : "memory");
         if (__builtin_amdgcn_readfirstlane(x) == v) return;
         __builtin_amdgcn_s_sleep(1);
     }
+    mark_poison(poison);
 }
 
 // Spin until the LDS word at `flag` is at least n.
-__device__ __forceinline__ void wait_count(const int* flag, int n) {
+__device__ __forceinline__ void wait_count(const int* flag, int n, int* poison) {
     const uint32_t a = lds_addr(flag);
-    for (int it = 0; it < (1 << 20); it++) {
+    for (int it = 0; it < kWaitBound; it++) {
         int v;
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
         if (__builtin_amdgcn_readfirstlane(v) >= n) return;
         __builtin_amdgcn_s_sleep(1);
     }
+    mark_poison(poison);
 }
 
 // Spin until the n <= 64 consecutive LDS words from `flags` are all >= v0:
 // lane l polls word l, so one LDS read per round covers all of them.
-__device__ __forceinline__ void wait_flags(const int* flags, int n, int lane, int v0 = 1) {
+__device__ __forceinline__ void wait_flags(const int* flags, int n, int lane, int* poison, int v0 = 1) {
     const uint32_t a = lds_addr(flags + (lane < n ? lane : 0));
-    for (int it = 0; it < (1 << 20); it++) {
+    for (int it = 0; it < kWaitBound; it++) {
         int v;
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
         if (__builtin_amdgcn_ballot_w64(v < v0) == 0) return;
         __builtin_amdgcn_s_sleep(1);
     }
+    mark_poison(poison);
 }
 
 // Spin until the LDS word each lane names is nonzero in every lane with
 // `need`: one LDS read per round for up to 64 flags anywhere in LDS.
-__device__ __forceinline__ void wait_lanes(const int* flag, bool need) {
+__device__ __forceinline__ void wait_lanes(const int* flag, bool need, int* poison) {
     const uint32_t a = lds_addr(flag);
-    for (int it = 0; it < (1 << 20); it++) {
+    for (int it = 0; it < kWaitBound; it++) {
         int v;
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
         if (__builtin_amdgcn_ballot_w64(need && v == 0) == 0) return;
         __builtin_amdgcn_s_sleep(1);
     }
+    mark_poison(poison);
 }
 
 // Sets the LDS word at `flag` to 1 once every load this wave has issued has

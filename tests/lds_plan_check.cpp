@@ -19,10 +19,19 @@
 //     the sub-tile's last step, after its own steps).
 //   AC plans (small A): the compute waves load all of A before the barrier and
 //     wait for it (no dependence on the loaders), the loaders stream weights only.
+// Bounded waits: every wait of the kernel gives up after a bound, marks the
+// workgroup poisoned (an LDS word every store of a result reads first) and
+// goes on.  Runs with a planted missing producer (a step marker, one loader's
+// activation marker, a batch-1 step count that never comes) check that the
+// protocol still ends, that a wait gave up, and that every sub-tile whose
+// partials were computed from data that had not landed (or were overwritten)
+// is stored while the poison word is set, i.e. as NaN.  In runs without a
+// missing producer no wait may give up.
 // Exit status 0 and a summary line on success; the first violation otherwise.
 // With --self-test it instead runs the model on plans with planted mistakes
 // (activation rings whose slots wait for steps of later groups, a step ring
-// that is not whole groups of four) and succeeds only if every one is caught.
+// that is not whole groups of four, stores that ignore the poison word) and
+// succeeds only if every one is caught.
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -91,12 +100,25 @@ struct Order {
     }
 };
 
+// A producer that never delivers (planted by a run): the marker of step
+// `step`, loader 0's marker of activation segment `seg`, the count of step
+// `count` (batch 1).  `bound`: blocked polls before a wait gives up (0: never).
+struct Drop {
+    int step = -1, seg = -1, count = -1;
+    int bound = 0;
+    bool ignore_poison = false;        // planted mistake: stores that do not read the poison word
+};
+
 struct Model {
     const LdsShape& g;
     const LdsPlan& p;
     int nsteps, S, G4R;
     bool a_ring;
     Order ord;
+    Drop drop;
+    bool poison = false;
+    int giveups = 0, poisoned_out = 0;
+    std::vector<char> taint, taint_seg, reduced;
     // LDS state
     bool cleared = false;
     int at_barrier = 0;
@@ -108,19 +130,22 @@ struct Model {
     int counter = 0;
 
     struct Loader {
-        int j, g4 = 0, phase = 0, s_lo = 0, s_hi = 0, s2 = 0, s_next = 0, sw = 0, so = 0;
+        int j, g4 = 0, phase = 0, s_lo = 0, s_hi = 0, s2 = 0, s_next = 0, sw = 0, so = 0, spins = 0;
         bool done = false, at_bar = false;
     };
     struct Wave {
-        int c, e = -1, t = 0, s = 0, phase = 0, k = 0, red = 0;
+        int c, e = -1, t = 0, s = 0, phase = 0, k = 0, red = 0, spins = 0;
         bool done = false, at_bar = false;
     };
     std::vector<Loader> L;
     std::vector<Wave> W;
 
-    Model(const LdsShape& g_, const LdsPlan& p_, int nsteps_)
+    Model(const LdsShape& g_, const LdsPlan& p_, int nsteps_, Drop d = Drop())
         : g(g_), p(p_), nsteps(nsteps_), S(p_.nsub * nsteps_), G4R((p_.nslot + 3) >> 2),
-          a_ring(p_.RG && p_.na < nsteps_), ord(p_, nsteps_) {
+          a_ring(p_.RG && p_.na < nsteps_), ord(p_, nsteps_), drop(d) {
+        taint.assign(S, 0);
+        taint_seg.assign(nsteps, 0);
+        reduced.assign(p.nsub, 0);
         amark.assign(nsteps * kNL, 0);
         stepmark.assign(S, 0);
         segcount.assign(nsteps, 0);
@@ -140,6 +165,22 @@ struct Model {
         }
     }
     int wslot_of(int e) const { return ((e >> 2) % G4R) * 4 + (e & 3); }
+
+    // a blocked poll of a bounded wait: true while the wait goes on, false once
+    // it gives up (the poison word is set before the wave moves on)
+    bool still_waiting(int& spins) {
+        if (drop.bound == 0 || ++spins < drop.bound) return true;
+        spins = 0;
+        poison = true;
+        giveups++;
+        return false;
+    }
+    // a slot or order check: data read after a wait gave up (or overwritten after
+    // one) is garbage, which the poison word covers; otherwise a protocol bug
+    void violation(const char* what, int a = -1, int b = -1, int e = -1) {
+        if (!poison) fail(what, g, p, a, b);
+        if (e >= 0) taint[e] = 1;
+    }
 
     // one action of loader l; false if it is blocked
     bool step_loader(Loader& l) {
@@ -166,11 +207,12 @@ struct Model {
                 const int s2 = l.s2;
                 if (a_ring && s2 >= p.na) {
                     if (!cleared) fail("loader waits before the barrier", g, p, s2);
-                    if (segcount[s2 - p.na] != p.nsub) return false;
+                    if (segcount[s2 - p.na] != p.nsub && still_waiting(l.spins)) return false;
                 }
+                l.spins = 0;
                 const int k = s2 % p.na;
                 if (aslot[k] >= 0 && aslot[k] != s2 && segcount[aslot[k]] != p.nsub)
-                    fail("activation slot reused early", g, p, s2, aslot[k]);
+                    violation("activation slot reused early", s2, aslot[k]);
                 aslot[k] = s2;
                 l.s2++;
                 return true;
@@ -179,11 +221,12 @@ struct Model {
                 if (e < S) {
                     if (e >= p.nslot) {
                         if (!cleared) fail("loader waits before the barrier", g, p, e);
-                        if (stepmark[e - p.nslot] != 2) return false;
+                        if (stepmark[e - p.nslot] != 2 && still_waiting(l.spins)) return false;
                     }
+                    l.spins = 0;
                     const int k = wslot_of(e);
                     if (k >= (int)wslot.size() || (k >= p.nslot && p.nslot != S)) fail("step slot out of range", g, p, e, k);
-                    if (wslot[k] >= 0 && stepmark[wslot[k]] != 2) fail("step slot reused early", g, p, e, wslot[k]);
+                    if (wslot[k] >= 0 && stepmark[wslot[k]] != 2) violation("step slot reused early", e, wslot[k]);
                     wslot[k] = e;
                 }
                 l.phase = 3;
@@ -194,12 +237,13 @@ struct Model {
                     if (!l.at_bar) { l.at_bar = true; at_barrier++; }
                     if (!cleared) return false;
                 }
-                if (e < S) stepmark[e] = 1;
+                if (e < S && e != drop.step) stepmark[e] = 1;
                 l.phase = 1;
                 return true;
             }
             case 4: {                                          // the segments' markers
-                for (int s2 = l.s_lo; s2 < l.s_hi; s2++) amark[s2 * kNL + l.j] = 1;
+                for (int s2 = l.s_lo; s2 < l.s_hi; s2++)
+                    if (!(s2 == drop.seg && l.j == 0)) amark[s2 * kNL + l.j] = 1;
                 l.g4++;
                 l.phase = 0;
                 if (4 * l.g4 >= S) l.done = true;
@@ -215,9 +259,18 @@ struct Model {
         return true;
     }
 
+    // sub-tile t is reduced and stored (after the wave read the poison word)
     void check_reduce(int t) {
-        for (int s2 = 0; s2 < nsteps; s2++)
-            if (!parked[t * nsteps + s2]) fail("sub-tile reduced before all its partials", g, p, t, s2);
+        bool tainted = false;
+        for (int s2 = 0; s2 < nsteps; s2++) {
+            if (!parked[t * nsteps + s2]) violation("sub-tile reduced before all its partials", t, s2);
+            tainted = tainted || !parked[t * nsteps + s2] || taint[t * nsteps + s2];
+        }
+        const bool nan = poison && !drop.ignore_poison;
+        if (tainted && !nan) fail("sub-tile stored from data that had not landed, without the poison word", g, p, t);
+        if (reduced[t]) fail("sub-tile stored twice", g, p, t);
+        reduced[t] = 1;
+        poisoned_out += nan;
     }
 
     bool step_wave(Wave& w) {
@@ -239,27 +292,44 @@ struct Model {
             }
             case 2:                                            // block sums by the segment's first step
                 if (!p.BD && g.q4k && w.t == 0) {
-                    if (!seg_landed(w.s)) return false;
-                    if (aslot[w.s % p.na] != w.s) fail("block sums of a segment not in its slot", g, p, w.s);
+                    if (!seg_landed(w.s)) {
+                        if (still_waiting(w.spins)) return false;
+                        taint_seg[w.s] = 1;                    // tabulated from activations that had not landed
+                    }
+                    w.spins = 0;
+                    if (aslot[w.s % p.na] != w.s) {
+                        violation("block sums of a segment not in its slot", w.s);
+                        taint_seg[w.s] = 1;
+                    }
                     tabflag[w.s] = 1;
                 }
                 w.phase = 3;
                 return true;
-            case 3:                                            // markers, read, release
-                if (!p.BD && !seg_landed(w.s)) return false;
-                if (!p.BD && g.q4k && !tabflag[w.s]) return false;
-                if (stepmark[w.e] == 0) return false;
-                if (wslot[wslot_of(w.e)] != w.e) fail("step read from a slot holding another step", g, p, w.e);
-                if (!p.BD && aslot[w.s % p.na] != w.s) fail("activations read from a slot holding another segment", g, p, w.s);
+            case 3: {                                          // markers, read, release
+                const bool ready = (p.BD || seg_landed(w.s)) && (p.BD || !g.q4k || tabflag[w.s]) && stepmark[w.e] != 0;
+                if (!ready) {
+                    if (still_waiting(w.spins)) return false;
+                    taint[w.e] = 1;                            // read before its data landed
+                }
+                w.spins = 0;
+                if (wslot[wslot_of(w.e)] != w.e) violation("step read from a slot holding another step", w.e, -1, w.e);
+                if (!p.BD && aslot[w.s % p.na] != w.s)
+                    violation("activations read from a slot holding another segment", w.s, -1, w.e);
                 stepmark[w.e] = 2;
                 w.phase = 4;
                 return true;
+            }
             case 4: {                                          // compute, count, park
-                if (!p.BD && aslot[w.s % p.na] != w.s) fail("activation slot changed under a step", g, p, w.s);
+                if (!p.BD && aslot[w.s % p.na] != w.s) violation("activation slot changed under a step", w.s, -1, w.e);
                 if (a_ring) segcount[w.s]++;
                 const int idx = w.t * nsteps + w.s;
                 if (parked[idx]) fail("partial parked twice", g, p, w.t, w.s);
                 parked[idx] = 1;
+                if (taint_seg[w.s]) taint[idx] = 1;
+                if (w.e == drop.count) {                       // a count that never comes (batch 1)
+                    w.phase = 1;
+                    return true;
+                }
                 if (++subcount[w.t] == nsteps && !p.BD) check_reduce(w.t);
                 w.phase = 1;
                 return true;
@@ -267,7 +337,11 @@ struct Model {
             case 5: {                                          // batch 1: the sub-tiles whose last step this wave took
                 while (w.red < p.nsub && (w.red * nsteps + nsteps - 1) % kNC != w.c) w.red++;
                 if (w.red >= p.nsub) { w.phase = 6; return true; }
-                if (subcount[w.red] != nsteps) return false;
+                if (subcount[w.red] != nsteps) {
+                    if (still_waiting(w.spins)) return false;
+                    taint[w.red * nsteps] = 1;                 // reduced without every count
+                }
+                w.spins = 0;
                 check_reduce(w.red);
                 w.red++;
                 return true;
@@ -324,8 +398,39 @@ struct Model {
         }
         for (int i = 0; i < S; i++)
             if (!parked[i]) fail("step never computed", g, p, i);
+        for (int t = 0; t < p.nsub; t++)
+            if (!reduced[t]) fail("sub-tile never stored", g, p, t);
+        const bool planted = drop.step >= 0 || drop.seg >= 0 || drop.count >= 0;
+        if (!planted && giveups) fail("a wait gave up without a missing producer", g, p, giveups);
+        if (planted && (!giveups || !poison || !poisoned_out)) fail("missing producer not seen as poison", g, p, giveups);
     }
 };
+
+// Runs with a planted missing producer under three schedules; throws on the first violation.
+void run_drops(const LdsShape& g, const LdsPlan& p, int nsteps, uint64_t seed, bool ignore_poison = false) {
+    const int S = p.nsub * nsteps;
+    std::vector<Drop> drops;
+    Drop d;
+    d.bound = 60;
+    d.ignore_poison = ignore_poison;
+    d.step = S / 2;
+    drops.push_back(d);
+    d.step = -1;
+    if (!p.BD && !p.AC) {
+        d.seg = nsteps / 2;
+        drops.push_back(d);
+        d.seg = -1;
+    }
+    if (p.BD) {
+        d.count = S - 1;
+        drops.push_back(d);
+    }
+    for (const Drop& dr : drops)
+        for (int mode = 0; mode < 3; mode++) {
+            Model m(g, p, nsteps, dr);
+            m.run(seed + 31u * mode, mode);
+        }
+}
 
 void check_bounds(const LdsShape& g, const LdsPlan& p) {
     const int nsg = g.K / 256, nsteps = nsg / p.G, R = 16 / p.G, S = p.nsub * nsteps;
@@ -386,6 +491,24 @@ int self_test() {
     }
     c.nslot = 18;                      // not whole groups of four: slots beyond the ring or reused early
     expect_failure("step ring of 18 slots", g2, c);
+    // stores that do not read the poison word, after a wait gave up on a missing producer
+    auto expect_drop_failure = [&](const char* name, const LdsShape& gg) {
+        planted++;
+        LdsPlan pp{};
+        if (!choose_lds(gg, pp)) {
+            std::printf("no plan for %s\n", name);
+            return;
+        }
+        try {
+            run_drops(gg, pp, gg.K / 256 / pp.G, 11u, true);
+            std::printf("not caught: %s\n", name);
+        } catch (const std::exception& e) {
+            caught++;
+            std::printf("caught %s: %s\n", name, e.what());
+        }
+    };
+    expect_drop_failure("batch 1 stores that ignore the poison word", LdsShape{1, 5120, 5120, true});
+    expect_drop_failure("batch 8 stores that ignore the poison word", LdsShape{8, 5120, 17408, true});
     std::printf("%d of %d planted mistakes caught\n", caught, planted);
     return caught == planted ? 0 : 1;
 }
@@ -394,7 +517,7 @@ int main(int argc, char** argv) {
     if (argc > 1 && std::strcmp(argv[1], "--self-test") == 0) return self_test();
     const int Ns[] = {1, 77, 512, 600, 1024, 3072, 4096, 5120, 7168, 13824, 17408, 27648};
     const int Ks[] = {256, 1024, 2048, 3072, 4096, 5120, 8192, 13824, 17408, 24576, 27648};
-    int plans = 0, rings = 0, aring = 0, ac = 0, runs = 0;
+    int plans = 0, rings = 0, aring = 0, ac = 0, runs = 0, drop_plans = 0;
     for (int q = 0; q < 2; q++)
         for (int M = 1; M <= 16; M++)
             for (int N : Ns)
@@ -419,12 +542,17 @@ int main(int argc, char** argv) {
                                 m.run((uint64_t)(sd * 7 + mode) * 1000003u + (uint64_t)(M * 131 + N) * 17u + K, mode);
                                 runs++;
                             }
+                        // every fifth plan: bounded waits against a missing producer
+                        if (plans % 5 == 0) {
+                            run_drops(g, p, nsteps, (uint64_t)(M * 131 + N) * 17u + K);
+                            drop_plans++;
+                        }
                     } catch (const std::exception& e) {
                         std::printf("FAIL %s\n", e.what());
                         return 1;
                     }
                 }
-    std::printf("ok: %d plans (%d with a step ring, %d with windows / activation ring), %d model runs, %d AC\n",
-                plans, rings, aring, runs, ac);
+    std::printf("ok: %d plans (%d with a step ring, %d with windows / activation ring), %d model runs, %d AC, "
+                "%d with missing producers\n", plans, rings, aring, runs, ac, drop_plans);
     return 0;
 }

@@ -446,6 +446,12 @@ def test_batched_matches_single_launches(dev, qt, Ms, otype):
         for i, (C, ref) in enumerate(zip(Cs, singles)):
             got = C.float().cpu().numpy().astype(np.float64)
             assert (got == ref).all(), (rep, i, BATCH_SHAPES[i], Ms[i])
+            if rep == 0:
+                # and each batched output against the oracle itself
+                if otype == bf.OUT_F32:
+                    Ref(ws[i], As[i]).check(got, f"batched {QT_NAME[qt]} {BATCH_SHAPES[i]} M={Ms[i]}")
+                else:
+                    assert_gate(got, O.gemm_f64(ws[i], As[i]), f"batched f16 {QT_NAME[qt]} {BATCH_SHAPES[i]}")
 
 
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
@@ -721,3 +727,17 @@ def test_gemm_q8_full_size_strided_f16_and_deterministic(dev):
     ref, mag = O.gemm_q8(w, q, d, s)
     tol = (K / 32 + 32) * 2.0 ** -24 * mag + np.abs(ref) * 2.0 ** -11 + 6e-8
     assert (np.abs(C[:M, :N].astype(np.float64) - ref) <= tol).all()
+
+
+@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408)])
+def test_sweep_shapes_full_size_large_batches(dev, N, K):
+    """The batch sweep's two 50 MB shapes at full size against the oracle at
+    M = 16, 32, 64 and 128 (the K-split plans at N = 17408 and K = 17408, and the
+    large-batch path), through the automatic choice."""
+    w = O.gen_weights(O.Q4_K, N, K, seed=N * 3 + K)
+    dw = upload(w, dev)
+    A = O.gen_act(128, K, seed=K + 128)
+    ref = Ref(w, A)
+    for M in (16, 32, 64, 128):
+        C = gpu_gemm(w, A[:M], dev, dw=dw)
+        ref.check(C, f"q4_k {N}x{K} M={M}", rows=M)
