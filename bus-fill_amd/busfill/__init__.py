@@ -29,7 +29,7 @@ OUT_F32, OUT_F16 = 0, 1
 # bf_algo
 ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT = 0, 1, 2, 3, 4, 5, 6
 
-EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
+EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_noalloc", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
            "bf_swiglu_f16", "bf_q8_bytes", "bf_quantize_q8", "bf_gemm_q8",
            "bf_gguf_open", "bf_gguf_close", "bf_gguf_tensor_count", "bf_gguf_tensor_at", "bf_gguf_find",
            "bf_gguf_get_u64", "bf_gguf_get_str", "bf_gguf_upload",
@@ -75,6 +75,7 @@ def lib() -> ctypes.CDLL:
         L.bf_busfill_q4.argtypes = [vp, vp, vp, vp, i, i, i, vp]
         L.bf_gemm.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
         L.bf_gemm_ex.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, i, vp]
+        L.bf_gemm_noalloc.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
         L.bf_dequant_f16.argtypes = [i, vp, vp, vp, i, i, vp]
         L.bf_gemm_batched.argtypes = [i, i, i, ctypes.POINTER(GemmDesc), vp]
         L.bf_gemm_swiglu.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
@@ -97,7 +98,7 @@ def lib() -> ctypes.CDLL:
         for f in ("bf_gguf_open", "bf_gguf_tensor_at", "bf_gguf_find", "bf_gguf_get_u64", "bf_gguf_get_str",
                   "bf_gguf_upload"):
             getattr(L, f).restype = i
-        for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
+        for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_noalloc", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
                   "bf_swiglu_f16", "bf_quantize_q8", "bf_gemm_q8"):
             getattr(L, f).restype = i
         L.bf_status_str.argtypes = [i]
@@ -139,6 +140,15 @@ def gemm(qtype: int, W, W_aux, A, C, M: int, N: int, K: int, *, lda: int | None 
     st = lib().bf_gemm_ex(qtype, _ptr(W), _ptr(W_aux), _ptr(A), K if lda is None else lda,
                           _ptr(C), N if ldc is None else ldc, otype, M, N, K, algo, _stream(stream))
     _check(st, "bf_gemm_ex")
+
+
+def gemm_noalloc(qtype: int, W, W_aux, A, C, M: int, N: int, K: int, *, lda: int | None = None,
+                 ldc: int | None = None, otype: int = OUT_F32, stream=None) -> None:
+    """bf_gemm_noalloc: bf_gemm with the K-split scratch in a per-GPU static
+    array instead of a workspace allocated per stream."""
+    st = lib().bf_gemm_noalloc(qtype, _ptr(W), _ptr(W_aux), _ptr(A), K if lda is None else lda,
+                               _ptr(C), N if ldc is None else ldc, otype, M, N, K, _stream(stream))
+    _check(st, "bf_gemm_noalloc")
 
 
 def gemm_swiglu(qtype: int, W, W_aux, gate_up, C, M: int, N: int, K: int, *, ld: int | None = None,

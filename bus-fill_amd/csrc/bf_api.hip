@@ -2,6 +2,7 @@
 // Declarations and the reference interfaces they replace: include/busfill.h.
 #include "busfill.h"
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -83,7 +84,8 @@ bf_status check_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uin
 }
 
 bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
-                   int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream) {
+                   int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream,
+                   const bf::Scratch* scratch = nullptr) {
     g_last_error[0] = '\0';
     bf_status st = check_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K);
     if (st != BF_OK) return st;
@@ -110,7 +112,7 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
         probe.K = K;
         if (fast_eligible(probe) && bf::split_supports(probe)) slice = kSplitMaxM;
     }
-    for (int m0 = 0; m0 < M; m0 += slice) {
+    auto slice_args = [&](int m0) {
         bf::GemmArgs g;
         g.qtype = (int)qtype;
         g.W = (const uint8_t*)W;
@@ -123,17 +125,33 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
         g.M = M - m0 < slice ? M - m0 : slice;
         g.N = N;
         g.K = K;
-
-        bf_algo use = algo;
-        const bool fast = fast_eligible(g);
-        if (use == BF_ALGO_AUTO) {
-            if (!fast) use = BF_ALGO_SIMPLE;
-            else if (bf::lds_supports(g)) use = BF_ALGO_LDS;
-            else if (bf::split_supports(g)) use = BF_ALGO_SPLIT;
-            else if (bf::slab_supports(g)) use = BF_ALGO_SLAB;
-            else if (g.M <= kDot2MaxM && bf::dot2_supports(g)) use = BF_ALGO_DOT2;
-            else use = BF_ALGO_MFMA;
+        return g;
+    };
+    auto choose = [&](const bf::GemmArgs& g, bool fast) {
+        if (algo != BF_ALGO_AUTO) return algo;
+        if (!fast) return BF_ALGO_SIMPLE;
+        if (bf::lds_supports(g)) return BF_ALGO_LDS;
+        if (bf::split_supports(g)) return BF_ALGO_SPLIT;
+        if (bf::slab_supports(g)) return BF_ALGO_SLAB;
+        if (g.M <= kDot2MaxM && bf::dot2_supports(g)) return BF_ALGO_DOT2;
+        return BF_ALGO_MFMA;
+    };
+    if (scratch) {
+        // a call with caller-bounded scratch is checked whole before anything is enqueued
+        for (int m0 = 0; m0 < M; m0 += slice) {
+            const bf::GemmArgs g = slice_args(m0);
+            const bool fast = fast_eligible(g);
+            if (choose(g, fast) != BF_ALGO_SPLIT || !fast || !bf::split_supports(g)) continue;
+            const size_t need = bf::split_scratch_bytes(g);
+            if (need > scratch->bytes)
+                return fail(BF_ERR_INVALID, "M=%d N=%d K=%d needs %zu bytes of K-split scratch, more than the "
+                            "%zu bytes bf_gemm_noalloc holds per GPU", g.M, N, K, need, scratch->bytes);
         }
+    }
+    for (int m0 = 0; m0 < M; m0 += slice) {
+        const bf::GemmArgs g = slice_args(m0);
+        const bool fast = fast_eligible(g);
+        const bf_algo use = choose(g, fast);
         hipError_t e;
         switch (use) {
             case BF_ALGO_MFMA:
@@ -155,7 +173,7 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
                 if (!fast || !bf::split_supports(g))
                     return fail(BF_ERR_UNSUPPORTED, "K-split path does not serve qtype %d M=%d N=%d K=%d",
                                 (int)qtype, g.M, N, K);
-                e = bf::gemm_split(g, nullptr, hs);
+                e = bf::gemm_split(g, scratch, hs);
                 break;
             case BF_ALGO_LDS:
                 if (!fast || !bf::lds_supports(g))
@@ -173,6 +191,37 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
     return BF_OK;
 }
 
+// Scratch of bf_gemm_noalloc: the K-split kernel's row-group counters and
+// partial sums, in place of the workspace bf_gemm allocates per stream.  Each
+// GPU the library runs on holds its own copy until the process ends.  In host
+// code `scratch` only names the symbol: its device address comes from
+// hipGetSymbolAddress (noalloc_scratch), once per device.
+constexpr size_t kNoallocScratch = 32u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoallocScratch];
+
+constexpr int kMaxDevices = 64;
+std::atomic<uint8_t*> g_scratch_ptr[kMaxDevices];
+
+// The current device's copy of `scratch`: looked up on the first call on each
+// device (with that device current) and kept.
+bf_status noalloc_scratch(uint8_t** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(BF_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(BF_ERR_UNSUPPORTED, "device %d: bf_gemm_noalloc serves devices 0-%d", dev, kMaxDevices - 1);
+    uint8_t* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        void* addr = nullptr;
+        e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !addr) return fail(BF_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        p = (uint8_t*)addr;
+        g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return BF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -185,6 +234,16 @@ bf_status bf_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16
 bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
                      int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream) {
     return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, algo, stream);
+}
+
+bf_status bf_gemm_noalloc(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
+                          int ldc, bf_otype otype, int M, int N, int K, void* stream) {
+    g_last_error[0] = '\0';
+    uint8_t* p = nullptr;
+    const bf_status st = noalloc_scratch(&p);
+    if (st != BF_OK) return st;
+    const bf::Scratch sc{p, kNoallocScratch};
+    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, BF_ALGO_AUTO, stream, &sc);
 }
 
 bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs, void* stream) {

@@ -89,6 +89,26 @@ bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux,
                      const uint16_t* A, int lda, void* C, int ldc, bf_otype otype,
                      int M, int N, int K, bf_algo algo, void* stream);
 
+/* bf_gemm that allocates nothing, for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference, whose kernel needs no scratch.
+ * Same arguments, kernels and results as bf_gemm, bit for bit; where bf_gemm's
+ * K-split kernel (9-32 batch rows per launch when the activations do not fit
+ * in LDS) uses the workspace it allocates per stream, this call uses a 32 MiB
+ * scratch array in device memory that each GPU holds for the life of the
+ * process.  It calls no hipMalloc or hipFree; its first call on a device looks
+ * up that device's array (hipGetSymbolAddress).  Every call on one GPU shares
+ * the array: calls that overlap on one GPU (concurrent streams, or a captured
+ * graph replayed while another such call runs) race and may return wrong
+ * results.  Each K-split launch first clears the array's counters with a small
+ * kernel on the stream (no memset node in a captured graph).  Returns
+ * BF_ERR_INVALID, enqueueing nothing, for a shape whose K-split launches need
+ * more than 32 MiB of scratch (partials of S K-splits x N x M rows in fp32;
+ * 11 MB at the 27B-class layer's largest shapes at M = 32). */
+bf_status bf_gemm_noalloc(bf_qtype qtype, const void* W, const void* W_aux,
+                          const uint16_t* A, int lda, void* C, int ldc, bf_otype otype,
+                          int M, int N, int K, void* stream);
+
 /* One GEMM of a batch: bf_gemm's arguments C[0:M][0:N] = A[0:M][0:K] . dequant(W)^T. */
 typedef struct {
     const void* W;
