@@ -12,7 +12,19 @@
  * describes in RESULTS.md:84-96) with a host-callable function.
  *
  * Conventions
- *   - All pointers are DEVICE pointers owned by the caller; nothing is allocated.
+ *   - All pointers are DEVICE pointers owned by the caller.  The one device
+ *     memory the library allocates itself is the K-split kernel's workspace
+ *     (BF_ALGO_SPLIT, which bf_gemm picks for 9-32 batch rows per launch when
+ *     the activations do not fit in LDS): split partials and row-group
+ *     counters, one workspace per (device, stream) -- per host thread for
+ *     hipStreamPerThread -- allocated by the first such call on the stream,
+ *     grown (the old buffer freed once the stream has passed it) and kept
+ *     until the process ends.  It is never allocated while the stream is being
+ *     captured into a graph: such a call returns BF_ERR_UNSUPPORTED; make one
+ *     uncaptured call of the shape on the stream first, or use
+ *     bf_gemm_noalloc.  A captured graph holds the workspace of the stream it
+ *     was captured on: replaying it while other K-split work runs on that
+ *     stream (or another replay of it) races.
  *   - fp16 values travel as uint16_t bit patterns.
  *   - A is [M][lda] row-major fp16, C is [M][ldc] row-major (fp32 or fp16),
  *     W is [N][K] in the chosen block format: C = A . dequant(W)^T.
@@ -20,8 +32,10 @@
  *     work; they are asynchronous with respect to the host.
  *   - Shapes, alignments and pointers are validated before anything is
  *     enqueued; a rejected call returns BF_ERR_INVALID and touches nothing.
- *   - The library holds no global mutable state apart from a thread-local
- *     text of the last error (bf_last_error).
+ *   - Global state: the thread-local text of the last error (bf_last_error),
+ *     per-device records that a kernel's LDS limit has been raised and of the
+ *     device's XCD count, the K-split workspaces above, and the per-GPU
+ *     address of bf_gemm_noalloc's scratch array.
  */
 #ifndef BUSFILL_H
 #define BUSFILL_H
