@@ -466,12 +466,14 @@ def main():
     ap.add_argument("--layer-m", type=int, default=32, help="layer workload: batch rows (config: 32)")
     ap.add_argument("--layer-launch", default="both", choices=["single", "batched", "both"],
                     help="layer workload: one bf_gemm per linear, one bf_gemm_batched per layer, or both")
-    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "dot2", "simple", "lds", "slab", "split"])
+    ap.add_argument("--algo", default="auto",
+                    choices=["auto", "mfma", "dot2", "simple", "lds", "slab", "split", "dense"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--out", default=None, help="also write the full record to this JSON file")
     args = ap.parse_args()
-    args.algo_id = {"auto": 0, "mfma": 1, "dot2": 2, "simple": 3, "lds": 4, "slab": 5, "split": 6}[args.algo]
+    args.algo_id = {"auto": 0, "mfma": 1, "dot2": 2, "simple": 3, "lds": 4, "slab": 5, "split": 6,
+                    "dense": 7}[args.algo]
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the GEMM runs on a single MI355X and there is no "

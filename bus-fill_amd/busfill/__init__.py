@@ -27,7 +27,7 @@ Q4_0, Q4_0_PLANES, Q4_K = 0, 1, 2
 # bf_otype
 OUT_F32, OUT_F16 = 0, 1
 # bf_algo
-ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT = 0, 1, 2, 3, 4, 5, 6
+ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT, ALGO_DENSE = 0, 1, 2, 3, 4, 5, 6, 7
 
 EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_noalloc", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
            "bf_swiglu_f16", "bf_q8_bytes", "bf_quantize_q8", "bf_gemm_q8",

@@ -89,14 +89,17 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
     g_last_error[0] = '\0';
     bf_status st = check_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K);
     if (st != BF_OK) return st;
-    if (algo < BF_ALGO_AUTO || algo > BF_ALGO_SPLIT) return fail(BF_ERR_INVALID, "unknown algo %d", (int)algo);
+    if (algo < BF_ALGO_AUTO || algo > BF_ALGO_DENSE) return fail(BF_ERR_INVALID, "unknown algo %d", (int)algo);
 
     const size_t csize = otype == BF_OUT_F32 ? 4 : 2;
     hipStream_t hs = (hipStream_t)stream;
-    // Batches above 32 rows: the K-split kernel over slices of 32 rows (the
-    // weights are streamed once per slice) beats the register-streaming MFMA
+    // Batches above 32 rows: the dense kernel, all batch rows of a launch per
+    // workgroup (the weights streamed once per 128 rows); where it cannot
+    // serve the shape, the K-split kernel over slices of 32 rows (the weights
+    // streamed once per slice), which beats the register-streaming MFMA
     // kernel, whose activation traffic grows with every 16-row tile.
     int slice = kMaxMPerLaunch;
+    bool dense_slices = false;
     if (algo == BF_ALGO_AUTO && M > kSplitMaxM) {
         bf::GemmArgs probe;
         probe.qtype = (int)qtype;
@@ -107,10 +110,12 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
         probe.C = C;
         probe.ldc = ldc;
         probe.out_f16 = otype == BF_OUT_F16;
-        probe.M = kSplitMaxM;
+        probe.M = M < kMaxMPerLaunch ? M : kMaxMPerLaunch;
         probe.N = N;
         probe.K = K;
-        if (fast_eligible(probe) && bf::split_supports(probe)) slice = kSplitMaxM;
+        dense_slices = fast_eligible(probe) && bf::dense_supports(probe);
+        probe.M = kSplitMaxM;
+        if (!dense_slices && fast_eligible(probe) && bf::split_supports(probe)) slice = kSplitMaxM;
     }
     auto slice_args = [&](int m0) {
         bf::GemmArgs g;
@@ -132,6 +137,7 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
         if (!fast) return BF_ALGO_SIMPLE;
         if (bf::lds_supports(g)) return BF_ALGO_LDS;
         if (bf::split_supports(g)) return BF_ALGO_SPLIT;
+        if (dense_slices && bf::dense_supports(g)) return BF_ALGO_DENSE;
         if (bf::slab_supports(g)) return BF_ALGO_SLAB;
         if (g.M <= kDot2MaxM && bf::dot2_supports(g)) return BF_ALGO_DOT2;
         return BF_ALGO_MFMA;
@@ -141,8 +147,11 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
         for (int m0 = 0; m0 < M; m0 += slice) {
             const bf::GemmArgs g = slice_args(m0);
             const bool fast = fast_eligible(g);
-            if (choose(g, fast) != BF_ALGO_SPLIT || !fast || !bf::split_supports(g)) continue;
-            const size_t need = bf::split_scratch_bytes(g);
+            const bf_algo use = choose(g, fast);
+            size_t need = 0;
+            if (use == BF_ALGO_SPLIT && fast && bf::split_supports(g)) need = bf::split_scratch_bytes(g);
+            else if (use == BF_ALGO_DENSE && fast && bf::dense_supports(g)) need = bf::dense_scratch_bytes(g, scratch->bytes);
+            else continue;
             if (need > scratch->bytes)
                 return fail(BF_ERR_INVALID, "M=%d N=%d K=%d needs %zu bytes of K-split scratch, more than the "
                             "%zu bytes bf_gemm_noalloc holds per GPU", g.M, N, K, need, scratch->bytes);
@@ -175,6 +184,12 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
                                 (int)qtype, g.M, N, K);
                 e = bf::gemm_split(g, scratch, hs);
                 break;
+            case BF_ALGO_DENSE:
+                if (!fast || !bf::dense_supports(g))
+                    return fail(BF_ERR_UNSUPPORTED, "dense path does not serve qtype %d M=%d N=%d K=%d",
+                                (int)qtype, g.M, N, K);
+                e = bf::gemm_dense(g, scratch, hs);
+                break;
             case BF_ALGO_LDS:
                 if (!fast || !bf::lds_supports(g))
                     return fail(BF_ERR_UNSUPPORTED, "LDS-staged path does not serve M=%d N=%d K=%d with these alignments",
@@ -185,7 +200,8 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
                 e = bf::gemm_simple(g, hs);
                 break;
         }
-        st = use == BF_ALGO_SPLIT ? from_split(e, "kernel launch") : from_hip(e, "kernel launch");
+        st = use == BF_ALGO_SPLIT || use == BF_ALGO_DENSE ? from_split(e, "kernel launch")
+                                                           : from_hip(e, "kernel launch");
         if (st != BF_OK) return st;
     }
     return BF_OK;

@@ -54,6 +54,91 @@
 
 namespace bf {
 namespace {
+__global__ void k_zero_u32(unsigned* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+}  // namespace
+
+// XCDs of the current device: the workgroup round robin the XCD-local exchange
+// lays its grid out for (1 on a device with one XCD per agent).
+int device_xcds() {
+    static std::atomic<int> cache[64];                 // 0: not queried yet
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || v < 1 || v > 16) v = -1;
+        cache[dev].store(v, std::memory_order_relaxed);
+        n = v;
+    }
+    return n > 0 ? n : 0;                                // unknown: device-scope exchange
+}
+
+// The library's own workspaces, one per (device, stream): launches on one
+// stream are ordered, so they can share it.  hipStreamPerThread names a
+// different stream in every host thread, so it is keyed by the thread too.
+// Grown on demand: the old buffer is freed once the stream has finished with
+// it.  Never allocated while the stream is being captured into a graph (an
+// allocation cannot be captured): such a call fails with
+// hipErrorStreamCaptureUnsupported unless a large enough workspace exists.
+hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t pbytes, unsigned** counters, float** parts) {
+    struct Slot {
+        uint8_t* p = nullptr;
+        size_t cb = 0, pb = 0;
+    };
+    static std::mutex mu;
+    static std::map<std::tuple<int, uintptr_t, std::thread::id>, Slot> cache;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const std::thread::id tid = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+    std::lock_guard<std::mutex> lock(mu);
+    Slot& slot = cache[{dev, (uintptr_t)st, tid}];
+    if (!slot.p || slot.cb < cbytes || slot.pb < pbytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(st, &cs);
+        if (e != hipSuccess) return e;
+        if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+        const size_t cb = std::max(cbytes, slot.cb), pb = std::max(pbytes, slot.pb);
+        uint8_t* p = nullptr;
+        e = hipMalloc((void**)&p, cb + pb);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_zero_u32, dim3(64), dim3(256), 0, st, (unsigned*)p, (int)(cb / 4));
+        e = hipGetLastError();
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return e;
+        }
+        if (slot.p) {
+            // launches already queued on the stream may still use the old buffer
+            e = hipStreamSynchronize(st);
+            if (e != hipSuccess) return e;
+            e = hipFree(slot.p);
+            if (e != hipSuccess) return e;
+        }
+        slot = Slot{p, cb, pb};
+    }
+    *counters = (unsigned*)slot.p;
+    *parts = (float*)(slot.p + slot.cb);
+    return hipSuccess;
+}
+
+// Counters and partials for one launch: carved out of the caller's scratch
+// (bytes == 0: none given) or the library's workspace for the stream.
+hipError_t split_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes, size_t pbytes,
+                            unsigned** counters, float** parts) {
+    if (!scratch) return library_workspace(st, cbytes, pbytes, counters, parts);
+    if (cbytes + pbytes > scratch->bytes) return hipErrorInvalidValue;
+    *counters = (unsigned*)scratch->base;
+    *parts = (float*)(scratch->base + cbytes);
+    // the counters must start at zero: cleared by a kernel on the stream
+    // (not a memset node, so a captured call replays correctly)
+    hipLaunchKernelGGL(k_zero_u32, dim3(16), dim3(256), 0, st, *counters, (int)(cbytes / 4));
+    return hipGetLastError();
+}
+
+namespace {
 
 // LDS: [0, 2048) flags: owners-done counter at 4, is-last word at 8, poison
 // word at 12 (a bounded wait gave up), unit markers of loader j for unit i at
@@ -370,9 +455,6 @@ void k_gemm_split_batched(const SplitJobs jobs) {
                        j.unit_bytes, j.Waux, j.C, j.ldc, jobs.out_f16, j.ws, j.counters, jobs.nx);
 }
 
-__global__ void k_zero_u32(unsigned* p, int n) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
-}
 
 struct SplitPlan {
     int S, nt, nsgS, MT, grid, unit_bytes, lds, nx, rgs;
@@ -382,22 +464,6 @@ int split_lds_bytes(int M, int nt, int nsgS, int MT) {
     const int unit = (M * 33 + nt * 144) * 16;
     const int parks = (kSpNC > nt ? kSpNC - nt : 0) * MT * 1024;
     return kSpFlags + nsgS * unit + parks;
-}
-
-// XCDs of the current device: the workgroup round robin the XCD-local exchange
-// lays its grid out for (1 on a device with one XCD per agent).
-int device_xcds() {
-    static std::atomic<int> cache[64];                 // 0: not queried yet
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    int n = cache[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || v < 1 || v > 16) v = -1;
-        cache[dev].store(v, std::memory_order_relaxed);
-        n = v;
-    }
-    return n > 0 ? n : 0;                                // unknown: device-scope exchange
 }
 
 // S divides the super-groups; nt tiles per workgroup (<= the compute waves);
@@ -443,69 +509,6 @@ size_t partial_bytes(const GemmArgs& g, const SplitPlan& p) {
     return p.S > 1 ? ((size_t)p.S * g.N * ((g.M + 3) & ~3) * 4 + 255) & ~(size_t)255 : 0;
 }
 
-// The library's own workspaces, one per (device, stream): launches on one
-// stream are ordered, so they can share it.  hipStreamPerThread names a
-// different stream in every host thread, so it is keyed by the thread too.
-// Grown on demand: the old buffer is freed once the stream has finished with
-// it.  Never allocated while the stream is being captured into a graph (an
-// allocation cannot be captured): such a call fails with
-// hipErrorStreamCaptureUnsupported unless a large enough workspace exists.
-hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t pbytes, unsigned** counters, float** parts) {
-    struct Slot {
-        uint8_t* p = nullptr;
-        size_t cb = 0, pb = 0;
-    };
-    static std::mutex mu;
-    static std::map<std::tuple<int, uintptr_t, std::thread::id>, Slot> cache;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    const std::thread::id tid = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
-    std::lock_guard<std::mutex> lock(mu);
-    Slot& slot = cache[{dev, (uintptr_t)st, tid}];
-    if (!slot.p || slot.cb < cbytes || slot.pb < pbytes) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        e = hipStreamIsCapturing(st, &cs);
-        if (e != hipSuccess) return e;
-        if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
-        const size_t cb = std::max(cbytes, slot.cb), pb = std::max(pbytes, slot.pb);
-        uint8_t* p = nullptr;
-        e = hipMalloc((void**)&p, cb + pb);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(k_zero_u32, dim3(64), dim3(256), 0, st, (unsigned*)p, (int)(cb / 4));
-        e = hipGetLastError();
-        if (e != hipSuccess) {
-            (void)hipFree(p);
-            return e;
-        }
-        if (slot.p) {
-            // launches already queued on the stream may still use the old buffer
-            e = hipStreamSynchronize(st);
-            if (e != hipSuccess) return e;
-            e = hipFree(slot.p);
-            if (e != hipSuccess) return e;
-        }
-        slot = Slot{p, cb, pb};
-    }
-    *counters = (unsigned*)slot.p;
-    *parts = (float*)(slot.p + slot.cb);
-    return hipSuccess;
-}
-
-// Counters and partials for one launch: carved out of the caller's scratch
-// (bytes == 0: none given) or the library's workspace for the stream.
-hipError_t launch_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes, size_t pbytes,
-                            unsigned** counters, float** parts) {
-    if (!scratch) return library_workspace(st, cbytes, pbytes, counters, parts);
-    if (cbytes + pbytes > scratch->bytes) return hipErrorInvalidValue;
-    *counters = (unsigned*)scratch->base;
-    *parts = (float*)(scratch->base + cbytes);
-    // the counters must start at zero: cleared by a kernel on the stream
-    // (not a memset node, so a captured call replays correctly)
-    hipLaunchKernelGGL(k_zero_u32, dim3(16), dim3(256), 0, st, *counters, (int)(cbytes / 4));
-    return hipGetLastError();
-}
-
 template <int QT, int MT>
 hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
     auto k = k_gemm_split<QT, MT>;
@@ -522,7 +525,7 @@ hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* sc
     unsigned* counters = nullptr;
     float* parts = nullptr;
     if (p.S > 1) {
-        e = launch_workspace(scratch, st, counter_bytes(p), partial_bytes(g, p), &counters, &parts);
+        e = split_workspace(scratch, st, counter_bytes(p), partial_bytes(g, p), &counters, &parts);
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kSpNC + kSpNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K,
@@ -562,7 +565,7 @@ hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, 
     unsigned* counters = nullptr;
     float* parts = nullptr;
     if (ctot) {
-        e = launch_workspace(scratch, st, ctot, ptot, &counters, &parts);
+        e = split_workspace(scratch, st, ctot, ptot, &counters, &parts);
         if (e != hipSuccess) return e;
     }
     SplitJobs jobs = {};

@@ -40,6 +40,17 @@ hipError_t gemm_lds_batched(const GemmArgs* gs, int n, hipStream_t st);
 bool lds_batched_supports(const GemmArgs* gs, int n);
 hipError_t gemm_slab(const GemmArgs& g, hipStream_t st);
 bool slab_supports(const GemmArgs& g);
+// XCDs of the current device (the workgroup round robin the XCD-local
+// exchanges lay their grids out for), 0 if unknown.
+int device_xcds();
+// Counters and partials of a cross-workgroup exchange: carved out of `scratch`
+// (its counters cleared by a kernel on the stream first) or the library's
+// workspace for the stream (allocated on first use; never while the stream is
+// capturing: hipErrorStreamCaptureUnsupported).  hipErrorInvalidValue when
+// scratch is too small.
+hipError_t split_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes, size_t pbytes,
+                           unsigned** counters, float** parts);
+
 // The K-split kernel.  With S > 1 splits it needs a workspace (counters and
 // partials): from `scratch` when given (its counters are cleared by a kernel
 // on the stream first), else the library's per-stream workspace, allocated on
@@ -55,6 +66,14 @@ hipError_t gemm_split_batched(const GemmArgs* gs, int n, const Scratch* scratch,
 bool split_batched_supports(const GemmArgs* gs, int n);
 size_t split_batched_scratch_bytes(const GemmArgs* gs, int n);
 bool dot2_supports(const GemmArgs& g);
+// The dense kernel (33-128 batch rows per launch, the weights streamed once):
+// 64 weight rows x all batch rows per workgroup, K split with the exchange
+// above when that balances the grid.
+hipError_t gemm_dense(const GemmArgs& g, const Scratch* scratch, hipStream_t st);
+bool dense_supports(const GemmArgs& g);
+// Workspace bytes of the plan chosen under a workspace limit (0 when it does
+// not split K; SIZE_MAX when no plan fits the limit).
+size_t dense_scratch_bytes(const GemmArgs& g, size_t limit);
 
 hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
                        int N, int K, hipStream_t st);

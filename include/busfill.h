@@ -74,8 +74,11 @@ typedef enum {
                             fits in LDS; weight steps and A segments cycle through
                             rings when they do not fit)                               */
     BF_ALGO_SLAB = 5,    /* weights and activation slabs through an LDS ring (M <= 32) */
-    BF_ALGO_SPLIT = 6    /* K split over workgroups, all operands resident in LDS (M <= 32);
+    BF_ALGO_SPLIT = 6,   /* K split over workgroups, all operands resident in LDS (M <= 32);
                             uses a per-stream workspace allocated on first use          */
+    BF_ALGO_DENSE = 7    /* all batch rows per workgroup, the weights streamed once
+                            (M <= 128 per launch; the default above 32 rows); K split
+                            with the same workspace when that balances the grid        */
 } bf_algo;
 
 /* Reference-compatible entry: Q4_0 planes, fp32 output, C[Bsz][N] overwritten.

@@ -117,10 +117,11 @@ KERNELS = {
     O.Q4_K: [(bf.ALGO_SPLIT, 32, "f16"), (bf.ALGO_SPLIT, 9, "f16"), (bf.ALGO_SLAB, 32, "f16"),
              (bf.ALGO_MFMA, 32, "f16"), (bf.ALGO_MFMA, 64, "f16"), (bf.ALGO_LDS, 4, "f32"), (bf.ALGO_LDS, 8, "f32"),
              (bf.ALGO_LDS, 1, "f32"), (bf.ALGO_DOT2, 2, "f32"), (bf.ALGO_SIMPLE, 32, "f32"),
+             (bf.ALGO_DENSE, 64, "f16"), (bf.ALGO_DENSE, 128, "f16"), (bf.ALGO_AUTO, 96, "f16"),
              (bf.ALGO_AUTO, 32, "f16"), (bf.ALGO_AUTO, 1, "f32")],
     O.Q4_0: [(bf.ALGO_SPLIT, 32, "f16"), (bf.ALGO_SLAB, 32, "f16"), (bf.ALGO_MFMA, 32, "f16"),
              (bf.ALGO_LDS, 4, "f16"), (bf.ALGO_LDS, 8, "f16"), (bf.ALGO_LDS, 1, "f32"), (bf.ALGO_SIMPLE, 32, "f32"),
-             (bf.ALGO_AUTO, 32, "f16"), (bf.ALGO_AUTO, 1, "f32")],
+             (bf.ALGO_DENSE, 128, "f16"), (bf.ALGO_AUTO, 32, "f16"), (bf.ALGO_AUTO, 1, "f32")],
 }
 KERNELS[O.Q4_0_PLANES] = [k for k in KERNELS[O.Q4_0] if k[0] != bf.ALGO_SLAB]     # the slab kernel reads blocks only
 
