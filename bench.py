@@ -437,11 +437,16 @@ def run_q8(L, args, dev):
     return res
 
 
+SWEEP_SHAPES = "17408x5120,5120x17408"
+SWEEP_BATCHES = "1,2,3,4,6,8,16,32,64,128"
+
+
 def run_sweep(L, args, dev):
     res = []
-    for (N, K) in ((17408, 5120), (5120, 17408)):
+    shapes = [tuple(int(v) for v in s.split("x")) for s in (args.shapes or SWEEP_SHAPES).split(",")]
+    for (N, K) in shapes:
         rot = Rotation("q4_k", N, K, ROTATION_BYTES, seed=N, dev=dev)
-        for M in (1, 2, 3, 4, 6, 8, 16, 32, 64, 128):
+        for M in [int(x) for x in (args.batches or SWEEP_BATCHES).split(",")]:
             ms = time_gemm(L, rot, M, args.steps, args.warmup, int(args.graph == "1"), args.algo_id, dev)
             r = gemm_record(rot, M, ms, args.steps, args.graph == "1")
             r.update({"N": N, "K": K})
@@ -460,7 +465,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3, help="untimed passes before the timed ones")
     ap.add_argument("--workload", default="q4_k",
                     choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy", "swiglu", "q8"])
-    ap.add_argument("--batches", default="1,8,32")
+    ap.add_argument("--batches", default=None,
+                    help="batch rows M to time (default 1,8,32; sweep: " + SWEEP_BATCHES + ")")
+    ap.add_argument("--shapes", default=None,
+                    help="sweep workload: NxK weight shapes (default " + SWEEP_SHAPES + ")")
     ap.add_argument("--graph", default="both", choices=["0", "1", "both"],
                     help="issue launches on the stream (0), replay a HIP graph (1), or time both")
     ap.add_argument("--layer-m", type=int, default=32, help="layer workload: batch rows (config: 32)")
@@ -484,7 +492,7 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     L = bench_lib()
-    batches = [int(x) for x in args.batches.split(",")]
+    batches = [int(x) for x in (args.batches if args.workload != "sweep" and args.batches else "1,8,32").split(",")]
 
     if args.workload in ("q4_k", "q4_0", "planes"):
         fmt = args.workload
@@ -566,7 +574,8 @@ def main():
                   "value": max(r["weight_GBps"] for r in recs), "unit": "GB/s", "n_gpus": 1,
                   "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
                   "vs_baseline": None, "dtype": "f16", "data": "synthetic",
-                  "config": {"workload": "q4_k M in 1..128 on 17408x5120 and 5120x17408", "algo": args.algo},
+                  "config": {"workload": f"q4_k M in {args.batches or SWEEP_BATCHES} on "
+                                         f"{args.shapes or SWEEP_SHAPES}", "algo": args.algo},
                   "sweep": recs}
     line = json.dumps(record)
     if args.out:
