@@ -207,12 +207,14 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
     return BF_OK;
 }
 
-// Scratch of bf_gemm_noalloc: the K-split kernel's row-group counters and
-// partial sums, in place of the workspace bf_gemm allocates per stream.  Each
+// Scratch of bf_gemm_noalloc: the K-split and dense kernels' row-group
+// counters and partial sums, in place of the workspace bf_gemm allocates per
+// stream (34 MiB: the dense kernel's 256 workgroups x two 128 x 128 fp32
+// pieces plus counters for up to 8192 row groups).  Each
 // GPU the library runs on holds its own copy until the process ends.  In host
 // code `scratch` only names the symbol: its device address comes from
 // hipGetSymbolAddress (noalloc_scratch), once per device.
-constexpr size_t kNoallocScratch = 32u << 20;
+constexpr size_t kNoallocScratch = 34u << 20;
 static __device__ __align__(256) uint8_t scratch[kNoallocScratch];
 
 constexpr int kMaxDevices = 64;

@@ -13,18 +13,19 @@
  *
  * Conventions
  *   - All pointers are DEVICE pointers owned by the caller.  The one device
- *     memory the library allocates itself is the K-split kernel's workspace
- *     (BF_ALGO_SPLIT, which bf_gemm picks for 9-32 batch rows per launch when
- *     the activations do not fit in LDS): split partials and row-group
- *     counters, one workspace per (device, stream) -- per host thread for
- *     hipStreamPerThread -- allocated by the first such call on the stream,
- *     grown (the old buffer freed once the stream has passed it) and kept
- *     until the process ends.  It is never allocated while the stream is being
- *     captured into a graph: such a call returns BF_ERR_UNSUPPORTED; make one
- *     uncaptured call of the shape on the stream first, or use
- *     bf_gemm_noalloc.  A captured graph holds the workspace of the stream it
- *     was captured on: replaying it while other K-split work runs on that
- *     stream (or another replay of it) races.
+ *     memory the library allocates itself is the workspace of its
+ *     cross-workgroup exchanges: the K-split kernel's (BF_ALGO_SPLIT, which
+ *     bf_gemm picks for 9-32 batch rows per launch when the activations do not
+ *     fit in LDS) and the dense kernel's (BF_ALGO_DENSE, above 32 rows):
+ *     partial sums and row-group counters, one workspace per (device, stream)
+ *     -- per host thread for hipStreamPerThread -- allocated by the first such
+ *     call on the stream, grown (the old buffer freed once the stream has
+ *     passed it) and kept until the process ends.  It is never allocated while
+ *     the stream is being captured into a graph: such a call returns
+ *     BF_ERR_UNSUPPORTED; make one uncaptured call of the shape on the stream
+ *     first, or use bf_gemm_noalloc.  A captured graph holds the workspace of
+ *     the stream it was captured on: replaying it while other exchanging work
+ *     runs on that stream (or another replay of it) races.
  *   - fp16 values travel as uint16_t bit patterns.
  *   - A is [M][lda] row-major fp16, C is [M][ldc] row-major (fp32 or fp16),
  *     W is [N][K] in the chosen block format: C = A . dequant(W)^T.
@@ -34,7 +35,7 @@
  *     enqueued; a rejected call returns BF_ERR_INVALID and touches nothing.
  *   - Global state: the thread-local text of the last error (bf_last_error),
  *     per-device records that a kernel's LDS limit has been raised and of the
- *     device's XCD count, the K-split workspaces above, and the per-GPU
+ *     device's XCD and CU counts, the workspaces above, and the per-GPU
  *     address of bf_gemm_noalloc's scratch array.
  */
 #ifndef BUSFILL_H
@@ -77,8 +78,9 @@ typedef enum {
     BF_ALGO_SPLIT = 6,   /* K split over workgroups, all operands resident in LDS (M <= 32);
                             uses a per-stream workspace allocated on first use          */
     BF_ALGO_DENSE = 7    /* all batch rows per workgroup, the weights streamed once
-                            (M <= 128 per launch; the default above 32 rows); K split
-                            with the same workspace when that balances the grid        */
+                            (M <= 128 per launch; the default above 32 rows); one
+                            workgroup per CU over equal shares of the row groups' K,
+                            partial row groups summed through the same workspace      */
 } bf_algo;
 
 /* Reference-compatible entry: Q4_0 planes, fp32 output, C[Bsz][N] overwritten.
@@ -110,18 +112,20 @@ bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux,
  * memory (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference, whose kernel needs no scratch.
  * Same arguments, kernels and results as bf_gemm, bit for bit; where bf_gemm's
- * K-split kernel (9-32 batch rows per launch when the activations do not fit
- * in LDS) uses the workspace it allocates per stream, this call uses a 32 MiB
- * scratch array in device memory that each GPU holds for the life of the
- * process.  It calls no hipMalloc or hipFree; its first call on a device looks
- * up that device's array (hipGetSymbolAddress).  Every call on one GPU shares
- * the array: calls that overlap on one GPU (concurrent streams, or a captured
+ * cross-workgroup exchanges (the K-split kernel at 9-32 batch rows per launch
+ * when the activations do not fit in LDS, the dense kernel above 32 rows) use
+ * the workspace it allocates per stream, this call uses a 34 MiB scratch
+ * array in device memory that each GPU holds for the life of the process.  It
+ * calls no hipMalloc or hipFree; its first call on a device looks up that
+ * device's array (hipGetSymbolAddress).  Every call on one GPU shares the
+ * array: calls that overlap on one GPU (concurrent streams, or a captured
  * graph replayed while another such call runs) race and may return wrong
- * results.  Each K-split launch first clears the array's counters with a small
+ * results.  Each such launch first clears the array's counters with a small
  * kernel on the stream (no memset node in a captured graph).  Returns
- * BF_ERR_INVALID, enqueueing nothing, for a shape whose K-split launches need
- * more than 32 MiB of scratch (partials of S K-splits x N x M rows in fp32;
- * 11 MB at the 27B-class layer's largest shapes at M = 32). */
+ * BF_ERR_INVALID, enqueueing nothing, for a shape whose launches need more
+ * than 34 MiB of scratch (K-split partials of S splits x N x M rows in fp32,
+ * 11 MB at the 27B-class layer's largest shapes at M = 32; dense partials of
+ * 256 workgroups x 2 x 128 x M rows, 32 MiB at M = 128). */
 bf_status bf_gemm_noalloc(bf_qtype qtype, const void* W, const void* W_aux,
                           const uint16_t* A, int lda, void* C, int ldc, bf_otype otype,
                           int M, int N, int K, void* stream);
