@@ -178,8 +178,9 @@ bf_status bf_swiglu_f16(const uint16_t* gate_up, int ld, uint16_t* out, int ldo,
                         int M, int K, void* stream);
 
 /* ---------------------------------------------------------------- integer-dot path
- * Activations quantized to int8 per 32 values, multiplied in with a 4-way
- * integer dot per four weights.  No counterpart in the reference's kernels;
+ * Activations quantized to int8 per 32 values, multiplied in with integer
+ * dots over the 4-bit codes (int8 MFMA per 32-weight block from 3 batch rows,
+ * a 4-way dot per four weights below).  No counterpart in the reference's kernels;
  * its results (RESULTS.md:72-77, 93-96) credit llama.cpp's quantized GEMM
  * (quantize_q8_1 + dp4a vec-dots) with this activation form.  Not bit-equal
  * to bf_gemm: each activation moves by at most half its block's step d/2

@@ -726,6 +726,30 @@ def test_gemm_q8_parity(dev, qt, M, N, K):
     assert (np.abs(Cg - O.gemm_f64(w, A)) <= bound * (1 + 1e-4) + tol).all()
 
 
+@pytest.mark.parametrize("qt", QTS)
+@pytest.mark.parametrize("N", [5120, 9001, 12300, 17408])
+def test_gemm_q8_mfma_row_tiles(dev, qt, N):
+    """The MFMA form of the integer-dot GEMM (batch 3-16), one workgroup per CU
+    over ceil(N / CUs) rows as 2-5 tiles of 16, the last overlapping the one
+    before it (ragged N: the last workgroup holds one row), against the
+    oracle's integer restatement at M = 3, 8 and 16."""
+    K = 1024
+    w = O.gen_weights(qt, N, K, 300 + N)
+    Wd, auxd = upload(w, dev)
+    for M in (3, 8, 16):
+        A = O.gen_act(M, K, 400 + M)
+        Aq = gpu_quantize_q8(A, dev)
+        C = torch.full((M, N), float("nan"), device=dev)
+        bf.gemm_q8(qt, Wd, auxd, Aq, C, M, N, K)
+        torch.cuda.synchronize()
+        Cg = C.cpu().numpy().astype(np.float64)
+        q, d, s = O.quantize_q8(A)
+        ref, mag = O.gemm_q8(w, q, d, s)
+        assert np.isfinite(Cg).all(), (QT_NAME[qt], N, M)
+        tol = (K / 32 + 32) * 2.0 ** -24 * mag + 1e-30
+        assert (np.abs(Cg - ref) <= tol).all(), (QT_NAME[qt], N, M, float((np.abs(Cg - ref) / tol).max()))
+
+
 def test_gemm_q8_full_size_strided_f16_and_deterministic(dev):
     """Q4_K 5120 x 5120 at batch 16 into an fp16 output with ldc > N: rows
     beyond M and columns beyond N untouched, values within the oracle's bound
