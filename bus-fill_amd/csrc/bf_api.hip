@@ -61,6 +61,21 @@ bf_status check_weights(bf_qtype qt, const void* W, const void* W_aux, int N, in
     return BF_OK;
 }
 
+// Batches of 9-32 rows on large matrices (3 * 2^24 weights or more, 28 MB of
+// Q4_K), measured per kernel: the dense kernel (one workgroup per CU over
+// equal shares of the units, sums in a second launch) beats the K-split
+// kernel at every batch when K >= N (4096x13824, 8192x8192, 6144x16384,
+// 5120x17408: 19.9-28.8 us against 21-42 us at M = 9-32) and from 17 rows
+// when N > K; below that the K-split kernel is faster there (17408x5120 at
+// M = 9-16: 25 against 28-31 us; 13824x4096: 19 against 21 us) and the LDS
+// kernel's all-of-A form is not (31 us at M = 9).  Smaller matrices keep the
+// automatic order (7168x5120 at M = 16: K-split 11.7 against dense 18.5 us).
+bf_algo mid_batch_choice(const bf::GemmArgs& g) {
+    if (g.M < 9 || g.M > kSplitMaxM || (int64_t)g.N * g.K < 3 * (int64_t(1) << 24)) return BF_ALGO_AUTO;
+    if (g.N > g.K && g.M <= 16) return bf::split_supports(g) ? BF_ALGO_SPLIT : BF_ALGO_AUTO;
+    return bf::dense_supports(g) ? BF_ALGO_DENSE : BF_ALGO_AUTO;
+}
+
 bool fast_eligible(const bf::GemmArgs& g) {
     if (g.K % 256 != 0) return false;
     if (!aligned(g.A, 16) || g.lda % 8 != 0) return false;
@@ -135,6 +150,8 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
     auto choose = [&](const bf::GemmArgs& g, bool fast) {
         if (algo != BF_ALGO_AUTO) return algo;
         if (!fast) return BF_ALGO_SIMPLE;
+        const bf_algo mid = mid_batch_choice(g);
+        if (mid != BF_ALGO_AUTO) return mid;
         if (bf::lds_supports(g)) return BF_ALGO_LDS;
         if (bf::split_supports(g)) return BF_ALGO_SPLIT;
         if (dense_slices && bf::dense_supports(g)) return BF_ALGO_DENSE;

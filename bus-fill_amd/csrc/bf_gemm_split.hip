@@ -134,6 +134,7 @@ hipError_t split_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes
     *parts = (float*)(scratch->base + cbytes);
     // the counters must start at zero: cleared by a kernel on the stream
     // (not a memset node, so a captured call replays correctly)
+    if (cbytes == 0) return hipSuccess;
     hipLaunchKernelGGL(k_zero_u32, dim3(16), dim3(256), 0, st, *counters, (int)(cbytes / 4));
     return hipGetLastError();
 }

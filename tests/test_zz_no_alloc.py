@@ -1,6 +1,7 @@
 """bf_gemm_noalloc: the same results as bf_gemm, bit for bit, with the K-split
-kernel's counters and partials in the library's static per-GPU scratch array
-instead of a workspace allocated per stream.  Two calls in a row, the second
+kernel's counters and partials and the dense kernel's partials in the
+library's static per-GPU scratch array instead of a workspace allocated per
+stream.  Two calls in a row, the second
 on a smaller input (the array keeps the first call's contents); calls
 alternating with bf_gemm on one stream; batches above 32 rows (several K-split
 launches in one call); and a shape that needs more scratch than the array
@@ -61,10 +62,10 @@ def test_noalloc_alternating_shapes_formats_and_batches(dev):
 
 
 def test_noalloc_refuses_more_scratch_than_it_holds(dev):
-    # K = 65536 at 32 batch rows runs only as 64 K-splits (fewer splits leave
-    # more activations per workgroup than the LDS holds): 64 x 8192 x 32 fp32
-    # partials are 64 MiB
-    N, K, M = 8192, 65536, 32
+    # 16 batch rows with N > K run on the K-split kernel; its plan for
+    # 49152 x 16384 has 16 splits (fewer leave more units per workgroup than
+    # the LDS holds): 16 x 49152 x 16 fp32 partials are 48 MiB
+    N, K, M = 49152, 16384, 16
     W = torch.zeros(N * K * 9 // 16, dtype=torch.uint8, device=dev)
     A = torch.zeros((M, K), dtype=torch.float16, device=dev)
     C = torch.full((M, N), 7.0, device=dev)
