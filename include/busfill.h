@@ -16,8 +16,9 @@
  *     memory the library allocates itself is the workspace of its
  *     cross-workgroup exchanges: the K-split kernel's (BF_ALGO_SPLIT, which
  *     bf_gemm picks for 9-32 batch rows per launch when the activations do not
- *     fit in LDS) and the dense kernel's (BF_ALGO_DENSE, above 32 rows):
- *     partial sums and row-group counters, one workspace per (device, stream)
+ *     fit in LDS) partial sums and row-group counters, and the dense kernel's
+ *     (BF_ALGO_DENSE, above 32 rows, and from 9 or 17 rows on matrices of
+ *     3 * 2^24 weights or more) partial sums, one workspace per (device, stream)
  *     -- per host thread for hipStreamPerThread -- allocated by the first such
  *     call on the stream, grown (the old buffer freed once the stream has
  *     passed it) and kept until the process ends.  It is never allocated while
@@ -78,9 +79,10 @@ typedef enum {
     BF_ALGO_SPLIT = 6,   /* K split over workgroups, all operands resident in LDS (M <= 32);
                             uses a per-stream workspace allocated on first use          */
     BF_ALGO_DENSE = 7    /* all batch rows per workgroup, the weights streamed once
-                            (M <= 128 per launch; the default above 32 rows); one
-                            workgroup per CU over equal shares of the row groups' K,
-                            partial row groups summed through the same workspace      */
+                            (M <= 128 per launch; the default above 32 rows and on
+                            large matrices from 9 rows); one workgroup per CU over
+                            equal shares of the row groups' K, split row groups
+                            summed by a second launch through the same workspace      */
 } bf_algo;
 
 /* Reference-compatible entry: Q4_0 planes, fp32 output, C[Bsz][N] overwritten.
@@ -113,15 +115,16 @@ bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux,
  * hipMalloc).  No counterpart in the reference, whose kernel needs no scratch.
  * Same arguments, kernels and results as bf_gemm, bit for bit; where bf_gemm's
  * cross-workgroup exchanges (the K-split kernel at 9-32 batch rows per launch
- * when the activations do not fit in LDS, the dense kernel above 32 rows) use
+ * when the activations do not fit in LDS, the dense kernel above 32 rows and
+ * on large matrices) use
  * the workspace it allocates per stream, this call uses a 34 MiB scratch
  * array in device memory that each GPU holds for the life of the process.  It
  * calls no hipMalloc or hipFree; its first call on a device looks up that
  * device's array (hipGetSymbolAddress).  Every call on one GPU shares the
  * array: calls that overlap on one GPU (concurrent streams, or a captured
  * graph replayed while another such call runs) race and may return wrong
- * results.  Each such launch first clears the array's counters with a small
- * kernel on the stream (no memset node in a captured graph).  Returns
+ * results.  Each K-split launch first clears the array's counters with a
+ * small kernel on the stream (no memset node in a captured graph).  Returns
  * BF_ERR_INVALID, enqueueing nothing, for a shape whose launches need more
  * than 34 MiB of scratch (K-split partials of S splits x N x M rows in fp32,
  * 11 MB at the 27B-class layer's largest shapes at M = 32; dense partials of
