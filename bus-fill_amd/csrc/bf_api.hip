@@ -309,9 +309,13 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
         g.M = d.M;
         g.N = d.N;
         g.K = d.K;
-        const bool fast = fast_eligible(g), lds = fast && bf::lds_supports(g);
+        // one launch only where bf_gemm would take the same kernel for every GEMM
+        // (its results are then the same bits)
+        const bool fast = fast_eligible(g), mid = fast && mid_batch_choice(g) != BF_ALGO_AUTO;
+        const bool lds = fast && !mid && bf::lds_supports(g);
         all_lds = all_lds && lds;
-        all_split = all_split && fast && !lds && d.M <= kSplitMaxM && bf::split_supports(g);
+        all_split = all_split && fast && !lds && d.M <= kSplitMaxM && bf::split_supports(g) &&
+                    (!mid || mid_batch_choice(g) == BF_ALGO_SPLIT);
     }
     if (all_lds && bf::lds_batched_supports(gs.data(), count))
         return from_hip(bf::gemm_lds_batched(gs.data(), count, (hipStream_t)stream), "batched launch");

@@ -358,21 +358,6 @@ struct DensePlan {
     bool split;                                        // some row group is split between workgroups
 };
 
-// CUs of the current device (one workgroup each), 0 if unknown.
-int device_cus() {
-    static std::atomic<int> cache[64];                 // 0: not queried yet
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    int n = cache[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = -1;
-        cache[dev].store(v, std::memory_order_relaxed);
-        n = v;
-    }
-    return n > 0 ? n : 0;
-}
-
 size_t dense_partial_bytes(const GemmArgs& g, const DensePlan& p) {
     return ((size_t)2 * p.G * kDnRows * ((g.M + 3) & ~3) * 4 + 255) & ~(size_t)255;
 }

@@ -75,6 +75,21 @@ int device_xcds() {
     return n > 0 ? n : 0;                                // unknown: device-scope exchange
 }
 
+// CUs of the current device (the dense kernel runs one workgroup on each), 0 if unknown.
+int device_cus() {
+    static std::atomic<int> cache[64];                 // 0: not queried yet
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = -1;
+        cache[dev].store(v, std::memory_order_relaxed);
+        n = v;
+    }
+    return n > 0 ? n : 0;
+}
+
 // The library's own workspaces, one per (device, stream): launches on one
 // stream are ordered, so they can share it.  hipStreamPerThread names a
 // different stream in every host thread, so it is keyed by the thread too.
@@ -169,8 +184,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t workspace_rsrc(float* ws, int 
     return __builtin_amdgcn_make_buffer_rsrc(ws, (short)0, (int)((int64_t)S * N * Mp * 4), 0x00020000);
 }
 
-// One GEMM's share of a launch: workgroup `bid` of its grid.
-template <int QT, int MT>
+// One GEMM's share of a launch: workgroup `bid` of its grid.  SUM2: the
+// splits' partials are left for k_split_sum (a second launch) instead of being
+// counted and summed by the row group's last split.
+template <int QT, int MT, bool SUM2>
 __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                            const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nt,
                                            int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux,
@@ -186,7 +203,7 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
         rg = x + nx * q;
         s = jx - q * S;
         if ((int64_t)rg * nt * 16 >= N) return;          // padding of the last XCD round
-        if (S > 1 && nx > 1 && xcc_id() != x) {
+        if (!SUM2 && S > 1 && nx > 1 && xcc_id() != x) {
             // not on the XCD the exchange assumes: poison this workgroup's rows
             for (int v = threadIdx.x; v < nt * 16 * M; v += blockDim.x) {
                 const int m = v / (nt * 16);
@@ -320,7 +337,7 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
                 const int m4 = mt * 16 + 4 * kg;
                 if (m4 < Mp && n < N) {
                     const int off = (int)((((int64_t)s * N + n) * Mp + m4) * 4);
-                    if (nx > 0) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr, off, 0, 0);
+                    if (SUM2 || nx > 0) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr, off, 0, 0);
                     else __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr, off, 0, kCoherent);
                 }
             }
@@ -336,10 +353,11 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
                     }
                 }
         }
+        if (SUM2) return;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (lane == 0) asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[1])), "v"(1) : "memory");
     }
-    if (S == 1) return;
+    if (SUM2 || S == 1) return;
 
     // --------------------------------------------------------- cross-split sum
     if (c == 0) {
@@ -413,14 +431,42 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
     }
 }
 
-template <int QT, int MT>
+template <int QT, int MT, bool SUM2>
 __global__ __launch_bounds__(64 * (kSpNC + kSpNL))
 void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
                   int nt, int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C,
                   int ldc, int out_f16, float* __restrict__ ws, unsigned* __restrict__ counters, int nx) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    split_body<QT, MT>((int)blockIdx.x, lds, W, A, lda, M, N, K, nt, S, nsgS, unit_bytes, Waux, C, ldc, out_f16, ws,
-                       counters, nx);
+    split_body<QT, MT, SUM2>((int)blockIdx.x, lds, W, A, lda, M, N, K, nt, S, nsgS, unit_bytes, Waux, C, ldc, out_f16,
+                             ws, counters, nx);
+}
+
+// C of a single K-split launch: the S partials [s][n][Mp] of each element
+// added in split order (the order the batched launch's last split uses, so
+// both give the same bits).  Block b: rows 32 b .. 32 b + 31 and all batch
+// rows (M <= 32: at most 256 quads, one per thread); coalesced partial loads,
+// an LDS transpose, C stored along its rows.
+__global__ __launch_bounds__(256) void k_split_sum(const float* __restrict__ ws, void* __restrict__ C, int ldc,
+                                                   int out_f16, int M, int N, int S) {
+    __shared__ float tr[32 * 33];
+    const int Mp = (M + 3) & ~3, nq = 32 * (Mp / 4);
+    const int n0 = 32 * (int)blockIdx.x, tid = (int)threadIdx.x;
+    if (tid < nq) {
+        const int nl = tid / (Mp / 4), m4 = 4 * (tid - nl * (Mp / 4));
+        f4 s = f4{0.f, 0.f, 0.f, 0.f};
+        if (n0 + nl < N)
+            for (int k = 0; k < S; k++) s += *(const f4*)(ws + ((size_t)k * N + n0 + nl) * Mp + m4);
+#pragma unroll
+        for (int i = 0; i < 4; i++) tr[(m4 + i) * 33 + nl] = s[i];
+    }
+    __syncthreads();
+    for (int y = tid; y < M * 32; y += 256) {
+        const int m = y >> 5, nl = y & 31;
+        if (n0 + nl >= N) continue;
+        const float x = tr[m * 33 + nl];
+        if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + n0 + nl] = (_Float16)x;
+        else ((float*)C)[(int64_t)m * ldc + n0 + nl] = x;
+    }
 }
 
 // Several independent GEMMs in one launch (their grids back to back): a
@@ -452,7 +498,7 @@ void k_gemm_split_batched(const SplitJobs jobs) {
 #pragma unroll
     for (int i = 1; i < kSpMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
-    split_body<QT, MT>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nt, j.S, j.nsgS,
+    split_body<QT, MT, false>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nt, j.S, j.nsgS,
                        j.unit_bytes, j.Waux, j.C, j.ldc, jobs.out_f16, j.ws, j.counters, jobs.nx);
 }
 
@@ -510,9 +556,19 @@ size_t partial_bytes(const GemmArgs& g, const SplitPlan& p) {
     return p.S > 1 ? ((size_t)p.S * g.N * ((g.M + 3) & ~3) * 4 + 255) & ~(size_t)255 : 0;
 }
 
-template <int QT, int MT>
-hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
-    auto k = k_gemm_split<QT, MT>;
+// A single launch's splits are summed by k_split_sum (a second launch) when its
+// grid takes more than one workgroup per CU: the row groups' last splits then
+// run in the last round and sum after everyone else (17408x5120 at M = 9-16:
+// 24-25 -> 22.5 us).  In one round the in-kernel sum is cheaper than the second
+// launch (5120^2 at M = 16-32: 10.3-11.6 against 11.3-12.0 us).
+bool split_sum2(const SplitPlan& p) {
+    const int cus = device_cus();
+    return p.S > 1 && p.grid > (cus > 0 ? cus : 256);
+}
+
+template <int QT, int MT, bool SUM2>
+hipError_t launch_split_k(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
+    auto k = k_gemm_split<QT, MT, SUM2>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -526,12 +582,23 @@ hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* sc
     unsigned* counters = nullptr;
     float* parts = nullptr;
     if (p.S > 1) {
-        e = split_workspace(scratch, st, counter_bytes(p), partial_bytes(g, p), &counters, &parts);
+        // summed by k_split_sum: partials only, no counters
+        e = split_workspace(scratch, st, SUM2 ? 0 : counter_bytes(p), partial_bytes(g, p), &counters, &parts);
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kSpNC + kSpNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K,
                        p.nt, p.S, p.nsgS, p.unit_bytes, g.Waux, g.C, g.ldc, g.out_f16, parts, counters, p.nx);
+    e = hipGetLastError();
+    if (e != hipSuccess || !SUM2) return e;
+    hipLaunchKernelGGL(k_split_sum, dim3((g.N + 31) / 32), dim3(256), 0, st, (const float*)parts, g.C, g.ldc,
+                       g.out_f16, g.M, g.N, p.S);
     return hipGetLastError();
+}
+
+template <int QT, int MT>
+hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
+    return split_sum2(p) ? launch_split_k<QT, MT, true>(g, p, scratch, st)
+                         : launch_split_k<QT, MT, false>(g, p, scratch, st);
 }
 
 template <int QT>
@@ -605,7 +672,7 @@ bool split_supports(const GemmArgs& g) {
 size_t split_scratch_bytes(const GemmArgs& g) {
     SplitPlan p;
     if (!plan_split(g, p, device_xcds())) return 0;
-    return counter_bytes(p) + partial_bytes(g, p);
+    return (split_sum2(p) ? 0 : counter_bytes(p)) + partial_bytes(g, p);
 }
 
 bool split_batched_supports(const GemmArgs* gs, int n) {

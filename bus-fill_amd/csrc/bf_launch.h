@@ -43,6 +43,8 @@ bool slab_supports(const GemmArgs& g);
 // XCDs of the current device (the workgroup round robin the XCD-local
 // exchanges lay their grids out for), 0 if unknown.
 int device_xcds();
+// CUs of the current device, 0 if unknown.
+int device_cus();
 // Counters and partials of a cross-workgroup exchange: carved out of `scratch`
 // (its counters cleared by a kernel on the stream first) or the library's
 // workspace for the stream (allocated on first use; never while the stream is

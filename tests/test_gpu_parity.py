@@ -476,6 +476,28 @@ def test_batched_matches_single_launches(dev, qt, Ms, otype):
                     assert_gate(got, O.gemm_f64(ws[i], As[i]), f"batched f16 {QT_NAME[qt]} {BATCH_SHAPES[i]}")
 
 
+def test_batched_matches_single_launches_large_matrices(dev):
+    """bf_gemm sums a K-split GEMM whose grid takes more than one workgroup per
+    CU in a second launch (k_split_sum) and sends 9-32 rows on matrices of
+    3 * 2^24 weights or more to the dense kernel; bf_gemm_batched's one launch
+    sums splits in-kernel.  Same split order, so the same bits; a batch holding
+    a GEMM that bf_gemm gives the dense kernel runs as one call per GEMM."""
+    for shapes in ([(17408, 5120, 16), (7168, 5120, 16)], [(7168, 5120, 32), (1792, 5120, 32)],
+                   [(5120, 17408, 32), (1792, 5120, 32)]):
+        ws = [O.gen_weights(O.Q4_K, N, K, seed=N + K + M) for N, K, M in shapes]
+        dws = [upload(w, dev) for w in ws]
+        As = [O.gen_act(M, K, seed=K + M + i) for i, (N, K, M) in enumerate(shapes)]
+        singles = [gpu_gemm(w, A, dev, dw=dw) for w, A, dw in zip(ws, As, dws)]
+        Cs = [torch.full((M, N), float("nan"), device=dev) for N, K, M in shapes]
+        bf.gemm_batched(O.Q4_K, [(dw[0], dw[1], to_dev(A, dev), C, M, N, K)
+                                 for dw, A, C, (N, K, M) in zip(dws, As, Cs, shapes)])
+        torch.cuda.synchronize()
+        for i, (C, ref) in enumerate(zip(Cs, singles)):
+            got = C.cpu().numpy().astype(np.float64)
+            assert (got == ref).all(), shapes[i]
+            Ref(ws[i], As[i]).check(got, f"batched q4_k {shapes[i]}")
+
+
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
 def test_full_size_exact_properties(dev, qt):
     """Size-independent checks at the benchmark shape: scaling A by 2 is exact
