@@ -369,7 +369,7 @@ size_t dense_partial_bytes(const GemmArgs& g, const DensePlan& p) {
 bool plan_dense(const GemmArgs& g, DensePlan& p, int cus) {
     if (g.M < 1 || g.M > 128 || g.K % 256 || g.N < 1) return false;
     if ((int64_t)g.M * g.ldc * (g.out_f16 ? 2 : 4) >= (1LL << 31)) return false;   // C by 32-bit offsets
-    const int MT = std::max(2, (g.M + 31) / 32);       // 32-row m-tiles
+    const int MT = (g.M + 31) / 32;                    // 32-row m-tiles
     if ((g.M * 17 + 63) / 64 > kDnNLA * kDnAQS || (kDnRows * 9 + 63) / 64 > kDnNLW * kDnWQS) return false;
     const int DW = 2, a_slot = g.M * kDnARow;
     const int DA = std::min(6, (kMaxLds - kDnFlags - DW * kDnWSlot) / a_slot);
@@ -414,6 +414,7 @@ hipError_t launch_dense(const GemmArgs& g, const DensePlan& p, const Scratch* sc
 
 template <int QT>
 hipError_t dispatch_dense(const GemmArgs& g, const DensePlan& p, const Scratch* scratch, hipStream_t st) {
+    if (p.MT == 1) return launch_dense<QT, 1>(g, p, scratch, st);
     if (p.MT == 2) return launch_dense<QT, 2>(g, p, scratch, st);
     if (p.MT == 3) return launch_dense<QT, 3>(g, p, scratch, st);
     return launch_dense<QT, 4>(g, p, scratch, st);

@@ -324,15 +324,15 @@ def test_split_batch_parity(dev, qt, N, K):
 @pytest.mark.parametrize("N,K", [(1, 256), (77, 2048), (200, 5120), (5120, 5120), (600, 17408), (7168, 5120)])
 def test_dense_batch_parity(dev, qt, N, K):
     """The dense kernel (all batch rows of a launch per workgroup, the weights
-    streamed once): ragged N (clamped weight rows), batches of 33-128 rows
-    (m-tiles split over two rows of waves, padded rows), K split with the
-    workspace exchange where the plan takes it (K = 17408), fp16 weights,
-    identical results on repeated runs."""
+    streamed once): ragged N (clamped weight rows), batches of 1-128 rows (one
+    to four 32-row m-tiles, padded rows), row groups split between workgroups
+    and summed by the second launch, fp16 weights, identical results on
+    repeated runs."""
     w = O.gen_weights(qt, N, K, seed=K * 13 + N + qt)
     dw = upload(w, dev)
     A = O.gen_act(128, K, seed=K + 19)
     ref = Ref(w, A)
-    for M in (33, 48, 64, 65, 96, 100, 128):
+    for M in (1, 9, 17, 32, 33, 48, 64, 65, 96, 100, 128):
         C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DENSE, dw=dw)
         ref.check(C, f"dense {QT_NAME[qt]} N={N} K={K} M={M}", rows=M, form="f16")
         assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DENSE, dw=dw) == C).all()
