@@ -203,7 +203,9 @@ bf_status bf_quantize_q8(const uint16_t* A, int lda, void* Aq, int M, int K, voi
 /* C[M][N] = sum over 32-blocks b of d_b * (scale * dot_b - offset * s_b), the
  * integer dots exact, over the weights in place (any of the three formats).
  * M = 1..16, K % 64 == 0, W and Aq 16-byte aligned; other shapes return
- * BF_ERR_UNSUPPORTED. */
+ * BF_ERR_UNSUPPORTED.  Aq must be bf_quantize_q8's output for the same M and
+ * K: its d and s regions start at offsets that depend on M (bf_q8_bytes), so
+ * to multiply the first rows of a larger batch, quantize those rows alone. */
 bf_status bf_gemm_q8(bf_qtype qtype, const void* W, const void* W_aux, const void* Aq, void* C, int ldc,
                      bf_otype otype, int M, int N, int K, void* stream);
 
