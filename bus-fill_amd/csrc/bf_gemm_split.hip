@@ -30,17 +30,22 @@
 //   ready for the next launch that uses it.  A writer's stores are complete
 //   (s_waitcnt vmcnt(0)) before its workgroup counts itself, and the last
 //   split reads only after its own count.
-// * XCD-local exchange (nx > 0): the dispatcher hands workgroup b to XCD
-//   b % nx, so the grid is laid out to put all S splits of a row group on one
-//   XCD, where they share one L2.  Partials are then plain (L2 write-back)
-//   stores that the last split's device-scope reads find in that L2 (those
-//   reads miss only the L1), instead of stores written through to memory.
-//   The counter stays a device-scope atomic.
-//   Each workgroup checks its XCC id against b % nx; a workgroup that finds
-//   itself elsewhere writes NaN over its rows of C, so a broken placement
-//   shows as a failed result rather than a silently wrong one.  With nx = 0
-//   the partials are written with device-scope (sc1) stores, which reach the
-//   point of coherence of all XCDs' L2s.
+// * XCD-local exchange (nx > 0): the dispatcher hands the workgroups of a
+//   launch to the nx XCDs round robin, starting from an XCD that depends on
+//   the hardware queue of the stream (measured: 0 on the null stream, 6 and 7
+//   on two created streams), so each round of nx consecutive workgroups
+//   covers every XCD once.  A workgroup takes its row group from the XCD it
+//   finds itself on (XCC id x) and its round (b / nx): XCD x holds row groups
+//   x, x + nx, ..., each as S consecutive rounds, so all S splits of a row
+//   group share one L2 whatever the starting XCD.  Partials are then plain
+//   (L2 write-back) stores that the last split's device-scope reads find in
+//   that L2 (those reads miss only the L1), instead of stores written through
+//   to memory.  The counter stays a device-scope atomic; each split adds
+//   1 + 2^(8 + s), so the last arrival sees exactly S + (2^S - 1) 2^8 unless
+//   a split came twice (a placement that was not round robin) or a split was
+//   poisoned (2^7): its row group's C is then NaN, never a silently wrong
+//   sum.  With nx = 0 the partials are written with device-scope (sc1)
+//   stores, which reach the point of coherence of all XCDs' L2s.
 #include <algorithm>
 #include <atomic>
 #include <map>
@@ -161,9 +166,11 @@ namespace {
 // 64 + 16 i + 4 j, park flag of compute wave c at 1024 + 4 c; then the units;
 // then the parked sums.
 constexpr int kSpPoison = 3;
-// A workgroup that counts itself with a poisoned result adds this to its row
-// group's counter too (on top of 1), so the split that finishes last writes NaN.
-constexpr unsigned kSpPoisonCount = 1u << 16;
+// Row-group counters (64-bit): arrivals in bits 0-6, split s adds bit 8 + s,
+// and a workgroup that counts itself with a poisoned result adds bit 7 too, so
+// the split that finishes last writes NaN.
+constexpr uint64_t kSpPoisonBit = 1ull << 7;
+constexpr int kSpMaxS = 56;                             // splits of a row group (one count bit each)
 constexpr int kSpFlags = 2048;
 constexpr int kSpMaxUnits = (1024 - 64) / 16;
 constexpr int kSpNC = 12, kSpNL = 4;    // compute and loader waves per workgroup
@@ -198,23 +205,14 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int rg, s;
     if (nx > 0) {
-        // XCD x = bid % nx holds row groups x, x + nx, ..., each as S consecutive workgroups
-        const int x = bid % nx, jx = bid / nx, q = jx / S;
+        // XCD x holds row groups x, x + nx, ..., each as S consecutive rounds;
+        // with the exchange x is the XCD this workgroup runs on (the same
+        // bijection for any starting XCD of the round robin)
+        const int x = !SUM2 && S > 1 && nx > 1 ? xcc_id() % nx : bid % nx;
+        const int jx = bid / nx, q = jx / S;
         rg = x + nx * q;
         s = jx - q * S;
         if ((int64_t)rg * nt * 16 >= N) return;          // padding of the last XCD round
-        if (!SUM2 && S > 1 && nx > 1 && xcc_id() != x) {
-            // not on the XCD the exchange assumes: poison this workgroup's rows
-            for (int v = threadIdx.x; v < nt * 16 * M; v += blockDim.x) {
-                const int m = v / (nt * 16);
-                const int64_t n = (int64_t)rg * nt * 16 + (v - m * nt * 16);
-                if (n < N) {
-                    if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + n] = (_Float16)__builtin_nanf("");
-                    else ((float*)C)[(int64_t)m * ldc + n] = __builtin_nanf("");
-                }
-            }
-            return;
-        }
     } else {
         rg = bid / S;
         s = bid - rg * S;
@@ -362,17 +360,18 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
     // --------------------------------------------------------- cross-split sum
     if (c == 0) {
         wait_flags(&flags[1], 1, lane, flags + kSpPoison, min(nt, NC));
-        // the count carries this workgroup's poison (a tile whose sums it did
-        // not see stored leaves a stale partial behind)
-        const unsigned add = poisoned(flags + kSpPoison) ? 1u + kSpPoisonCount : 1u;
-        unsigned old = 0;
-        unsigned* const cnt = counters + rg * kSpCounterStride;
+        // the count carries this split's bit and its poison (a tile whose sums
+        // it did not see stored leaves a stale partial behind)
+        const uint64_t add = 1ull + (1ull << (8 + s)) + (poisoned(flags + kSpPoison) ? kSpPoisonBit : 0ull);
+        uint64_t old = 0;
+        uint64_t* const cnt = (uint64_t*)(counters + rg * kSpCounterStride);
         if (lane == 0) old = __hip_atomic_fetch_add(cnt, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __builtin_amdgcn_readfirstlane(old);
-        const int last = (old & (kSpPoisonCount - 1)) == (unsigned)(S - 1);
-        if (last && lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // 1: last and clean, 3: last with a poisoned split, 2: not last
-        const int word = !last ? 2 : (old >= kSpPoisonCount || add > 1u) ? 3 : 1;
+        const uint64_t fin = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(old >> 32)) << 32 |
+                              (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)old)) + add;
+        const int last = (fin & 0x7Full) == (uint64_t)S;
+        if (last && lane == 0) __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // 1: last and clean, 3: last with a poisoned or repeated split, 2: not last
+        const int word = !last ? 2 : fin == ((uint64_t)S | (((1ull << S) - 1ull) << 8)) ? 1 : 3;
         if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[2])), "v"(word) : "memory");
     }
     wait_flags(&flags[2], 1, lane, flags + kSpPoison);
@@ -523,7 +522,7 @@ bool plan_split(const GemmArgs& g, SplitPlan& p, int nx) {
     const int nsg = g.K / 256, T = (g.N + 15) / 16;
     const int MT = g.M <= 16 ? 1 : 2;
     double best = 1e300;
-    for (int S = 1; S <= nsg; S++) {
+    for (int S = 1; S <= nsg && S <= kSpMaxS; S++) {
         if (nsg % S) continue;
         const int nsgS = nsg / S;
         if (nsgS > kSpMaxUnits) continue;
