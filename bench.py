@@ -58,14 +58,14 @@ def log(*a):
 class Rotation:
     """`count` distinct N x K matrices of one format in one device allocation."""
 
-    def __init__(self, fmt, N, K, min_bytes, seed, dev):
+    def __init__(self, fmt, N, K, min_bytes, seed, dev, scales=None, count=None):
         import torch
         self.fmt, self.N, self.K = fmt, N, K
         self.wbytes = N * K * 9 // 16
-        self.count = max(1, math.ceil(min_bytes / self.wbytes))
+        self.count = count or max(1, math.ceil(min_bytes / self.wbytes))
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
-        lo, hi = SCALE_RANGE[fmt]
+        lo, hi = scales or SCALE_RANGE[fmt]
         if fmt == "planes":
             self.W = torch.randint(0, 256, (self.count, N * K // 2), dtype=torch.uint8, device=dev, generator=g)
             d = torch.rand((self.count, N * K // 32), device=dev, generator=g) * (hi - lo) + lo
@@ -107,9 +107,10 @@ def bench_lib():
     L.bfb_time_swiglu.argtypes = [i, vp, vp, i, vp, i, vp, vp, i, i, i, i, i, i, vp, d]
     L.bfb_copy.argtypes = [vp, vp, ctypes.c_size_t, i, vp, d]
     L.bfb_time_q8.argtypes = [i, vp, vp, i, vp, vp, vp, i, i, i, i, i, i, vp, d]
+    L.bfb_time_ffn.argtypes = [i, vp, vp, vp, vp, vp, vp, i, vp, vp, vp, i, i, i, i, i, i, i, i, vp, d]
     L.bfb_last_error.restype = ctypes.c_char_p
     for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_time_sequence_batched", "bfb_read_peak", "bfb_read_slices",
-              "bfb_copy", "bfb_time_swiglu", "bfb_time_q8"):
+              "bfb_copy", "bfb_time_swiglu", "bfb_time_q8", "bfb_time_ffn"):
         getattr(L, f).restype = i
     return L
 
@@ -407,6 +408,56 @@ def run_swiglu(L, args, dev):
     return res
 
 
+FFN_FORMS = {"one_launch": 1, "two_launches": 2, "calls": 3}
+
+
+def run_ffn(L, args, dev):
+    """The 27B-class SwiGLU feed-forward block (gate and up 5120 -> 17408,
+    SiLU(g) * u, down 17408 -> 5120; 150.4 MB of Q4_K weights) through
+    bf_ffn_swiglu_ex in each form that serves the batch, over a >= 1 GB
+    rotation of distinct blocks.  Q4_K scales d, dmin ~ U[1e-4, 1e-3]: with
+    the single-GEMM workloads' U[1e-3, 1e-2] the weights' mean is near 1 and
+    SiLU(g) * u overflows fp16."""
+    import torch
+    K, F, N = 5120, 17408, 5120
+    sr = (1e-4, 1e-3)
+    block = 3 * F * K * 9 // 16
+    count = max(1, math.ceil(ROTATION_BYTES / block))
+    rots = [Rotation("q4_k", F, K, 0, seed=1, dev=dev, scales=sr, count=count),
+            Rotation("q4_k", F, K, 0, seed=2, dev=dev, scales=sr, count=count),
+            Rotation("q4_k", N, F, 0, seed=3, dev=dev, scales=sr, count=count)]
+    ptrs = [r.ptr_arrays()[0] for r in rots]
+    log(f"[bench] ffn: {count} distinct blocks x {block / 1e6:.1f} MB")
+    res = []
+    for M in [int(x) for x in (args.batches or "1,2,8,32").split(",")]:
+        A = torch.randn((M, K), device=dev).half()
+        gu = torch.empty((M, 2 * F), device=dev, dtype=torch.float16)
+        C = torch.empty((M, N), device=dev, dtype=torch.float32)
+        for form, fid in FFN_FORMS.items():
+            if fid != FFN_FORMS["calls"] and M > 2:
+                continue
+            for graph in ((0, 1) if args.graph == "both" else (int(args.graph),)):
+                ms = ctypes.c_double()
+                torch.cuda.synchronize()
+                rc = L.bfb_time_ffn(QT["q4_k"], P(ptrs[0]), None, P(ptrs[1]), None, P(ptrs[2]), None, count,
+                                    A.data_ptr(), gu.data_ptr(), C.data_ptr(), M, K, F, N, fid,
+                                    args.warmup * count, args.steps * count, graph, stream_handle(),
+                                    ctypes.byref(ms))
+                torch.cuda.synchronize()
+                if rc != 0:
+                    raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+                if not torch.isfinite(C).all():
+                    raise RuntimeError("non-finite feed-forward output during timing")
+                t = ms.value / 1e3 / (args.steps * count)
+                r = {"M": M, "form": form, "launch": "graph" if graph else "stream",
+                     "us_per_block": round(t * 1e6, 3), "weight_GBps": round(block / t / 1e9, 2),
+                     "tok_s": round(M / t, 1), "blocks_timed": args.steps * count}
+                log(f"[bench] ffn M={M} {form} {r['launch']}: {r['us_per_block']:.2f} us/block "
+                    f"{r['weight_GBps']:.1f} GB/s")
+                res.append(r)
+    return res, count, block
+
+
 def run_q8(L, args, dev):
     """The integer-dot activation path (int8 activations per 32 values,
     v_dot4_i32_i8) against the fp16 GEMM, Q4_K 5120x5120, M = 1-16: the q8
@@ -464,7 +515,7 @@ def main():
                     help="timed passes over the >= 1 GB weight rotation per configuration (one GEMM per matrix)")
     ap.add_argument("--warmup", type=int, default=3, help="untimed passes before the timed ones")
     ap.add_argument("--workload", default="q4_k",
-                    choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy", "swiglu", "q8"])
+                    choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy", "swiglu", "q8", "ffn"])
     ap.add_argument("--batches", default=None,
                     help="batch rows M to time (default 1,8,32; sweep: " + SWEEP_BATCHES + ")")
     ap.add_argument("--shapes", default=None,
@@ -558,6 +609,19 @@ def main():
                   "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
                   "data": "synthetic",
                   "config": {"workload": "q4_k down projection N=5120 K=17408 fed by gate|up [M][2K], M=1 and 2"},
+                  "runs": recs}
+    elif args.workload == "ffn":
+        recs, count, block = run_ffn(L, args, dev)
+        head = min((r for r in recs if r["M"] == recs[0]["M"]), key=lambda r: r["us_per_block"])
+        record = {"metric": "SwiGLU feed-forward block (Q4_K gate/up 5120->17408, down 17408->5120): "
+                            "weight-stream GB/s and us per block",
+                  "value": head["weight_GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+                  "warmup": args.warmup, "ms_per_step": round(head["us_per_block"] * count / 1e3, 6),
+                  "step": f"one pass over {count} distinct blocks ({block} weight bytes each)",
+                  "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+                  "data": "synthetic",
+                  "config": {"workload": "q4_k SwiGLU block K=5120 F=17408 N=5120", "M": head["M"],
+                             "form": head["form"], "launch": head["launch"]},
                   "runs": recs}
     elif args.workload == "q8":
         recs = run_q8(L, args, dev)

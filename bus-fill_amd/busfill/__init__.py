@@ -26,11 +26,13 @@ OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 Q4_0, Q4_0_PLANES, Q4_K = 0, 1, 2
 # bf_otype
 OUT_F32, OUT_F16 = 0, 1
+# bf_ffn_form
+FFN_AUTO, FFN_ONE_LAUNCH, FFN_TWO_LAUNCHES, FFN_CALLS = 0, 1, 2, 3
 # bf_algo
 ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT, ALGO_DENSE = 0, 1, 2, 3, 4, 5, 6, 7
 
 EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_noalloc", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
-           "bf_swiglu_f16", "bf_q8_bytes", "bf_quantize_q8", "bf_gemm_q8",
+           "bf_swiglu_f16", "bf_ffn_swiglu", "bf_ffn_swiglu_ex", "bf_q8_bytes", "bf_quantize_q8", "bf_gemm_q8",
            "bf_gguf_open", "bf_gguf_close", "bf_gguf_tensor_count", "bf_gguf_tensor_at", "bf_gguf_find",
            "bf_gguf_get_u64", "bf_gguf_get_str", "bf_gguf_upload",
            "bf_status_str", "bf_last_error", "bf_version")
@@ -41,6 +43,11 @@ class GemmDesc(ctypes.Structure):
     _fields_ = [("W", ctypes.c_void_p), ("W_aux", ctypes.c_void_p), ("A", ctypes.c_void_p),
                 ("lda", ctypes.c_int), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int),
                 ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int)]
+
+
+class QWeights(ctypes.Structure):
+    """bf_qweights: the weights of one linear (W, and the scale plane for planes)."""
+    _fields_ = [("W", ctypes.c_void_p), ("W_aux", ctypes.c_void_p)]
 
 
 class GgufTensor(ctypes.Structure):
@@ -80,6 +87,8 @@ def lib() -> ctypes.CDLL:
         L.bf_gemm_batched.argtypes = [i, i, i, ctypes.POINTER(GemmDesc), vp]
         L.bf_gemm_swiglu.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
         L.bf_swiglu_f16.argtypes = [vp, i, vp, i, i, i, vp]
+        L.bf_ffn_swiglu.argtypes = [i, QWeights, QWeights, QWeights, vp, i, vp, i, vp, i, i, i, i, i, i, vp]
+        L.bf_ffn_swiglu_ex.argtypes = [i, QWeights, QWeights, QWeights, vp, i, vp, i, vp, i, i, i, i, i, i, i, vp]
         L.bf_q8_bytes.argtypes = [i, i]
         L.bf_q8_bytes.restype = ctypes.c_size_t
         L.bf_quantize_q8.argtypes = [vp, i, vp, i, i, vp]
@@ -99,7 +108,7 @@ def lib() -> ctypes.CDLL:
                   "bf_gguf_upload"):
             getattr(L, f).restype = i
         for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_noalloc", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
-                  "bf_swiglu_f16", "bf_quantize_q8", "bf_gemm_q8"):
+                  "bf_swiglu_f16", "bf_ffn_swiglu", "bf_ffn_swiglu_ex", "bf_quantize_q8", "bf_gemm_q8"):
             getattr(L, f).restype = i
         L.bf_status_str.argtypes = [i]
         L.bf_status_str.restype = ctypes.c_char_p
@@ -159,6 +168,19 @@ def gemm_swiglu(qtype: int, W, W_aux, gate_up, C, M: int, N: int, K: int, *, ld:
     st = lib().bf_gemm_swiglu(qtype, _ptr(W), _ptr(W_aux), _ptr(gate_up), 2 * K if ld is None else ld, _ptr(C),
                               N if ldc is None else ldc, otype, M, N, K, _stream(stream))
     _check(st, "bf_gemm_swiglu")
+
+
+def ffn_swiglu(qtype: int, gate, up, down, A, gate_up, C, M: int, K: int, F: int, N: int, *,
+               lda: int | None = None, ldgu: int | None = None, ldc: int | None = None, otype: int = OUT_F32,
+               form: int = FFN_AUTO, stream=None) -> None:
+    """C[M][N] = (SiLU(A . Wg^T) * (A . Wu^T)) . Wd^T.  gate, up and down are
+    (W, W_aux) pairs (W_aux None except for the planes format); gate_up is the
+    caller's fp16 [M][ldgu >= 2F] intermediate; form one of FFN_*."""
+    qw = [QWeights(_ptr(w), _ptr(a)) for (w, a) in (gate, up, down)]
+    st = lib().bf_ffn_swiglu_ex(qtype, qw[0], qw[1], qw[2], _ptr(A), K if lda is None else lda, _ptr(gate_up),
+                                2 * F if ldgu is None else ldgu, _ptr(C), N if ldc is None else ldc, otype, M, K, F, N,
+                                form, _stream(stream))
+    _check(st, "bf_ffn_swiglu_ex")
 
 
 def swiglu_f16(gate_up, out, M: int, K: int, *, ld: int | None = None, ldo: int | None = None,

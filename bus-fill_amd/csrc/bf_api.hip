@@ -355,6 +355,65 @@ bf_status bf_gemm_swiglu(bf_qtype qtype, const void* W, const void* W_aux, const
     return from_hip(bf::gemm_lds_swiglu(g, (hipStream_t)stream), "kernel launch");
 }
 
+bf_status bf_ffn_swiglu_ex(bf_qtype qtype, bf_qweights gate, bf_qweights up, bf_qweights down, const uint16_t* A,
+                           int lda, uint16_t* gate_up, int ldgu, void* C, int ldc, bf_otype otype, int M, int K,
+                           int F, int N, bf_ffn_form form, void* stream) {
+    g_last_error[0] = '\0';
+    if (form < BF_FFN_AUTO || form > BF_FFN_CALLS) return fail(BF_ERR_INVALID, "unknown form %d", (int)form);
+    if (!gate_up) return fail(BF_ERR_INVALID, "gate_up is NULL");
+    if (F < 8 || F % 8) return fail(BF_ERR_INVALID, "F=%d must be a positive multiple of 8", F);
+    if (ldgu < 2 * (int64_t)F) return fail(BF_ERR_INVALID, "ldgu=%d < 2F=%lld", ldgu, 2 * (long long)F);
+    if (!aligned(gate_up, 16) || ldgu % 8) return fail(BF_ERR_INVALID, "gate_up rows must be 16-byte aligned (ldgu %% 8 == 0)");
+    bf_status st = check_gemm(qtype, gate.W, gate.W_aux, A, lda, gate_up, ldgu, BF_OUT_F16, M, F, K);
+    if (st == BF_OK) st = check_gemm(qtype, up.W, up.W_aux, A, lda, gate_up + F, ldgu, BF_OUT_F16, M, F, K);
+    if (st == BF_OK) st = check_gemm(qtype, down.W, down.W_aux, gate_up, ldgu, C, ldc, otype, M, N, F);
+    if (st != BF_OK) return st;
+    hipStream_t hs = (hipStream_t)stream;
+    bf::GemmArgs gs[3];
+    const bf_qweights* w[3] = {&gate, &up, &down};
+    for (int i = 0; i < 3; i++) {
+        bf::GemmArgs& g = gs[i];
+        g.qtype = (int)qtype;
+        g.W = (const uint8_t*)w[i]->W;
+        g.Waux = (const uint8_t*)w[i]->W_aux;
+        g.A = i < 2 ? A : gate_up;
+        g.lda = i < 2 ? lda : ldgu;
+        g.C = i == 0 ? (void*)gate_up : i == 1 ? (void*)(gate_up + F) : C;
+        g.ldc = i < 2 ? ldgu : ldc;
+        g.out_f16 = i < 2 ? 1 : otype == BF_OUT_F16;
+        g.M = M;
+        g.N = i < 2 ? F : N;
+        g.K = i < 2 ? K : F;
+    }
+    const bool fast = fast_eligible(gs[0]) && fast_eligible(gs[1]) && fast_eligible(gs[2]);
+    if (form == BF_FFN_ONE_LAUNCH) {
+        if (!fast || !bf::ffn_lds_supports(gs))
+            return fail(BF_ERR_UNSUPPORTED, "one-launch feed-forward block: batch 1-2 with every GEMM on the LDS-staged "
+                                            "kernel's batch-1 or all-of-A form (M=%d K=%d F=%d N=%d)", M, K, F, N);
+        return from_split(bf::ffn_lds(gs, hs), "feed-forward launch");
+    }
+    const bf_gemm_desc d[2] = {{gate.W, gate.W_aux, A, lda, gate_up, ldgu, M, F, K},
+                               {up.W, up.W_aux, A, lda, gate_up + F, ldgu, M, F, K}};
+    const bool two = fast && bf::lds_swiglu_supports(gs[2]);
+    if (form == BF_FFN_TWO_LAUNCHES && !two)
+        return fail(BF_ERR_UNSUPPORTED, "two-launch feed-forward block: batch 1-2 with the down projection's "
+                                        "activations resident in LDS (M=%d F=%d)", M, F);
+    st = bf_gemm_batched(qtype, BF_OUT_F16, 2, d, stream);
+    if (st != BF_OK) return st;
+    if (two && form != BF_FFN_CALLS) return from_hip(bf::gemm_lds_swiglu(gs[2], hs), "kernel launch");
+    // SiLU(gate) * up in place over the gate half, then the down GEMM
+    st = from_hip(bf::swiglu_f16(gate_up, ldgu, gate_up, ldgu, M, F, hs), "kernel launch");
+    if (st != BF_OK) return st;
+    return run_gemm(qtype, down.W, down.W_aux, gate_up, ldgu, C, ldc, otype, M, N, F, BF_ALGO_AUTO, stream);
+}
+
+bf_status bf_ffn_swiglu(bf_qtype qtype, bf_qweights gate, bf_qweights up, bf_qweights down, const uint16_t* A,
+                        int lda, uint16_t* gate_up, int ldgu, void* C, int ldc, bf_otype otype, int M, int K, int F,
+                        int N, void* stream) {
+    return bf_ffn_swiglu_ex(qtype, gate, up, down, A, lda, gate_up, ldgu, C, ldc, otype, M, K, F, N, BF_FFN_AUTO,
+                            stream);
+}
+
 bf_status bf_swiglu_f16(const uint16_t* gate_up, int ld, uint16_t* out, int ldo, int M, int K, void* stream) {
     g_last_error[0] = '\0';
     if (!gate_up || !out) return fail(BF_ERR_INVALID, "gate_up or out is NULL");

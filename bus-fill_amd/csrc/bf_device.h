@@ -205,9 +205,8 @@ __device__ __forceinline__ _Float16 swiglu_f16(_Float16 g, _Float16 u) {
     return (_Float16)(gf * __builtin_amdgcn_rcpf(1.0f + e) * (float)u);
 }
 
-// Eight fp16 pairs (16 bytes of gate at g, 16 of up at u) -> eight fp16 swiglu values.
-__device__ __forceinline__ u4 swiglu8(const uint16_t* g, const uint16_t* u) {
-    const u4 gv = *(const u4*)g, uv = *(const u4*)u;
+// Eight fp16 pairs (16 bytes of gate, 16 of up) -> eight fp16 swiglu values.
+__device__ __forceinline__ u4 swiglu8v(u4 gv, u4 uv) {
     u4 r;
 #pragma unroll
     for (int w = 0; w < 4; w++) {
@@ -219,6 +218,10 @@ __device__ __forceinline__ u4 swiglu8(const uint16_t* g, const uint16_t* u) {
         r[w] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
     }
     return r;
+}
+
+__device__ __forceinline__ u4 swiglu8(const uint16_t* g, const uint16_t* u) {
+    return swiglu8v(*(const u4*)g, *(const u4*)u);
 }
 
 }  // namespace bf

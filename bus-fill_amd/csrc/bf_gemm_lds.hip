@@ -80,11 +80,21 @@ namespace {
 // compute waves load all of A before the barrier (small A).  SW (batch 1 or
 // AC): A[m][k] = SiLU(A[m][k]) * A[m][K + k], formed as the compute waves load
 // it (the fused gate|up projection's output in, the down projection out).
-template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC, bool SW = false>
+// DEP (with BD or AC): A is the output of dep_n other workgroups of the same
+// launch (the dependency words at dep, laid out as kDepWords describes); the
+// compute waves meet the loaders first (so the weight stream starts at once),
+// wait for the release flag, then load A with device-scope loads.  dep_users
+// workgroups wait; the last of them past its wait clears the words.  CO: C is
+// stored with device-scope stores (written through to the point of coherence:
+// the output is such a dependency's A).
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC, bool SW = false, bool DEP = false,
+          bool CO = false>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                          const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
                                          int nslot, int na, int win, const uint8_t* __restrict__ Waux,
-                                         void* __restrict__ C, int ldc, int out_f16) {
+                                         void* __restrict__ C, int ldc, int out_f16, unsigned* dep = nullptr,
+                                         unsigned dep_n = 0, unsigned dep_users = 0) {
+    static_assert(!DEP || BD || AC, "a dependency needs A loaded by the compute waves");
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     static_assert(!BD || G == 4, "sub-block rows: four K segments");
     // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
@@ -140,6 +150,44 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         static_assert((NC + NL) * 256 == kFlagBytes, "each wave clears 64 flags");
         flags[64 * wave + lane] = 0;
         barrier_lds();
+    };
+    // DEP: the first compute wave polls its release flag (device scope), then
+    // releases the other compute waves through an LDS flag.  A wait that gives
+    // up poisons.
+    auto wait_dep = [&]() {
+        if (wave == NL) {
+            wait_device_count(dep + kDepLine0 + 64 * (bid % kDepLines), 1u, lane, flags + kPoison);
+            if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kDepFlag])), "v"(1) : "memory");
+        } else {
+            wait_flag(&flags[kDepFlag], flags + kPoison);
+        }
+    };
+    // DEP: A through a buffer resource, read with device-scope loads (the
+    // producers' stores were written through to the point of coherence)
+    const __amdgpu_buffer_rsrc_t a_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, DEP ? (int)(((int64_t)(M - 1) * lda + 2 * K) * 2) : 0,
+                                          0x00020000);
+    auto swiglu_dep = [&](int64_t elem) {
+        const int off = (int)(elem * 2);
+        return swiglu8v(__builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, kDeviceScope)),
+                        __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off + 2 * K, 0,
+                                                                                      kDeviceScope)));
+    };
+    // one result: C[m][row] (CO: a device-scope store)
+    auto store_c = [&](int64_t m, int64_t row, float v) {
+        const int64_t idx = m * ldc + row;
+        if constexpr (CO) {
+            const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, 0x7FFFFFFF, 0x00020000);
+            if (out_f16)
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)v), cr, (int)(idx * 2), 0,
+                                                      kDeviceScope);
+            else
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), cr, (int)(idx * 4), 0,
+                                                      kDeviceScope);
+        } else {
+            if (out_f16) ((_Float16*)C)[idx] = (_Float16)v;
+            else ((float*)C)[idx] = v;
+        }
     };
 
     if (wave < NL) {
@@ -270,6 +318,25 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         asm volatile("" :: "v"(warm));
+        if constexpr (DEP) {
+            // off the compute waves' path: once this workgroup is past its
+            // wait, count it; the last of the dep_users waiting workgroups
+            // takes the counts and the release flags back to zero for the next
+            // launch
+            if (wave == 0) {
+                wait_flag(&flags[kDepFlag], flags + kPoison);
+                unsigned old = 0;
+                if (lane == 0) old = __hip_atomic_fetch_add(dep + 64, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((unsigned)__builtin_amdgcn_readfirstlane(old) == dep_users - 1u) {
+                    if (lane < kDepLines) __hip_atomic_store(dep + kDepLine0 + 64 * lane, 0u, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT);
+                    if (lane == 0) {
+                        __hip_atomic_fetch_sub(dep, dep_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_fetch_sub(dep + 64, dep_users, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+            }
+        }
         return;
     }
 
@@ -298,18 +365,24 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         // raise a flag once their own loads are complete
         const int cw = wave - NL, nA = (nsg * 33 + 63) >> 6;
         const int rot = (int)(((unsigned)bid * 7u) % (unsigned)nA);
+        if constexpr (DEP) {
+            clear_flags_and_meet();
+            wait_dep();
+        }
         for (int i0 = cw; i0 < nA; i0 += NC) {
             const int i = i0 + rot < nA ? i0 + rot : i0 + rot - nA;
             const int P = 64 * i + lane;
             const int sg = min(P / 33, nsg - 1), c = min(P - 33 * (P / 33), 31);
-            if constexpr (SW) {
+            if constexpr (SW && DEP) {
+                if (P < nsg * 33) *(u4*)(lds + kFlagBytes + 1024 * i + 16 * lane) = swiglu_dep(256 * sg + 8 * c);
+            } else if constexpr (SW) {
                 if (P < nsg * 33)
                     *(u4*)(lds + kFlagBytes + 1024 * i + 16 * lane) = swiglu8(A + 256 * sg + 8 * c, A + K + 256 * sg + 8 * c);
             } else {
                 if (P < nsg * 33) dma16(A + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + 1024 * i));
             }
         }
-        clear_flags_and_meet();
+        if constexpr (!DEP) clear_flags_and_meet();
         signal_own_loads(&flags[cw], lane);
         wait_flags(flags, NC, lane, flags + kPoison);
     } else if constexpr (AC) {
@@ -318,19 +391,27 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         // ...) so that the loaders stream weights only, then wait for all of it
         const int cw = wave - NL;
         const int PA = M * G * 33, IA = (PA + 63) >> 6;
+        if constexpr (DEP) {
+            clear_flags_and_meet();
+            wait_dep();
+        }
         for (int f = cw; f < nsteps * IA; f += NC) {
             const int sg = f / IA, i = f - sg * IA;
             const uint32_t P = 64u * i + lane;
             const uint32_t m = P / (33u * G), rem = P - 33u * G * m, gg = rem / 33u, c = rem - 33u * gg;
-            const uint16_t* src = A + (int64_t)min((int)m, M - 1) * lda + 256 * (G * sg + gg) + 8 * min((int)c, 31);
-            if constexpr (SW) {
+            const int64_t elem = (int64_t)min((int)m, M - 1) * lda + 256 * (G * sg + gg) + 8 * min((int)c, 31);
+            const uint16_t* src = A + elem;
+            if constexpr (SW && DEP) {
+                if (P < (uint32_t)PA && c < 32)
+                    *(u4*)(lds + kFlagBytes + sg * seg_bytes + (i << 10) + 16 * lane) = swiglu_dep(elem);
+            } else if constexpr (SW) {
                 if (P < (uint32_t)PA && c < 32)
                     *(u4*)(lds + kFlagBytes + sg * seg_bytes + (i << 10) + 16 * lane) = swiglu8(src, src + K);
             } else {
                 if (P < (uint32_t)PA && c < 32) dma16(src, lds0 + (uint32_t)(kFlagBytes + sg * seg_bytes + (i << 10)));
             }
         }
-        clear_flags_and_meet();
+        if constexpr (!DEP) clear_flags_and_meet();
         signal_own_loads(&flags[cw], lane);
         wait_flags(flags, NC, lane, flags + kPoison);
     } else {
@@ -654,10 +735,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                 if (bad) sum = __builtin_nanf("");
                 const int m = v / R, rl = v - m * R;   // m = mt * R + m_loc
                 const int64_t row = row0 + rl;
-                if (m < M && row < N) {
-                    if (out_f16) ((_Float16*)C)[(int64_t)m * ldc + row] = (_Float16)sum;
-                    else ((float*)C)[(int64_t)m * ldc + row] = sum;
-                }
+                if (m < M && row < N) store_c(m, row, sum);
             }
         }
     }
@@ -680,10 +758,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                 y += dpp_xor(y, 1);
                 y += dpp_xor(y, 2);
                 if (bad) y = __builtin_nanf("");
-                if (g == 0 && kg == 0 && mt < M && row < N) {
-                    if (out_f16) ((_Float16*)C)[(int64_t)mt * ldc + row] = (_Float16)y;
-                    else ((float*)C)[(int64_t)mt * ldc + row] = y;
-                }
+                if (g == 0 && kg == 0 && mt < M && row < N) store_c(mt, row, y);
             }
         }
     }
@@ -813,7 +888,123 @@ hipError_t dispatch_lds_batched(const GemmArgs* gs, const LdsPlan* ps, int n, hi
     return launch_lds_batched<QT, 4, 2, false, false>(gs, ps, n, st);
 }
 
+// The SwiGLU feed-forward block in one launch: the gate and up projections
+// (jobs 0 and 1, fp16 outputs into the two halves of one gate|up buffer) and
+// the down projection (job 2) over SiLU(gate) * up, formed as its compute
+// waves load it.  Workgroups [0, g01) run the gate and up GEMMs with
+// device-scope stores and count themselves in cnt[0] once those have landed;
+// the last raises the release flags.  The down projection's workgroups start
+// their weight stream at once and wait for a release flag before they load
+// the activations.  Workgroups are dispatched
+// in id order, so every producer has started before any consumer waits, and
+// producers never wait on consumers: the launch cannot deadlock, whatever the
+// number of CUs.  The last down workgroup past its wait takes both counts back
+// (cnt[64] counts those workgroups), so the next launch that uses the
+// workspace finds them at zero.
+template <int QT, bool BD>
+__global__ __launch_bounds__(64 * (kNC + kNL))
+void k_ffn_lds(const LdsJobs jobs, unsigned* cnt) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    constexpr bool AC = !BD;
+    const int b = (int)blockIdx.x;
+    const int g01 = jobs.job[2].grid0;
+    if (b < g01) {
+        LdsJob j = jobs.job[0];
+        if (b >= jobs.job[1].grid0) j = jobs.job[1];
+        lds_body<QT, 4, 1, kNC, kNL, BD, false, AC, false, false, true>(b - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N,
+                                                                         j.K, j.nsub, j.nslot, j.na, j.win, j.Waux,
+                                                                         j.C, j.ldc, 1);
+        // every wave's device-scope stores have reached the point of coherence
+        // before the workgroup counts itself; the last producer raises the
+        // release flags
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            unsigned old = 0;
+            if (threadIdx.x == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((unsigned)__builtin_amdgcn_readfirstlane(old) == (unsigned)g01 - 1u && threadIdx.x < kDepLines)
+                __hip_atomic_store(cnt + kDepLine0 + 64 * threadIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+    const LdsJob j = jobs.job[2];
+    lds_body<QT, 4, 1, kNC, kNL, BD, false, AC, true, true>(b - g01, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nsub,
+                                                            j.nslot, j.na, j.win, j.Waux, j.C, j.ldc, jobs.out_f16,
+                                                            cnt, (unsigned)g01, gridDim.x - (unsigned)g01);
+}
+
+// Plans of the three GEMMs when the one-launch block serves them: batch 1
+// (sub-block rows form everywhere) or batch 2 (G = 4, one m-tile, all of A
+// resident, loaded by the compute waves).
+bool ffn_plans(const GemmArgs* gs, LdsPlan* ps) {
+    const int M = gs[2].M;
+    if (M > 2) return false;
+    for (int i = 0; i < 3; i++) {
+        if (gs[i].M != M || gs[i].qtype != gs[2].qtype) return false;
+        if (gs[i].qtype == QT_PLANES && ((uintptr_t)gs[i].Waux & 15)) return false;
+        if (!choose_lds(lds_shape(gs[i]), ps[i])) return false;
+        const LdsPlan& p = ps[i];
+        if (M == 1 ? !p.BD : (p.BD || p.RG || p.G != 4 || p.MT != 1 || p.na != gs[i].K / 1024)) return false;
+    }
+    return true;
+}
+
+template <int QT, bool BD>
+hipError_t launch_ffn(const GemmArgs* gs, const LdsPlan* ps, unsigned* cnt, hipStream_t st) {
+    auto k = k_ffn_lds<QT, BD>;
+    static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(attr_set.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        if (e != hipSuccess) return e;
+        attr_set.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    LdsJobs jobs = {};
+    jobs.n = 3;
+    jobs.out_f16 = gs[2].out_f16;
+    int grid = 0, lds = 0;
+    for (int i = 0; i < 3; i++) {
+        const GemmArgs& g = gs[i];
+        jobs.job[i] = LdsJob{g.W, g.Waux, g.A, g.C, g.lda, g.ldc, g.M, g.N, g.K, ps[i].nsub, ps[i].nslot,
+                             ps[i].na, ps[i].win, grid};
+        grid += ps[i].grid;
+        lds = std::max(lds, ps[i].lds);
+    }
+    hipLaunchKernelGGL(k, dim3(grid), dim3(64 * (kNC + kNL)), lds, st, jobs, cnt);
+    return hipGetLastError();
+}
+
+template <int QT>
+hipError_t dispatch_ffn(const GemmArgs* gs, const LdsPlan* ps, unsigned* cnt, hipStream_t st) {
+    if (ps[0].BD) return launch_ffn<QT, true>(gs, ps, cnt, st);
+    return launch_ffn<QT, false>(gs, ps, cnt, st);
+}
+
 }  // namespace
+
+bool ffn_lds_supports(const GemmArgs* gs) {
+    LdsPlan ps[3];
+    return ffn_plans(gs, ps);
+}
+
+hipError_t ffn_lds(const GemmArgs* gs, hipStream_t st) {
+    LdsPlan ps[3];
+    if (!ffn_plans(gs, ps)) return hipErrorInvalidValue;
+    // the dependency words at the start of the stream's workspace (left at
+    // zero by every launch that uses them)
+    unsigned* cnt = nullptr;
+    float* unused = nullptr;
+    hipError_t e = split_workspace(nullptr, st, kDepWords * 4, 0, &cnt, &unused);
+    if (e != hipSuccess) return e;
+    switch (gs[0].qtype) {
+        case QT_Q4_K: return dispatch_ffn<QT_Q4_K>(gs, ps, cnt, st);
+        case QT_PLANES: return dispatch_ffn<QT_PLANES>(gs, ps, cnt, st);
+        default: return dispatch_ffn<QT_Q4_0>(gs, ps, cnt, st);
+    }
+}
 
 bool lds_batched_supports(const GemmArgs* gs, int n) {
     if (n < 1) return false;

@@ -84,6 +84,14 @@ hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_
 hipError_t gemm_lds_swiglu(const GemmArgs& g, hipStream_t st);
 bool lds_swiglu_supports(const GemmArgs& g);
 hipError_t swiglu_f16(const uint16_t* gu, int ld, uint16_t* out, int ldo, int M, int K, hipStream_t st);
+// The SwiGLU feed-forward block in one launch (gs[0] gate and gs[1] up into
+// the two halves of one fp16 gate|up buffer, gs[2] the down projection whose A
+// is that buffer, SiLU(gate) * up formed as it is loaded): batch 1-2 where
+// every GEMM takes the LDS kernel's batch-1 form or its all-of-A form.  Two
+// counters in the stream's workspace (allocated on first use, never while
+// the stream is capturing: hipErrorStreamCaptureUnsupported).
+hipError_t ffn_lds(const GemmArgs* gs, hipStream_t st);
+bool ffn_lds_supports(const GemmArgs* gs);
 
 // Integer-dot activation path: int8 activations per 32 values (q | d | s
 // regions of one buffer of q8_bytes(M, K)) and the v_dot4_i32_i8 GEMM.

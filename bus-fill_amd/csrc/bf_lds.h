@@ -161,6 +161,37 @@ __device__ __forceinline__ void wait_lanes(const int* flag, bool need, int* pois
     mark_poison(poison);
 }
 
+// Buffer access cache policy sc1: device scope.  Such a store is written
+// through the XCD's L2 to the point of coherence of all XCDs; such a load
+// misses the L1 and the XCD's L2 for lines another XCD may have written.
+constexpr int kDeviceScope = 16;
+
+// A dependency between the workgroups of one launch, in device memory (one
+// 256-byte line per word): word 0 counts the producers that have stored their
+// results; word 64 counts the consumers that are past their wait; the last
+// producer raises kDepLines release flags (words kDepLine0 + 64 i), which the
+// consumers poll round robin, so that no one line takes every consumer's polls
+// (polls of a single line from every CU queue behind each other for several
+// microseconds).  The last consumer past its wait clears everything.
+constexpr int kDepLines = 32, kDepLine0 = 128;
+constexpr int kDepWords = kDepLine0 + 64 * kDepLines;
+
+// Spin until the device-scope word *cnt is at least n (lane 0 polls with
+// agent-scope atomic loads, which bypass the XCD's L2; a short s_sleep
+// between polls).  The bound (2^15 polls of about a microsecond each) stays
+// below the LDS waits' so that the poller, not a waiter, is the one to give up.
+constexpr int kDeviceWaitBound = 1 << 15;
+
+__device__ __forceinline__ void wait_device_count(const unsigned* cnt, unsigned n, int lane, int* poison) {
+    for (int it = 0; it < kDeviceWaitBound; it++) {
+        unsigned v = 0;
+        if (lane == 0) v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((unsigned)__builtin_amdgcn_readfirstlane(v) >= n) return;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    mark_poison(poison);
+}
+
 // Sets the LDS word at `flag` to 1 once every load this wave has issued has
 // completed; for direct-to-LDS loads completion includes the LDS write.
 __device__ __forceinline__ void signal_own_loads(int* flag, int lane) {

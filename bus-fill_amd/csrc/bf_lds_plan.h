@@ -36,6 +36,7 @@ inline constexpr int kSubCount = 768, kMaxSub = 128;
 inline constexpr int kSegCount = 896;                    // steps done with activation segment s, at 896 + s
 inline constexpr int kStepCounter = 15;                  // flags[15]: next step to take
 inline constexpr int kPoison = 13;                       // flags[13]: a bounded wait gave up (results become NaN)
+inline constexpr int kDepFlag = 14;                      // flags[14]: the activations' producers are done (one launch, two phases)
 inline constexpr int kASlots = 6;                        // activation instructions per loader and segment
 inline constexpr int kMinRing = 16;                      // fewest steps in a ring of reused step slots
 inline constexpr int kRingAhead = 16;                    // steps of lead that keep the weight stream going

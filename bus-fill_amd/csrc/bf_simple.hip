@@ -100,8 +100,10 @@ hipError_t gemm_simple(const GemmArgs& g, hipStream_t st) {
 
 // out[m][k] = SiLU(gu[m][k]) * gu[m][K + k] in fp16 (the formula the fused
 // down-projection GEMM applies while loading A), eight elements per thread.
-__global__ __launch_bounds__(256) void k_swiglu_f16(const uint16_t* __restrict__ gu, int ld,
-                                                    uint16_t* __restrict__ out, int ldo, int M, int K) {
+// out may be gu itself (in place over the gate half): each thread reads its
+// eight gate and eight up values before it writes the eight results.
+__global__ __launch_bounds__(256) void k_swiglu_f16(const uint16_t* gu, int ld, uint16_t* out, int ldo, int M,
+                                                    int K) {
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;   // group of eight in a row
     const int per_row = K >> 3;
     if (i >= (int64_t)M * per_row) return;

@@ -129,6 +129,61 @@ int time_seq(const std::vector<Launch>& seq, int otype, int algo, int warmup, in
     return 0;
 }
 
+// Times `steps` calls of call(i) (i continuing from the `warmup` untimed
+// ones), issued on st directly or captured into a graph and replayed.  One
+// uncaptured call comes first, so that any workspace the calls use exists
+// before a capture.
+template <class Call>
+int time_calls(Call call, int warmup, int steps, int use_graph, hipStream_t st, double* ms_out) {
+    if ((g_bf = call(0)) != BF_OK) return -1;
+    HCK(hipStreamSynchronize(st));
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    float ms = 0.f;
+    if (!use_graph) {
+        for (int i = 0; i < warmup; i++)
+            if ((g_bf = call(i)) != BF_OK) return -1;
+        HCK(hipStreamSynchronize(st));
+        HCK(hipEventRecord(e0, st));
+        for (int i = warmup; i < warmup + steps; i++)
+            if ((g_bf = call(i)) != BF_OK) return -1;
+        HCK(hipEventRecord(e1, st));
+    } else {
+        auto capture = [&](int first, int count, hipGraphExec_t* exec) -> int {
+            hipGraph_t g;
+            HCK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            for (int i = first; i < first + count; i++)
+                if ((g_bf = call(i)) != BF_OK) {
+                    hipGraph_t dead;
+                    (void)hipStreamEndCapture(st, &dead);
+                    return -1;
+                }
+            HCK(hipStreamEndCapture(st, &g));
+            HCK(hipGraphInstantiate(exec, g, nullptr, nullptr, 0));
+            HCK(hipGraphDestroy(g));
+            return 0;
+        };
+        hipGraphExec_t gw = nullptr, gs = nullptr;
+        if (warmup > 0 && capture(0, warmup, &gw)) return -1;
+        if (capture(warmup, steps, &gs)) return -1;
+        if (gw) HCK(hipGraphLaunch(gw, st));
+        HCK(hipStreamSynchronize(st));
+        HCK(hipEventRecord(e0, st));
+        HCK(hipGraphLaunch(gs, st));
+        HCK(hipEventRecord(e1, st));
+        HCK(hipEventSynchronize(e1));
+        if (gw) HCK(hipGraphExecDestroy(gw));
+        HCK(hipGraphExecDestroy(gs));
+    }
+    HCK(hipEventSynchronize(e1));
+    HCK(hipEventElapsedTime(&ms, e0, e1));
+    HCK(hipEventDestroy(e0));
+    HCK(hipEventDestroy(e1));
+    *ms_out = ms;
+    return 0;
+}
+
 __global__ __launch_bounds__(1024) void k_stream_read(const uint4* __restrict__ src, size_t n16,
                                                      unsigned* __restrict__ sink) {
     unsigned acc = 0;
@@ -245,6 +300,24 @@ int bfb_time_swiglu(int qtype, const void* const* W, const void* const* W_aux, i
     HCK(hipEventDestroy(e0));
     HCK(hipEventDestroy(e1));
     return 0;
+}
+
+// SwiGLU feed-forward blocks (bf_ffn_swiglu_ex in one form), cycling through
+// `count` blocks' weights (gate Wg[i], up Wu[i], down Wd[i]; planes scale
+// planes in the *_aux arrays or NULL), same A, gate_up and C.
+int bfb_time_ffn(int qtype, const void* const* Wg, const void* const* Wg_aux, const void* const* Wu,
+                 const void* const* Wu_aux, const void* const* Wd, const void* const* Wd_aux, int count,
+                 const uint16_t* A, uint16_t* gate_up, void* C, int M, int K, int F, int N, int form, int warmup,
+                 int steps, int use_graph, void* stream, double* ms_out) {
+    hipStream_t st = (hipStream_t)stream;
+    auto call = [&](int r) -> bf_status {
+        const int i = r % count;
+        const bf_qweights g{Wg[i], Wg_aux ? Wg_aux[i] : nullptr}, u{Wu[i], Wu_aux ? Wu_aux[i] : nullptr},
+            d{Wd[i], Wd_aux ? Wd_aux[i] : nullptr};
+        return bf_ffn_swiglu_ex((bf_qtype)qtype, g, u, d, A, K, gate_up, 2 * F, C, N, BF_OUT_F32, M, K, F, N,
+                                (bf_ffn_form)form, st);
+    };
+    return time_calls(call, warmup, steps, use_graph, st, ms_out);
 }
 
 // The integer-dot path against the fp16 GEMM over the same weight rotation:

@@ -24,7 +24,9 @@
  *     passed it) and kept until the process ends.  It is never allocated while
  *     the stream is being captured into a graph: such a call returns
  *     BF_ERR_UNSUPPORTED; make one uncaptured call of the shape on the stream
- *     first, or use bf_gemm_noalloc.  A captured graph holds the workspace of
+ *     first, or use bf_gemm_noalloc.  The one-launch feed-forward block
+ *     (bf_ffn_swiglu_ex, BF_FFN_ONE_LAUNCH) keeps its hand-over words in the
+ *     same workspace.  A captured graph holds the workspace of
  *     the stream it was captured on: replaying it while other exchanging work
  *     runs on that stream (or another replay of it) races.
  *   - fp16 values travel as uint16_t bit patterns.
@@ -176,9 +178,67 @@ bf_status bf_gemm_swiglu(bf_qtype qtype, const void* W, const void* W_aux,
                          int M, int N, int K, void* stream);
 
 /* out[m][k] = RN_fp16(SiLU(g) * u) for g = gate_up[m][k], u = gate_up[m][K + k],
- * computed in fp32 as g / (1 + e^-g) * u.  K % 8 == 0; rows 16-byte aligned. */
+ * computed in fp32 as g / (1 + e^-g) * u.  K % 8 == 0; rows 16-byte aligned.
+ * out may be gate_up itself (ldo = ld): the results then replace the gate half. */
 bf_status bf_swiglu_f16(const uint16_t* gate_up, int ld, uint16_t* out, int ldo,
                         int M, int K, void* stream);
+
+/* The weights of one linear: W, and for BF_Q4_0_PLANES its scale plane
+ * (NULL for the other formats). */
+typedef struct {
+    const void* W;
+    const void* W_aux;
+} bf_qweights;
+
+/* A SwiGLU feed-forward block, C[M][N] = (SiLU(A . Wg^T) * (A . Wu^T)) . Wd^T,
+ * with gate and up [F][K] and down [N][F] in one format.  gate_up[M][ldgu]
+ * (ldgu >= 2F, rows 16-byte aligned) is the caller's fp16 buffer for the
+ * intermediate: the gate projection goes to columns 0..F-1 and the up
+ * projection to F..2F-1, each rounded to fp16 as bf_gemm rounds an fp16
+ * output, and SiLU(g) * u is rounded as bf_swiglu_f16 rounds it, so C is
+ * bit-identical to bf_gemm (gate), bf_gemm (up), bf_swiglu_f16, bf_gemm
+ * (down), whichever form runs:
+ *   BF_FFN_TWO_LAUNCHES: batch 1-2 with the down projection's activations
+ *     resident in LDS (as bf_gemm_swiglu): the gate and up GEMMs in one
+ *     launch (bf_gemm_batched), then the down projection with SiLU(g) * u
+ *     formed as its activations are loaded.  gate_up holds the two
+ *     projections on return.
+ *   BF_FFN_ONE_LAUNCH: batch 1-2 where every GEMM takes the LDS-staged
+ *     kernel's batch-1 or all-of-A form: one launch, the down projection's
+ *     workgroups streaming their weights while the gate and up workgroups
+ *     finish and loading their activations once the last of those has
+ *     stored its rows (device-scope stores, a count and release flags in the
+ *     stream's workspace, described at the top of this file: allocated on
+ *     the first such call, BF_ERR_UNSUPPORTED when that call is captured).
+ *     Measured slower than two launches at every size tried (7-150 MB of
+ *     weights: the in-launch hand-over costs more serial memory round trips
+ *     than a kernel boundary); kept for comparison.  gate_up as above.
+ *   BF_FFN_CALLS: any batch: the gate and up GEMMs, SiLU(g) * u in place over
+ *     the gate half of gate_up, the down GEMM (gate_up then holds SiLU(g) * u
+ *     and the up projection).
+ *   BF_FFN_AUTO (bf_ffn_swiglu): two launches where they apply, else calls.
+ * gate_up must not overlap A, C or the weights.  No counterpart in the
+ * reference, whose only entry point is the single-GEMM kernel
+ * (kernels/busfill_v1a.cu:41-46) and whose end-to-end runs drive a dense
+ * Q4_K_M model through llama.cpp (RESULTS.md:66-68); in a 27B-class decoder
+ * layer this block holds 150 MB of the linears' 186 MB of weights. */
+typedef enum {
+    BF_FFN_AUTO = 0,
+    BF_FFN_ONE_LAUNCH = 1,
+    BF_FFN_TWO_LAUNCHES = 2,
+    BF_FFN_CALLS = 3
+} bf_ffn_form;
+
+bf_status bf_ffn_swiglu(bf_qtype qtype, bf_qweights gate, bf_qweights up, bf_qweights down,
+                        const uint16_t* A, int lda, uint16_t* gate_up, int ldgu,
+                        void* C, int ldc, bf_otype otype, int M, int K, int F, int N, void* stream);
+
+/* bf_ffn_swiglu in a chosen form; BF_ERR_UNSUPPORTED when that form does not
+ * serve the shape (nothing enqueued). */
+bf_status bf_ffn_swiglu_ex(bf_qtype qtype, bf_qweights gate, bf_qweights up, bf_qweights down,
+                           const uint16_t* A, int lda, uint16_t* gate_up, int ldgu,
+                           void* C, int ldc, bf_otype otype, int M, int K, int F, int N,
+                           bf_ffn_form form, void* stream);
 
 /* ---------------------------------------------------------------- integer-dot path
  * Activations quantized to int8 per 32 values, multiplied in with integer

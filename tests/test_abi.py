@@ -144,6 +144,47 @@ def test_swiglu_entries_reject_before_any_launch():
     assert L.bf_swiglu_f16(FAKE, 2 * K, FAKE + 8, K, 1, K, None) == bf.ERR_INVALID
 
 
+def test_ffn_entry_rejects_before_any_launch():
+    """bf_ffn_swiglu argument checks: every case returns before a launch (and
+    before the workspace is looked up), so no GPU is needed."""
+    L = bf.lib()
+    K, F, N = 1024, 2048, 512
+    w = bf.QWeights(FAKE, None)
+
+    def call(qtype=bf.Q4_K, gate=w, up=w, down=w, A=FAKE, lda=K, gu=FAKE, ldgu=2 * F, C=FAKE, ldc=N,
+             otype=bf.OUT_F32, M=1, K_=K, F_=F, N_=N):
+        return L.bf_ffn_swiglu(qtype, gate, up, down, A, lda, gu, ldgu, C, ldc, otype, M, K_, F_, N_, None)
+
+    assert call(gu=None) == bf.ERR_INVALID
+    assert call(F_=12) == bf.ERR_INVALID                       # F % 8
+    assert call(ldgu=2 * F - 8) == bf.ERR_INVALID              # gate and up must both fit
+    assert call(gu=FAKE + 8) == bf.ERR_INVALID                 # 16-byte rows
+    assert call(ldgu=2 * F + 4) == bf.ERR_INVALID
+    assert call(gate=bf.QWeights(None, None)) == bf.ERR_INVALID
+    assert call(up=bf.QWeights(None, None)) == bf.ERR_INVALID
+    assert call(down=bf.QWeights(FAKE, FAKE)) == bf.ERR_INVALID   # W_aux only for planes
+    assert call(qtype=bf.Q4_0_PLANES) == bf.ERR_INVALID          # planes without scale planes
+    assert call(K_=1000) == bf.ERR_INVALID
+    assert call(F_=2048 + 8, ldgu=2 * 2048 + 16) == bf.ERR_INVALID   # down's K = F: multiple of 256 for Q4_K
+    assert "multiple of 256" in L.bf_last_error().decode()
+    assert call(A=None) == bf.ERR_INVALID
+    assert call(C=None) == bf.ERR_INVALID
+    assert call(ldc=N - 1) == bf.ERR_INVALID
+    assert call(M=0) == bf.ERR_INVALID
+    assert call(otype=3) == bf.ERR_INVALID
+    assert L.bf_ffn_swiglu_ex(bf.Q4_K, w, w, w, FAKE, K, FAKE, 2 * F, FAKE, N, bf.OUT_F32, 1, K, F, N, 4,
+                              None) == bf.ERR_INVALID          # unknown form
+    # forms that do not serve batch 3 refuse before anything is enqueued
+    for form in (bf.FFN_ONE_LAUNCH, bf.FFN_TWO_LAUNCHES):
+        assert L.bf_ffn_swiglu_ex(bf.Q4_K, w, w, w, FAKE, K, FAKE, 2 * F, FAKE, N, bf.OUT_F32, 3, K, F, N, form,
+                                  None) == bf.ERR_UNSUPPORTED
+
+
+def test_qweights_layout_matches_header():
+    assert ctypes.sizeof(bf.QWeights) == 16 and bf.QWeights.W_aux.offset == 8
+    assert "bf_qweights" in HDR
+
+
 def test_q8_entries_reject_before_any_launch():
     """bf_q8_bytes / bf_quantize_q8 / bf_gemm_q8 argument checks (no GPU needed:
     every call below is rejected before a launch)."""
