@@ -320,6 +320,39 @@ def test_split_batch_parity(dev, qt, N, K):
         gpu_gemm(w, O.gen_act(33, K, seed=1), dev, algo=bf.ALGO_SPLIT, dw=dw)
 
 
+def test_split_exchange_on_every_stream(dev):
+    """The K-split kernel's XCD-local exchange on streams whose hardware queues
+    start the workgroup round robin on different XCDs (the null stream and
+    several created streams): finite, identical bits on every stream, and
+    single and batched launches agree on each (a workgroup takes its row group
+    from the XCD it runs on, whatever the starting XCD)."""
+    N, K, M = 5120, 5120, 32
+    w = O.gen_weights(O.Q4_K, N, K, seed=41)
+    dw = upload(w, dev)
+    A = O.gen_act(M, K, seed=42)
+    Ad = to_dev(A, dev)
+    ref = None
+    streams = [None] + [torch.cuda.Stream() for _ in range(5)]
+    torch.cuda.synchronize()
+    for i, s in enumerate(streams):
+        C = torch.full((M, N), float("nan"), device=dev)
+        C2 = torch.full((M, N), float("nan"), device=dev)
+        st = s.cuda_stream if s is not None else 0
+        bf.gemm(O.Q4_K, dw[0], None, Ad, C, M, N, K, algo=bf.ALGO_SPLIT, stream=st)
+        d = (bf.GemmDesc * 2)(bf.GemmDesc(dw[0].data_ptr(), None, Ad.data_ptr(), K, C2.data_ptr(), N, M, N // 2, K),
+                              bf.GemmDesc(dw[0].data_ptr() + (N // 2) * (K // 256) * 144, None, Ad.data_ptr(), K,
+                                          C2.data_ptr() + (N // 2) * 4, N, M, N // 2, K))
+        assert bf.lib().bf_gemm_batched(O.Q4_K, bf.OUT_F32, 2, d, st) == 0
+        torch.cuda.synchronize()
+        got = C.cpu().numpy().astype(np.float64)
+        assert np.isfinite(got).all(), f"stream {i}"
+        if ref is None:
+            ref = got
+            Ref(w, A).check(got, "split on the null stream", form="f16")
+        assert (got == ref).all(), f"stream {i}"
+        assert np.isfinite(C2.cpu().numpy()).all(), f"batched, stream {i}"
+
+
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
 @pytest.mark.parametrize("N,K", [(1, 256), (77, 2048), (200, 5120), (5120, 5120), (600, 17408), (7168, 5120)])
 def test_dense_batch_parity(dev, qt, N, K):
