@@ -325,7 +325,7 @@ def run_layer(L, args, dev):
               arr(ctypes.c_int, [s[4] for s in seq]), 0)
     out = []
     # "single": one bf_gemm per linear; "batched": the layer's five linears in one
-    # bf_gemm_batched call (one launch when all of them are K-split GEMMs)
+    # bf_gemm_batched call (one launch per kernel the linears take)
     modes = ("single", "batched") if args.layer_launch == "both" else (args.layer_launch,)
     for mode in modes:
         for graph in ((0, 1) if args.graph == "both" else (int(args.graph),)):

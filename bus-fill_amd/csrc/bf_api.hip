@@ -84,6 +84,20 @@ bool fast_eligible(const bf::GemmArgs& g) {
     return true;
 }
 
+// The kernel bf_gemm launches for g when it takes one launch of a kernel that
+// has a batched form (BF_ALGO_LDS, _SPLIT or _DENSE); BF_ALGO_AUTO otherwise
+// (several launches, or another kernel).
+bf_algo one_launch_algo(const bf::GemmArgs& g) {
+    if (!fast_eligible(g) || g.M > kMaxMPerLaunch) return BF_ALGO_AUTO;
+    // above 32 rows bf_gemm takes one launch only where the dense kernel serves g
+    if (g.M > kSplitMaxM && !bf::dense_supports(g)) return BF_ALGO_AUTO;
+    const bf_algo mid = mid_batch_choice(g);
+    if (mid != BF_ALGO_AUTO) return mid;
+    if (bf::lds_supports(g)) return BF_ALGO_LDS;
+    if (bf::split_supports(g)) return BF_ALGO_SPLIT;
+    return g.M > kSplitMaxM ? BF_ALGO_DENSE : BF_ALGO_AUTO;
+}
+
 bf_status check_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
                      int ldc, bf_otype otype, int M, int N, int K) {
     bf_status st = check_weights(qtype, W, W_aux, N, K);
@@ -290,12 +304,16 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
         const bf_status st = check_gemm(qtype, d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, otype, d.M, d.N, d.K);
         if (st != BF_OK) return st;
     }
-    // one launch per eight GEMMs when every one of them takes the same
-    // LDS-staged kernel shape (batch 1-8) or every one is a K-split GEMM (the
-    // automatic choice at 9-32 rows when the activations do not fit in LDS)
+    // The GEMMs are grouped by the kernel bf_gemm would launch for each (its
+    // results are then the same bits) and every group of two or more shares
+    // launches: the LDS-staged kernel at batch 1-8 (one kernel shape), the
+    // K-split kernel at 9-32 rows, the dense kernel (one batch size); the
+    // rest, and any group its batched launch does not serve, run one by one.
+    hipStream_t hs = (hipStream_t)stream;
     std::vector<bf::GemmArgs> gs(count);
-    bool all_lds = count > 1, all_split = count > 1;
-    for (int i = 0; i < count && (all_lds || all_split); i++) {
+    std::vector<int> grp[3];                           // LDS, K-split, dense
+    std::vector<int> single;
+    for (int i = 0; i < count; i++) {
         const bf_gemm_desc& d = descs[i];
         bf::GemmArgs& g = gs[i];
         g.qtype = (int)qtype;
@@ -309,19 +327,29 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
         g.M = d.M;
         g.N = d.N;
         g.K = d.K;
-        // one launch only where bf_gemm would take the same kernel for every GEMM
-        // (its results are then the same bits)
-        const bool fast = fast_eligible(g), mid = fast && mid_batch_choice(g) != BF_ALGO_AUTO;
-        const bool lds = fast && !mid && bf::lds_supports(g);
-        all_lds = all_lds && lds;
-        all_split = all_split && fast && !lds && d.M <= kSplitMaxM && bf::split_supports(g) &&
-                    (!mid || mid_batch_choice(g) == BF_ALGO_SPLIT);
+        const bf_algo a = one_launch_algo(g);
+        if (a == BF_ALGO_LDS) grp[0].push_back(i);
+        else if (a == BF_ALGO_SPLIT) grp[1].push_back(i);
+        else if (a == BF_ALGO_DENSE) grp[2].push_back(i);
+        else single.push_back(i);
     }
-    if (all_lds && bf::lds_batched_supports(gs.data(), count))
-        return from_hip(bf::gemm_lds_batched(gs.data(), count, (hipStream_t)stream), "batched launch");
-    if (all_split && bf::split_batched_supports(gs.data(), count))
-        return from_split(bf::gemm_split_batched(gs.data(), count, nullptr, (hipStream_t)stream), "batched launch");
-    for (int i = 0; i < count; i++) {
+    for (int k = 0; k < 3; k++) {
+        std::vector<bf::GemmArgs> sub;
+        for (int i : grp[k]) sub.push_back(gs[i]);
+        const int n = (int)sub.size();
+        const bool ok = n > 1 && (k == 0   ? bf::lds_batched_supports(sub.data(), n)
+                                  : k == 1 ? bf::split_batched_supports(sub.data(), n)
+                                           : bf::dense_batched_supports(sub.data(), n));
+        if (!ok) {
+            single.insert(single.end(), grp[k].begin(), grp[k].end());
+            continue;
+        }
+        const bf_status st = k == 0   ? from_hip(bf::gemm_lds_batched(sub.data(), n, hs), "batched launch")
+                             : k == 1 ? from_split(bf::gemm_split_batched(sub.data(), n, nullptr, hs), "batched launch")
+                                      : from_split(bf::gemm_dense_batched(sub.data(), n, nullptr, hs), "batched launch");
+        if (st != BF_OK) return st;
+    }
+    for (int i : single) {
         const bf_gemm_desc& d = descs[i];
         const bf_status st =
             run_gemm(qtype, d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, otype, d.M, d.N, d.K, BF_ALGO_AUTO, stream);

@@ -89,17 +89,15 @@ __host__ __device__ __forceinline__ int range_owner(int t, int T, int G) {
     return (int)(((int64_t)(t + 1) * G + T - 1) / T) - 1;
 }
 
-// One workgroup per CU (the rings fill the LDS), so at most two waves per SIMD.
+// One GEMM's share of a launch: workgroup p of its G.
 template <int QT, int MT>
-__global__ __launch_bounds__(64 * (kDnNC + kDnNL)) __attribute__((amdgpu_waves_per_eu(1, 2)))
-void k_gemm_dense(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux, const uint16_t* __restrict__ A,
-                  int lda, void* __restrict__ C, int ldc, int out_f16, int M, int N, int K, int T, int G, int DW,
-                  int DA, float* __restrict__ ws) {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+__device__ __forceinline__ void dense_body(int p, uint8_t* lds, const uint8_t* __restrict__ W,
+                                           const uint8_t* __restrict__ Waux, const uint16_t* __restrict__ A, int lda,
+                                           void* __restrict__ C, int ldc, int out_f16, int M, int N, int K, int T,
+                                           int G, int DW, int DA, float* __restrict__ ws) {
     constexpr int NC = kDnNC, NL = kDnNL, ROWS = kDnRows;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int p = (int)blockIdx.x;
     const int nsg = K >> 8;
     const int t0 = range_first(p, T, G), t1 = range_first(p + 1, T, G);
     int* const flags = (int*)lds;
@@ -318,15 +316,57 @@ void k_gemm_dense(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Wau
     }
 }
 
+// One workgroup per CU (the rings fill the LDS), so at most two waves per SIMD.
+template <int QT, int MT>
+__global__ __launch_bounds__(64 * (kDnNC + kDnNL)) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void k_gemm_dense(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux, const uint16_t* __restrict__ A,
+                  int lda, void* __restrict__ C, int ldc, int out_f16, int M, int N, int K, int T, int G, int DW,
+                  int DA, float* __restrict__ ws) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    dense_body<QT, MT>((int)blockIdx.x, lds, W, Waux, A, lda, C, ldc, out_f16, M, N, K, T, G, DW, DA, ws);
+}
+
+// Several independent GEMMs of one batch size in one launch, their grids back
+// to back: each GEMM keeps the ranges, pieces and partial slots a launch of
+// its own would have (so the same bits), and one k_dense_sum_batched launch
+// adds the split row groups of all of them.
+constexpr int kDnMaxJobs = 8;
+struct DenseJob {
+    const uint8_t* W;
+    const uint8_t* Waux;
+    const uint16_t* A;
+    void* C;
+    float* ws;                           // this GEMM's partial slots
+    int lda, ldc, N, K, T, G, grid0, rg0;  // rg0: the GEMM's first row group in the sum launch
+};
+struct DenseJobs {
+    DenseJob job[kDnMaxJobs];
+    int n, M, out_f16, DW, DA;
+};
+
+template <int QT, int MT>
+__global__ __launch_bounds__(64 * (kDnNC + kDnNL)) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void k_gemm_dense_batched(const DenseJobs jobs) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    // the last job whose grid starts at or before this workgroup (uniform
+    // selects over the kernel arguments: no dynamic indexing)
+    DenseJob j = jobs.job[0];
+#pragma unroll
+    for (int i = 1; i < kDnMaxJobs; i++)
+        if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
+    dense_body<QT, MT>((int)blockIdx.x - j.grid0, lds, j.W, j.Waux, j.A, j.lda, j.C, j.ldc, jobs.out_f16, jobs.M, j.N,
+                       j.K, j.T, j.G, jobs.DW, jobs.DA, j.ws);
+}
+
 // C for the row groups split between workgroups: the sum of their pieces in
 // piece order (the workgroup order), so the bits never depend on timing.
 // Block (rg, y): batch rows 8 y .. 8 y + 7, thread x: row quad x % 32 of
 // batch row 8 y + x / 32.  Row groups held whole by one workgroup were
 // written by it.
-__global__ __launch_bounds__(256) void k_dense_sum(const float* __restrict__ ws, void* __restrict__ C, int ldc,
-                                                   int out_f16, int M, int N, int T, int G, int nsg) {
+__device__ __forceinline__ void dense_sum_body(int rg, const float* __restrict__ ws, void* __restrict__ C, int ldc,
+                                               int out_f16, int M, int N, int T, int G, int nsg) {
     constexpr int ROWS = kDnRows;
-    const int rg = (int)blockIdx.x, m = 8 * (int)blockIdx.y + ((int)threadIdx.x >> 5);
+    const int m = 8 * (int)blockIdx.y + ((int)threadIdx.x >> 5);
     const int pf = range_owner(rg * nsg, T, G), pl = range_owner(rg * nsg + nsg - 1, T, G);
     if (pf == pl || m >= M) return;
     const int Mp = (M + 3) & ~3, nl = 4 * ((int)threadIdx.x & 31);
@@ -351,6 +391,19 @@ __global__ __launch_bounds__(256) void k_dense_sum(const float* __restrict__ ws,
             else ((float*)C)[o + i] = s[i];
         }
     }
+}
+
+__global__ __launch_bounds__(256) void k_dense_sum(const float* __restrict__ ws, void* __restrict__ C, int ldc,
+                                                   int out_f16, int M, int N, int T, int G, int nsg) {
+    dense_sum_body((int)blockIdx.x, ws, C, ldc, out_f16, M, N, T, G, nsg);
+}
+
+__global__ __launch_bounds__(256) void k_dense_sum_batched(const DenseJobs jobs) {
+    DenseJob j = jobs.job[0];
+#pragma unroll
+    for (int i = 1; i < kDnMaxJobs; i++)
+        if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].rg0) j = jobs.job[i];
+    dense_sum_body((int)blockIdx.x - j.rg0, j.ws, j.C, j.ldc, jobs.out_f16, jobs.M, j.N, j.T, j.G, j.K / 256);
 }
 
 struct DensePlan {
@@ -412,6 +465,65 @@ hipError_t launch_dense(const GemmArgs& g, const DensePlan& p, const Scratch* sc
     return hipGetLastError();
 }
 
+// Up to kDnMaxJobs GEMMs of one format, one batch size and one output type:
+// one launch of their grids back to back, one sum launch.
+template <int QT, int MT>
+hipError_t launch_dense_batched(const GemmArgs* gs, const DensePlan* ps, int n, const Scratch* scratch,
+                                hipStream_t st) {
+    auto k = k_gemm_dense_batched<QT, MT>;
+    static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(attr_set.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        if (e != hipSuccess) return e;
+        attr_set.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    // one workspace: every GEMM's partial slots at its own 256-byte offset
+    size_t ptot = 0;
+    for (int i = 0; i < n; i++) ptot += dense_partial_bytes(gs[i], ps[i]);
+    unsigned* counters = nullptr;
+    float* parts = nullptr;
+    e = split_workspace(scratch, st, 0, ptot, &counters, &parts);
+    if (e != hipSuccess) return e;
+    DenseJobs jobs = {};
+    jobs.n = n;
+    jobs.M = gs[0].M;
+    jobs.out_f16 = gs[0].out_f16;
+    jobs.DW = ps[0].DW;
+    jobs.DA = ps[0].DA;
+    int grid = 0, lds = 0, rgs = 0;
+    bool split = false;
+    size_t po = 0;
+    for (int i = 0; i < n; i++) {
+        const GemmArgs& g = gs[i];
+        const DensePlan& p = ps[i];
+        jobs.job[i] = DenseJob{g.W, g.Waux, g.A, g.C, (float*)((uint8_t*)parts + po), g.lda, g.ldc, g.N, g.K,
+                               p.T, p.G, grid, rgs};
+        po += dense_partial_bytes(g, p);
+        grid += p.G;
+        rgs += p.rgs;
+        lds = std::max(lds, p.lds);
+        split = split || p.split;
+    }
+    hipLaunchKernelGGL(k, dim3(grid), dim3(64 * (kDnNC + kDnNL)), lds, st, jobs);
+    e = hipGetLastError();
+    if (e != hipSuccess || !split) return e;
+    hipLaunchKernelGGL(k_dense_sum_batched, dim3(rgs, (jobs.M + 7) / 8), dim3(256), 0, st, jobs);
+    return hipGetLastError();
+}
+
+template <int QT>
+hipError_t dispatch_dense_batched(const GemmArgs* gs, const DensePlan* ps, int n, const Scratch* scratch,
+                                  hipStream_t st) {
+    if (ps[0].MT == 1) return launch_dense_batched<QT, 1>(gs, ps, n, scratch, st);
+    if (ps[0].MT == 2) return launch_dense_batched<QT, 2>(gs, ps, n, scratch, st);
+    if (ps[0].MT == 3) return launch_dense_batched<QT, 3>(gs, ps, n, scratch, st);
+    return launch_dense_batched<QT, 4>(gs, ps, n, scratch, st);
+}
+
 template <int QT>
 hipError_t dispatch_dense(const GemmArgs& g, const DensePlan& p, const Scratch* scratch, hipStream_t st) {
     if (p.MT == 1) return launch_dense<QT, 1>(g, p, scratch, st);
@@ -433,6 +545,34 @@ size_t dense_scratch_bytes(const GemmArgs& g, size_t limit) {
     if (!plan_dense(g, p, device_cus())) return ~(size_t)0;
     const size_t need = dense_partial_bytes(g, p);
     return need <= limit ? need : ~(size_t)0;
+}
+
+bool dense_batched_supports(const GemmArgs* gs, int n) {
+    if (n < 1) return false;
+    for (int i = 0; i < n; i++) {
+        DensePlan p;
+        if (gs[i].qtype != gs[0].qtype || gs[i].out_f16 != gs[0].out_f16 || gs[i].M != gs[0].M) return false;
+        if (gs[i].qtype == QT_PLANES && ((uintptr_t)gs[i].Waux & 15)) return false;
+        if (!plan_dense(gs[i], p, device_cus())) return false;
+    }
+    return true;
+}
+
+hipError_t gemm_dense_batched(const GemmArgs* gs, int n, const Scratch* scratch, hipStream_t st) {
+    if (!dense_batched_supports(gs, n)) return hipErrorInvalidValue;
+    for (int i0 = 0; i0 < n; i0 += kDnMaxJobs) {
+        const int m = std::min(kDnMaxJobs, n - i0);
+        DensePlan ps[kDnMaxJobs];
+        for (int i = 0; i < m; i++) plan_dense(gs[i0 + i], ps[i], device_cus());
+        hipError_t e;
+        switch (gs[0].qtype) {
+            case QT_Q4_K: e = dispatch_dense_batched<QT_Q4_K>(gs + i0, ps, m, scratch, st); break;
+            case QT_PLANES: e = dispatch_dense_batched<QT_PLANES>(gs + i0, ps, m, scratch, st); break;
+            default: e = dispatch_dense_batched<QT_Q4_0>(gs + i0, ps, m, scratch, st); break;
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t gemm_dense(const GemmArgs& g, const Scratch* scratch, hipStream_t st) {

@@ -76,6 +76,11 @@ bool dense_supports(const GemmArgs& g);
 // Workspace bytes of the plan chosen under a workspace limit (0 when it does
 // not split K; SIZE_MAX when no plan fits the limit).
 size_t dense_scratch_bytes(const GemmArgs& g, size_t limit);
+// Independent dense-kernel GEMMs of one format, one batch size and one output
+// type, in launches of up to eight (their grids back to back, each with the
+// ranges of a launch of its own) and one sum launch each.
+hipError_t gemm_dense_batched(const GemmArgs* gs, int n, const Scratch* scratch, hipStream_t st);
+bool dense_batched_supports(const GemmArgs* gs, int n);
 
 hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
                        int N, int K, hipStream_t st);

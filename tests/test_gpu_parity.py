@@ -513,8 +513,8 @@ def test_batched_matches_single_launches_large_matrices(dev):
     """bf_gemm sums a K-split GEMM whose grid takes more than one workgroup per
     CU in a second launch (k_split_sum) and sends 9-32 rows on matrices of
     3 * 2^24 weights or more to the dense kernel; bf_gemm_batched's one launch
-    sums splits in-kernel.  Same split order, so the same bits; a batch holding
-    a GEMM that bf_gemm gives the dense kernel runs as one call per GEMM."""
+    sums splits in-kernel.  Same split order, so the same bits; a GEMM that
+    bf_gemm gives the dense kernel goes to the batch's dense launch."""
     for shapes in ([(17408, 5120, 16), (7168, 5120, 16)], [(7168, 5120, 32), (1792, 5120, 32)],
                    [(5120, 17408, 32), (1792, 5120, 32)]):
         ws = [O.gen_weights(O.Q4_K, N, K, seed=N + K + M) for N, K, M in shapes]
@@ -529,6 +529,35 @@ def test_batched_matches_single_launches_large_matrices(dev):
             got = C.cpu().numpy().astype(np.float64)
             assert (got == ref).all(), shapes[i]
             Ref(ws[i], As[i]).check(got, f"batched q4_k {shapes[i]}")
+
+
+@pytest.mark.parametrize("M,shapes", [
+    (32, [(7168, 5120), (5120, 5120), (17408, 5120), (17408, 5120), (5120, 17408)]),   # a 27B-class layer
+    (64, [(200, 5120), (5120, 2048), (77, 2048), (1792, 5120)]),
+    (128, [(5120, 5120), (300, 1024)]),
+    (9, [(17408, 5120), (5120, 17408), (1000, 2048)]),
+], ids=["layer-m32", "m64", "m128", "m9"])
+def test_batched_groups_by_kernel(dev, M, shapes):
+    """bf_gemm_batched groups the GEMMs by the kernel bf_gemm gives each: the
+    K-split ones share a launch, the dense ones share a launch (each with the
+    ranges of a launch of its own) and one sum launch.  Bit-identical to one
+    bf_gemm per GEMM, twice in a row (the workspace reused), and the smaller
+    outputs against the oracle."""
+    ws = [O.gen_weights(O.Q4_K, N, K, seed=N + 3 * K + M) for N, K in shapes]
+    dws = [upload(w, dev) for w in ws]
+    As = [O.gen_act(M, K, seed=K + M + i) for i, (N, K) in enumerate(shapes)]
+    dAs = [to_dev(A, dev) for A in As]
+    for rep in range(2):
+        singles = [gpu_gemm(w, A, dev, dw=dw) for w, A, dw in zip(ws, As, dws)]
+        Cs = [torch.full((M, N), float("nan"), device=dev) for N, K in shapes]
+        bf.gemm_batched(O.Q4_K, [(dw[0], dw[1], dA, C, M, N, K) for dw, dA, C, (N, K) in zip(dws, dAs, Cs, shapes)])
+        torch.cuda.synchronize()
+        for i, (C, ref) in enumerate(zip(Cs, singles)):
+            got = C.cpu().numpy().astype(np.float64)
+            assert np.isfinite(got).all(), (rep, shapes[i])
+            assert (got == ref).all(), (rep, shapes[i], M)
+            if rep == 0 and shapes[i][0] * shapes[i][1] <= 5120 * 5120:
+                Ref(ws[i], As[i]).check(got, f"batched q4_k {shapes[i]} M={M}")
 
 
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
