@@ -46,6 +46,16 @@
 //   poisoned (2^7): its row group's C is then NaN, never a silently wrong
 //   sum.  With nx = 0 the partials are written with device-scope (sc1)
 //   stores, which reach the point of coherence of all XCDs' L2s.
+// * Counter-free exchange (XCD-local, library workspace): the partials go to
+//   slots that hold kSlotFree (a signaling NaN, never an arithmetic result)
+//   between launches.  The splits other than the last store their tile sums
+//   and are done; the row group's last split (s = S - 1) reads all S slots of
+//   each of its elements from the L2 until no word is free, adds them in
+//   split order (the same bits as the counted exchange and k_split_sum),
+//   writes C and frees the slots.  This drops the store acknowledgement and
+//   the counter's round trip from the exchange.  A slot still free after the
+//   bound (a protocol bug) makes the element NaN; a poisoned split's sums are
+//   NaN and so is the row group's C.
 #include <algorithm>
 #include <atomic>
 #include <map>
@@ -58,9 +68,19 @@
 #include "bf_lds.h"
 
 namespace bf {
+// A free partial slot word: a signaling NaN, which no arithmetic result is
+// (results that are NaN are quiet NaNs), so a written partial never looks free.
+constexpr unsigned kSlotFree = 0x7FA5A5A5u;
+
 namespace {
 __global__ void k_zero_u32(unsigned* p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// A new workspace: counters at zero, free partial slots (kSlotFree) after them.
+__global__ void k_init_workspace(unsigned* p, int nzero, int nfree) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nzero + nfree; i += gridDim.x * blockDim.x)
+        p[i] = i < nzero ? 0u : kSlotFree;
 }
 }  // namespace
 
@@ -98,14 +118,18 @@ int device_cus() {
 // The library's own workspaces, one per (device, stream): launches on one
 // stream are ordered, so they can share it.  hipStreamPerThread names a
 // different stream in every host thread, so it is keyed by the thread too.
-// Grown on demand: the old buffer is freed once the stream has finished with
-// it.  Never allocated while the stream is being captured into a graph (an
-// allocation cannot be captured): such a call fails with
+// Three regions: counters (kept zero between launches by the kernels that use
+// them), partial slots (kept free, every word kSlotFree, between launches by
+// the K-split exchange that uses them) and partials (no state between
+// launches).  Grown on demand: the old buffer is freed once the stream has
+// finished with it.  Never allocated while the stream is being captured into
+// a graph (an allocation cannot be captured): such a call fails with
 // hipErrorStreamCaptureUnsupported unless a large enough workspace exists.
-hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t pbytes, unsigned** counters, float** parts) {
+hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t sbytes, size_t pbytes, unsigned** counters,
+                             float** slots, float** parts) {
     struct Slot {
         uint8_t* p = nullptr;
-        size_t cb = 0, pb = 0;
+        size_t cb = 0, sb = 0, pb = 0;
     };
     static std::mutex mu;
     static std::map<std::tuple<int, uintptr_t, std::thread::id>, Slot> cache;
@@ -115,16 +139,16 @@ hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t pbytes, unsig
     const std::thread::id tid = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
     std::lock_guard<std::mutex> lock(mu);
     Slot& slot = cache[{dev, (uintptr_t)st, tid}];
-    if (!slot.p || slot.cb < cbytes || slot.pb < pbytes) {
+    if (!slot.p || slot.cb < cbytes || slot.sb < sbytes || slot.pb < pbytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         e = hipStreamIsCapturing(st, &cs);
         if (e != hipSuccess) return e;
         if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
-        const size_t cb = std::max(cbytes, slot.cb), pb = std::max(pbytes, slot.pb);
+        const size_t cb = std::max(cbytes, slot.cb), sb = std::max(sbytes, slot.sb), pb = std::max(pbytes, slot.pb);
         uint8_t* p = nullptr;
-        e = hipMalloc((void**)&p, cb + pb);
+        e = hipMalloc((void**)&p, cb + sb + pb);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(k_zero_u32, dim3(64), dim3(256), 0, st, (unsigned*)p, (int)(cb / 4));
+        hipLaunchKernelGGL(k_init_workspace, dim3(256), dim3(256), 0, st, (unsigned*)p, (int)(cb / 4), (int)(sb / 4));
         e = hipGetLastError();
         if (e != hipSuccess) {
             (void)hipFree(p);
@@ -137,18 +161,28 @@ hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t pbytes, unsig
             e = hipFree(slot.p);
             if (e != hipSuccess) return e;
         }
-        slot = Slot{p, cb, pb};
+        slot = Slot{p, cb, sb, pb};
     }
     *counters = (unsigned*)slot.p;
-    *parts = (float*)(slot.p + slot.cb);
+    *slots = (float*)(slot.p + slot.cb);
+    *parts = (float*)(slot.p + slot.cb + slot.sb);
     return hipSuccess;
 }
 
 // Counters and partials for one launch: carved out of the caller's scratch
 // (bytes == 0: none given) or the library's workspace for the stream.
+// Free partial slots for one launch of the counter-free exchange: only in the
+// library's workspace for the stream (a caller's scratch has no slot region).
+hipError_t slot_workspace(hipStream_t st, size_t sbytes, float** slots) {
+    unsigned* counters = nullptr;
+    float* parts = nullptr;
+    return library_workspace(st, 0, sbytes, 0, &counters, slots, &parts);
+}
+
 hipError_t split_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes, size_t pbytes,
                             unsigned** counters, float** parts) {
-    if (!scratch) return library_workspace(st, cbytes, pbytes, counters, parts);
+    float* slots = nullptr;
+    if (!scratch) return library_workspace(st, cbytes, 0, pbytes, counters, &slots, parts);
     if (cbytes + pbytes > scratch->bytes) return hipErrorInvalidValue;
     *counters = (unsigned*)scratch->base;
     *parts = (float*)(scratch->base + cbytes);
@@ -199,7 +233,7 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
                                            const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nt,
                                            int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux,
                                            void* __restrict__ C, int ldc, int out_f16, float* __restrict__ ws,
-                                           unsigned* __restrict__ counters, int nx) {
+                                           unsigned* __restrict__ counters, int nx, int slots) {
     constexpr int NC = kSpNC, NL = kSpNL;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -352,10 +386,70 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
                 }
         }
         if (SUM2) return;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if (lane == 0) asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[1])), "v"(1) : "memory");
+        if (!slots) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (lane == 0) asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[1])), "v"(1) : "memory");
+        }
     }
     if (SUM2 || S == 1) return;
+
+    if (slots) {
+        // --------------------------------------- counter-free exchange (slots)
+        // The row group's last split reads every split's slots (its own too)
+        // until no word is free, adds them in split order, writes C and frees
+        // the slots for the next launch; the other splits are done.
+        if (s != S - 1) return;
+        const int rows = nt * 16, nq = rows * (Mp / 4);
+        const int64_t n0 = (int64_t)rg * rows;
+        const __amdgpu_buffer_rsrc_t wr = workspace_rsrc(ws, S, N, Mp);
+        const int sstride = N * Mp * 4;                  // bytes between two splits' slots
+        const u4 freev = u4{kSlotFree, kSlotFree, kSlotFree, kSlotFree};
+        bool late = false;                               // a slot stayed free past the bound
+        for (int b = c * 64; b < nq; b += NC * 64) {
+            const int v = b + lane;
+            const int nl = v / (Mp / 4), m4 = 4 * (v - nl * (Mp / 4));
+            const bool ok = v < nq && n0 + nl < N;
+            const int off = ok ? (int)(((n0 + nl) * Mp + m4) * 4) : 0;
+            f4 sum = f4{0.f, 0.f, 0.f, 0.f};
+            for (int s0 = 0; s0 < S && !late; s0 += 4) {
+                u4 x[4];
+                for (int it = 0;; it++) {
+                    bool miss = false;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        x[k] = ok && s0 + k < S ? __builtin_amdgcn_raw_buffer_load_b128(wr, off + (s0 + k) * sstride, 0,
+                                                                                          kCoherent)
+                                                : u4{0u, 0u, 0u, 0u};
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const u4 w = x[k];
+                        miss = miss || w[0] == kSlotFree || w[1] == kSlotFree || w[2] == kSlotFree || w[3] == kSlotFree;
+                    }
+                    if (__builtin_amdgcn_ballot_w64(miss) == 0) break;
+                    if (it == kDeviceWaitBound) {
+                        late = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (s0 + k < S) sum += __builtin_bit_cast(f4, x[k]);      // splits in order
+            }
+            if (!ok) continue;
+            for (int k = 0; k < S; k++) __builtin_amdgcn_raw_buffer_store_b128(freev, wr, off + k * sstride, 0, 0);
+            const bool bad = late || poisoned(flags + kSpPoison);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (m4 + i >= M) break;
+                const float y = bad ? __builtin_nanf("") : sum[i];
+                if (out_f16) ((_Float16*)C)[(int64_t)(m4 + i) * ldc + n0 + nl] = (_Float16)y;
+                else ((float*)C)[(int64_t)(m4 + i) * ldc + n0 + nl] = y;
+            }
+        }
+        return;
+    }
 
     // --------------------------------------------------------- cross-split sum
     if (c == 0) {
@@ -434,10 +528,11 @@ template <int QT, int MT, bool SUM2>
 __global__ __launch_bounds__(64 * (kSpNC + kSpNL))
 void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
                   int nt, int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C,
-                  int ldc, int out_f16, float* __restrict__ ws, unsigned* __restrict__ counters, int nx) {
+                  int ldc, int out_f16, float* __restrict__ ws, unsigned* __restrict__ counters, int nx,
+                  int slots) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     split_body<QT, MT, SUM2>((int)blockIdx.x, lds, W, A, lda, M, N, K, nt, S, nsgS, unit_bytes, Waux, C, ldc, out_f16,
-                             ws, counters, nx);
+                             ws, counters, nx, slots);
 }
 
 // C of a single K-split launch: the S partials [s][n][Mp] of each element
@@ -485,6 +580,7 @@ struct SplitJob {
 struct SplitJobs {
     SplitJob job[kSpMaxJobs];
     int n, out_f16, nx;                  // nx: XCD-local exchange (every job's grid0 a multiple of nx)
+    int slots;                           // counter-free exchange through free slots
 };
 
 template <int QT, int MT>
@@ -498,7 +594,7 @@ void k_gemm_split_batched(const SplitJobs jobs) {
     for (int i = 1; i < kSpMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
     split_body<QT, MT, false>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nt, j.S, j.nsgS,
-                       j.unit_bytes, j.Waux, j.C, j.ldc, jobs.out_f16, j.ws, j.counters, jobs.nx);
+                       j.unit_bytes, j.Waux, j.C, j.ldc, jobs.out_f16, j.ws, j.counters, jobs.nx, jobs.slots);
 }
 
 
@@ -565,6 +661,11 @@ bool split_sum2(const SplitPlan& p) {
     return p.S > 1 && p.grid > (cus > 0 ? cus : 256);
 }
 
+// The in-kernel exchange goes through free slots (no counter round trip) where
+// the splits of a row group share an XCD's L2 and the library's workspace is
+// used; with a caller's scratch (no slot region) it counts arrivals.
+bool use_slots(const SplitPlan& p, const Scratch* scratch) { return !scratch && p.nx > 0 && p.S > 1; }
+
 template <int QT, int MT, bool SUM2>
 hipError_t launch_split_k(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
     auto k = k_gemm_split<QT, MT, SUM2>;
@@ -580,13 +681,15 @@ hipError_t launch_split_k(const GemmArgs& g, const SplitPlan& p, const Scratch* 
     }
     unsigned* counters = nullptr;
     float* parts = nullptr;
+    const int slots = use_slots(p, scratch) && !SUM2;
     if (p.S > 1) {
         // summed by k_split_sum: partials only, no counters
-        e = split_workspace(scratch, st, SUM2 ? 0 : counter_bytes(p), partial_bytes(g, p), &counters, &parts);
+        e = slots ? slot_workspace(st, partial_bytes(g, p), &parts)
+                  : split_workspace(scratch, st, SUM2 ? 0 : counter_bytes(p), partial_bytes(g, p), &counters, &parts);
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kSpNC + kSpNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K,
-                       p.nt, p.S, p.nsgS, p.unit_bytes, g.Waux, g.C, g.ldc, g.out_f16, parts, counters, p.nx);
+                       p.nt, p.S, p.nsgS, p.unit_bytes, g.Waux, g.C, g.ldc, g.out_f16, parts, counters, p.nx, slots);
     e = hipGetLastError();
     if (e != hipSuccess || !SUM2) return e;
     hipLaunchKernelGGL(k_split_sum, dim3((g.N + 31) / 32), dim3(256), 0, st, (const float*)parts, g.C, g.ldc,
@@ -631,14 +734,16 @@ hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, 
     }
     unsigned* counters = nullptr;
     float* parts = nullptr;
+    const bool slots = !scratch && nx > 0;
     if (ctot) {
-        e = split_workspace(scratch, st, ctot, ptot, &counters, &parts);
+        e = slots ? slot_workspace(st, ptot, &parts) : split_workspace(scratch, st, ctot, ptot, &counters, &parts);
         if (e != hipSuccess) return e;
     }
     SplitJobs jobs = {};
     jobs.n = n;
     jobs.out_f16 = gs[0].out_f16;
     jobs.nx = nx;
+    jobs.slots = slots;
     int grid = 0, lds = 0;
     size_t co = 0, po = 0;
     for (int i = 0; i < n; i++) {
@@ -646,7 +751,7 @@ hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, 
         const SplitPlan& p = ps[i];
         jobs.job[i] = SplitJob{g.W, g.Waux, g.A, g.C,
                                p.S > 1 ? (float*)((uint8_t*)parts + po) : nullptr,
-                               p.S > 1 ? (unsigned*)((uint8_t*)counters + co) : nullptr,
+                               p.S > 1 && !slots ? (unsigned*)((uint8_t*)counters + co) : nullptr,
                                g.lda, g.ldc, g.M, g.N, g.K, p.nt, p.S, p.nsgS, p.unit_bytes, grid};
         co += cb[i];
         po += pb[i];
