@@ -2,9 +2,9 @@
 kernel stamps s_memrealtime (100 MHz) at fixed points into a device array,
 one row of 256 stamps per workgroup.
 
-    python bus-fill_amd/devtools/timeline.py build lds|dense     (CPU: patch and compile)
-    python bus-fill_amd/devtools/timeline.py run lds|dense N K M (GPU: 60 GEMMs over a 1 GB
-                                                                   rotation, the last one's stamps)
+    python bus-fill_amd/devtools/timeline.py build lds|dense|split     (CPU: patch and compile)
+    python bus-fill_amd/devtools/timeline.py run lds|dense|split N K M (GPU: 60 GEMMs over a 1 GB
+                                                                         rotation, the last one's stamps)
 
 `build` writes bus-fill_amd/devtools/_tl_<kernel>/ (libbusfill.so with the
 stamps and bf_tl_copy); `run` loads that copy instead of the product library
@@ -20,6 +20,12 @@ dense (k_gemm_dense):
     127 workgroup start; compute wave 0: u / 40 + u start / end of its wait for
     activation half-slab u, 128 + v / 168 + v for weight unit v; 80 + u / 208 + v
     activation / weight loader issuing unit u / v; 121 compute wave 0 done.
+split (k_gemm_split, one launch):
+    127 workgroup start; 64 + i: loader 0 issuing unit i; 125 loader 0's loads
+    landed; i / 32 + i: compute wave 0 starts / ends its wait for unit i; 120 the
+    last compute wave done with its units, 121 compute wave 0 done; 122 tile 0's
+    sums stored (issued); 123 the last split (reducer) starts reading the
+    partials, 124 its wave 0 has written its share of C.
 """
 from __future__ import annotations
 
@@ -84,6 +90,26 @@ PATCHES = {
         ("        t += s1 - s0;\n    }\n}\n\n// C for the row groups split",
          "        t += s1 - s0;\n    }\n    if (c == 0) TL(121);\n}\n\n// C for the row groups split"),
     ]),
+    "split": ("bf_gemm_split.hip", [
+        ("constexpr unsigned kSlotFree = 0x7FA5A5A5u;\n\nnamespace {\n",
+         "constexpr unsigned kSlotFree = 0x7FA5A5A5u;\n" + HEADER[len("namespace bf {\n"):]),
+        ("    const int sg0 = s * nsgS;\n", "    const int sg0 = s * nsgS;\n    if (wave == 0) TL(127);\n"),
+        ("            if (i == 0) clear_flags_and_meet();\n",
+         "            if (j == 0 && i < 32) TL(64 + i);\n            if (i == 0) clear_flags_and_meet();\n"),
+        ("        asm volatile(\"s_waitcnt vmcnt(0)\" ::: \"memory\");\n        return;\n    }\n",
+         "        asm volatile(\"s_waitcnt vmcnt(0)\" ::: \"memory\");\n        if (j == 0) TL(125);\n        return;\n    }\n"),
+        ("        wait_flags(flags + 16 + 4 * i, NL, lane, flags + kSpPoison);\n",
+         "        if (c == 0 && i < 32) TL(i);\n        wait_flags(flags + 16 + 4 * i, NL, lane, flags + kSpPoison);\n"
+         "        if (c == 0 && i < 32) TL(32 + i);\n"),
+        ("    // the tile's first wave adds the others' sums (in wave order) and writes the tile\n",
+         "    if (c == 0) TL(121);\n    if (c == NC - 1) TL(120);\n"
+         "    // the tile's first wave adds the others' sums (in wave order) and writes the tile\n"),
+        ("        if (SUM2) return;\n        if (!slots) {\n", "        if (c == 0) TL(122);\n        if (SUM2) return;\n        if (!slots) {\n"),
+        ("        if (s != S - 1) return;\n", "        if (s != S - 1) return;\n        if (c == 0) TL(123);\n"),
+        ("                else ((float*)C)[(int64_t)(m4 + i) * ldc + n0 + nl] = y;\n            }\n        }\n        return;\n",
+         "                else ((float*)C)[(int64_t)(m4 + i) * ldc + n0 + nl] = y;\n            }\n        }\n"
+         "        if (c == 0) TL(124);\n        return;\n"),
+    ]),
 }
 
 
@@ -142,7 +168,7 @@ def run(kernel: str, N: int, K: int, M: int) -> None:
     rot = Rotation("q4_k", N, K, 1_050_000_000, seed=11, dev=dev)
     A = torch.randn((M, K), device=dev).half()
     C = torch.empty((M, N), device=dev)
-    algo = bf.ALGO_DENSE if kernel == "dense" else bf.ALGO_LDS
+    algo = {"dense": bf.ALGO_DENSE, "split": bf.ALGO_SPLIT}.get(kernel, bf.ALGO_LDS)
     for i in range(60):
         bf.gemm(bf.Q4_K, rot.W[i % rot.count], None, A, C, M, N, K, algo=algo)
     torch.cuda.synchronize()
@@ -175,6 +201,23 @@ def run(kernel: str, N: int, K: int, M: int) -> None:
         ends = np.max(np.where(hu[:, 240:248] != 0, H[:, 240:248], 0), axis=1)
         print(f"workgroup end (last of sub-tiles 0-7 stored): median {np.median(ends):.2f} p90 {_pct(ends, 90):.2f} "
               f"max {ends.max():.2f}")
+    elif kernel == "split":
+        print("loader 0, unit i issued (median us):",
+              " ".join(f"{i}:{np.median(col(64 + i)):.2f}" for i in range(32) if (hu[:, 64 + i] != 0).any()))
+        print(" unit  wait start  wait end   (compute wave 0, medians us)")
+        for i in range(32):
+            if not (hu[:, i] != 0).any():
+                break
+            print(f"  {i:3d}  {np.median(col(i)):9.2f}  {np.median(col(32 + i)):8.2f}")
+        for k, what in ((125, "loader 0's loads landed"), (121, "compute wave 0 done"),
+                        (120, "last compute wave done"), (122, "tile 0 sums stored"),
+                        (123, "reducer starts reading"), (124, "reducer wave 0 wrote C")):
+            x = col(k)
+            if len(x):
+                print(f"{what:>26}: median {np.median(x):6.2f} p90 {_pct(x, 90):6.2f} max {x.max():6.2f} "
+                      f"({len(x)} workgroups)")
+        ends = np.max(np.where(hu[:, 120:126] != 0, H[:, 120:126], 0), axis=1)
+        print(f"workgroup end (last stamp): median {np.median(ends):.2f} p90 {_pct(ends, 90):.2f} max {ends.max():.2f}")
     else:
         d = col(121)
         print(f"compute done: median {np.median(d):.2f} p90 {_pct(d, 90):.2f} max {d.max():.2f}")
