@@ -49,7 +49,15 @@ HEADER = ("namespace bf {\n__device__ uint64_t g_tl[8192 * 256];\n"
           "#define TL(k) do { if (lane == 0 && blockIdx.x < 8192 && (k) < 256) "
           "g_tl[(size_t)blockIdx.x * 256 + (k)] = tl_now(); } while (0)\n")
 EXPORT = ('extern "C" int bf_tl_copy(void* host, size_t bytes) {\n'
-          '    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(bf::g_tl), bytes, 0, hipMemcpyDeviceToHost);\n}\n')
+          '    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(bf::g_tl), bytes, 0, hipMemcpyDeviceToHost);\n}\n'
+          # a one-wave kernel that stamps row 8191, column k: launched before and after
+          # a GEMM on the same stream, it brackets the GEMM's dispatch
+          'namespace bf {\n__global__ void k_tl_mark(int k) {\n'
+          '    const uint64_t t = tl_now();\n'
+          '    if (threadIdx.x == 0) g_tl[(size_t)8191 * 256 + k] = t;\n}\n}  // namespace bf\n'
+          'extern "C" int bf_tl_mark(int k) {\n'
+          '    hipLaunchKernelGGL(bf::k_tl_mark, dim3(1), dim3(64), 0, (hipStream_t)0, k);\n'
+          '    return (int)hipGetLastError();\n}\n')
 
 # (old, new) replacements, each of which must match exactly once
 PATCHES = {
@@ -65,8 +73,8 @@ PATCHES = {
         ("            wait_count(&flags[kSubCount + t_in], nsteps, flags + kPoison);\n",
          "            if (t_in < 8) TL(224 + t_in);\n            wait_count(&flags[kSubCount + t_in], nsteps, flags + kPoison);\n"
          "            if (t_in < 8) TL(232 + t_in);\n"),
-        ("                    else ((float*)C)[(int64_t)mt * ldc + row] = y;\n                }\n            }\n",
-         "                    else ((float*)C)[(int64_t)mt * ldc + row] = y;\n                }\n            }\n"
+        ("                if (g == 0 && kg == 0 && mt < M && row < N) store_c(mt, row, y);\n            }\n",
+         "                if (g == 0 && kg == 0 && mt < M && row < N) store_c(mt, row, y);\n            }\n"
          "            if (t_in < 8) TL(240 + t_in);\n"),
     ]),
     "dense": ("bf_gemm_dense.hip", [
@@ -87,8 +95,8 @@ PATCHES = {
         ("                    const uint32_t wb = lds0 + (uint32_t)(kDnFlags + (v % DW) * kDnWSlot);\n",
          "                    const uint32_t wb = lds0 + (uint32_t)(kDnFlags + (v % DW) * kDnWSlot);\n"
          "                    if (j == 0 && v < 40) TL(208 + v);\n"),
-        ("        t += s1 - s0;\n    }\n}\n\n// C for the row groups split",
-         "        t += s1 - s0;\n    }\n    if (c == 0) TL(121);\n}\n\n// C for the row groups split"),
+        ("        t += s1 - s0;\n    }\n}\n\n// One workgroup per CU",
+         "        t += s1 - s0;\n    }\n    if (c == 0) TL(121);\n}\n\n// One workgroup per CU"),
     ]),
     "split": ("bf_gemm_split.hip", [
         ("constexpr unsigned kSlotFree = 0x7FA5A5A5u;\n\nnamespace {\n",
@@ -171,10 +179,16 @@ def run(kernel: str, N: int, K: int, M: int) -> None:
     algo = {"dense": bf.ALGO_DENSE, "split": bf.ALGO_SPLIT}.get(kernel, bf.ALGO_LDS)
     for i in range(60):
         bf.gemm(bf.Q4_K, rot.W[i % rot.count], None, A, C, M, N, K, algo=algo)
+    # the last GEMM bracketed by two one-wave stamp kernels on the same stream
+    L.bf_tl_mark(0)
+    bf.gemm(bf.Q4_K, rot.W[60 % rot.count], None, A, C, M, N, K, algo=algo)
+    L.bf_tl_mark(1)
     torch.cuda.synchronize()
     h = np.zeros((8192, 256), np.uint64)
     if L.bf_tl_copy(h.ctypes.data, h.nbytes) != 0:
         raise SystemExit("bf_tl_copy failed")
+    marks = h[8191, :2].astype(np.int64)
+    h[8191, :] = 0
     used = h[:, 127] != 0
     hu = h[used]
     H = (hu.astype(np.int64) - int(hu[:, 127].min())) / 100.0
@@ -185,6 +199,12 @@ def run(kernel: str, N: int, K: int, M: int) -> None:
 
     print(f"{kernel} N={N} K={K} M={M}: {int(used.sum())} workgroups; starts median {np.median(H[:, 127]):.2f} "
           f"max {H[:, 127].max():.2f} us")
+    if marks.all():
+        last = int(hu[hu != 0].astype(np.int64).max())
+        t0 = int(hu[:, 127].min())
+        print(f"stamp kernel before -> first workgroup start: {(t0 - marks[0]) / 100.0:.2f} us; last stamp of the GEMM "
+              f"-> stamp kernel after: {(marks[1] - last) / 100.0:.2f} us; before -> after: "
+              f"{(marks[1] - marks[0]) / 100.0:.2f} us")
     if kernel == "lds":
         print("loader 0, step of group g issued (median us):",
               " ".join(f"{g}:{np.median(col(64 + g)):.2f}" for g in range(32) if (hu[:, 64 + g] != 0).any()))
