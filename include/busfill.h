@@ -16,7 +16,8 @@
  *     memory the library allocates itself is the workspace of its
  *     cross-workgroup exchanges: the K-split kernel's (BF_ALGO_SPLIT, which
  *     bf_gemm picks for 9-32 batch rows per launch when the activations do not
- *     fit in LDS) partial sums and row-group counters, and the dense kernel's
+ *     fit in LDS) partial sums (and row-group counters where the splits of a
+ *     row group cannot be kept on one XCD), and the dense kernel's
  *     (BF_ALGO_DENSE, above 32 rows, and from 9 or 17 rows on matrices of
  *     3 * 2^24 weights or more) partial sums, one workspace per (device, stream)
  *     -- per host thread for hipStreamPerThread -- allocated by the first such
