@@ -68,10 +68,6 @@
 #include "bf_lds.h"
 
 namespace bf {
-// A free partial slot word: a signaling NaN, which no arithmetic result is
-// (results that are NaN are quiet NaNs), so a written partial never looks free.
-constexpr unsigned kSlotFree = 0x7FA5A5A5u;
-
 namespace {
 __global__ void k_zero_u32(unsigned* p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
@@ -212,13 +208,6 @@ constexpr int kSpQS = 12;               // instruction slots per loader and unit
 constexpr int kSpMaxPieces = 64 * kSpNL * kSpQS;
 constexpr int kSpCounterStride = 64;    // one row-group counter per 256-byte line: no shared lines
 constexpr int kCoherent = 16;           // buffer access cache policy: sc1 (device scope: misses the L1)
-
-// The XCC (XCD) this wave runs on.
-__device__ __forceinline__ int xcc_id() {
-    int x;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-    return x & 0xF;
-}
 
 // Buffer resource over the split partials [S][N][Mp] (fp32).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t workspace_rsrc(float* ws, int S, int N, int Mp) {

@@ -161,6 +161,18 @@ __device__ __forceinline__ void wait_lanes(const int* flag, bool need, int* pois
     mark_poison(poison);
 }
 
+// A free partial slot word of the counter-free exchanges: a signaling NaN,
+// which no arithmetic result is (results that are NaN are quiet NaNs), so a
+// written partial never looks free.
+constexpr unsigned kSlotFree = 0x7FA5A5A5u;
+
+// The XCC (XCD) this wave runs on.
+__device__ __forceinline__ int xcc_id() {
+    int x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 0xF;
+}
+
 // Buffer access cache policy sc1: device scope.  Such a store is written
 // through the XCD's L2 to the point of coherence of all XCDs; such a load
 // misses the L1 and the XCD's L2 for lines another XCD may have written.

@@ -79,8 +79,9 @@ PATCHES = {
     ]),
     "dense": ("bf_gemm_dense.hip", [
         ("namespace bf {\nnamespace {\n", HEADER),
-        ("    const int t0 = range_first(p, T, G), t1 = range_first(p + 1, T, G);\n",
-         "    const int t0 = range_first(p, T, G), t1 = range_first(p + 1, T, G);\n    if (wave == 0) TL(127);\n"),
+        ("    const int nsg = K >> 8;\n    const int t0 = range_first(p, T, G), t1 = range_first(p + 1, T, G);\n",
+         "    const int nsg = K >> 8;\n    const int t0 = range_first(p, T, G), t1 = range_first(p + 1, T, G);\n"
+         "    if (wave == 0) TL(127);\n"),
         ("                wait_flags(flags + kDnAReady + kDnNLA * u, kDnNLA, lane, flags + kDnPoison);\n",
          "                if (c == 0 && u < 40) TL(u);\n"
          "                wait_flags(flags + kDnAReady + kDnNLA * u, kDnNLA, lane, flags + kDnPoison);\n"
@@ -99,8 +100,7 @@ PATCHES = {
          "        t += s1 - s0;\n    }\n    if (c == 0) TL(121);\n}\n\n// One workgroup per CU"),
     ]),
     "split": ("bf_gemm_split.hip", [
-        ("constexpr unsigned kSlotFree = 0x7FA5A5A5u;\n\nnamespace {\n",
-         "constexpr unsigned kSlotFree = 0x7FA5A5A5u;\n" + HEADER[len("namespace bf {\n"):]),
+        ("namespace bf {\nnamespace {\n", HEADER),
         ("    const int sg0 = s * nsgS;\n", "    const int sg0 = s * nsgS;\n    if (wave == 0) TL(127);\n"),
         ("            if (i == 0) clear_flags_and_meet();\n",
          "            if (j == 0 && i < 32) TL(64 + i);\n            if (i == 0) clear_flags_and_meet();\n"),
