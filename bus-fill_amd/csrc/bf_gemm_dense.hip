@@ -371,9 +371,18 @@ __device__ __forceinline__ void dense_sum_body(int rg, const float* __restrict__
     if (pf == pl || m >= M) return;
     const int Mp = (M + 3) & ~3, nl = 4 * ((int)threadIdx.x & 31);
     f4 s = f4{0.f, 0.f, 0.f, 0.f};
-    for (int q = pf; q <= pl; q++) {
-        const int slot = 2 * q + (range_first(q, T, G) >= rg * nsg ? 0 : 1);
-        s += *(const f4*)(ws + ((size_t)slot * Mp + m) * ROWS + nl);
+    // up to eight pieces' loads in flight before the first add (pieces in order)
+    for (int q0 = pf; q0 <= pl; q0 += 8) {
+        f4 x[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int q = q0 + k;
+            const int slot = 2 * q + (range_first(q, T, G) >= rg * nsg ? 0 : 1);
+            x[k] = q <= pl ? *(const f4*)(ws + ((size_t)slot * Mp + m) * ROWS + nl) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (q0 + k <= pl) s += x[k];
     }
     const int64_t n0 = (int64_t)rg * ROWS + nl, o = (int64_t)m * ldc + n0;
     if (((uintptr_t)C & 15) == 0 && (ldc & 3) == 0 && n0 + 3 < N) {

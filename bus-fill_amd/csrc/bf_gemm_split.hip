@@ -538,7 +538,17 @@ __global__ __launch_bounds__(256) void k_split_sum(const float* __restrict__ ws,
         const int nl = tid / (Mp / 4), m4 = 4 * (tid - nl * (Mp / 4));
         f4 s = f4{0.f, 0.f, 0.f, 0.f};
         if (n0 + nl < N)
-            for (int k = 0; k < S; k++) s += *(const f4*)(ws + ((size_t)k * N + n0 + nl) * Mp + m4);
+            // up to eight splits' loads in flight before the first add (splits in order)
+            for (int k0 = 0; k0 < S; k0 += 8) {
+                f4 x[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    x[k] = k0 + k < S ? *(const f4*)(ws + ((size_t)(k0 + k) * N + n0 + nl) * Mp + m4)
+                                      : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    if (k0 + k < S) s += x[k];
+            }
 #pragma unroll
         for (int i = 0; i < 4; i++) tr[(m4 + i) * 33 + nl] = s[i];
     }
