@@ -698,8 +698,14 @@ hipError_t launch_split_k(const GemmArgs& g, const SplitPlan& p, const Scratch* 
 
 template <int QT, int MT>
 hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
-    return split_sum2(p) ? launch_split_k<QT, MT, true>(g, p, scratch, st)
-                         : launch_split_k<QT, MT, false>(g, p, scratch, st);
+    // grids of more than one round but less than two: the counter-free
+    // exchange in the kernel where it is available (7168x5120 at M = 32, 448
+    // workgroups: 17.9 -> 17.1 us); from two full rounds on a second launch
+    // (17408x5120 at M = 16, 512 workgroups: 23.1 against 23.8-24.3 us in
+    // the kernel)
+    const int cus = device_cus() > 0 ? device_cus() : 256;
+    const bool sum2 = split_sum2(p) && (!use_slots(p, scratch) || p.grid >= 2 * cus);
+    return sum2 ? launch_split_k<QT, MT, true>(g, p, scratch, st) : launch_split_k<QT, MT, false>(g, p, scratch, st);
 }
 
 template <int QT>
