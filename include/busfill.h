@@ -29,7 +29,10 @@
  *     (bf_ffn_swiglu_ex, BF_FFN_ONE_LAUNCH) keeps its hand-over words in the
  *     same workspace.  A captured graph holds the workspace of
  *     the stream it was captured on: replaying it while other exchanging work
- *     runs on that stream (or another replay of it) races.
+ *     runs on that stream (or another replay of it) races, and a later call
+ *     on the stream that grows the workspace frees the buffer the graph
+ *     refers to -- capture after the stream has run its largest shape, or
+ *     use bf_gemm_noalloc in graphs.
  *   - fp16 values travel as uint16_t bit patterns.
  *   - A is [M][lda] row-major fp16, C is [M][ldc] row-major (fp32 or fp16),
  *     W is [N][K] in the chosen block format: C = A . dequant(W)^T.
