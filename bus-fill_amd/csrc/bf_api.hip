@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <vector>
 
 #include "bf_device.h"
@@ -306,12 +307,13 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
     }
     // The GEMMs are grouped by the kernel bf_gemm would launch for each (its
     // results are then the same bits) and every group of two or more shares
-    // launches: the LDS-staged kernel at batch 1-8 (one kernel shape), the
-    // K-split kernel at 9-32 rows, the dense kernel (one batch size); the
-    // rest, and any group its batched launch does not serve, run one by one.
+    // launches: the LDS-staged kernel at batch 1-8 (one batch size, so one
+    // kernel shape), the K-split kernel at 9-32 rows (one m-tile count), the
+    // dense kernel (one batch size); the rest, and any group its batched
+    // launch does not serve, run one by one.
     hipStream_t hs = (hipStream_t)stream;
     std::vector<bf::GemmArgs> gs(count);
-    std::vector<int> grp[3];                           // LDS, K-split, dense
+    std::map<std::pair<int, int>, std::vector<int>> grp;   // (0 LDS / 1 K-split / 2 dense, batch key)
     std::vector<int> single;
     for (int i = 0; i < count; i++) {
         const bf_gemm_desc& d = descs[i];
@@ -328,20 +330,21 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
         g.N = d.N;
         g.K = d.K;
         const bf_algo a = one_launch_algo(g);
-        if (a == BF_ALGO_LDS) grp[0].push_back(i);
-        else if (a == BF_ALGO_SPLIT) grp[1].push_back(i);
-        else if (a == BF_ALGO_DENSE) grp[2].push_back(i);
+        if (a == BF_ALGO_LDS) grp[{0, g.M}].push_back(i);
+        else if (a == BF_ALGO_SPLIT) grp[{1, g.M <= 16}].push_back(i);
+        else if (a == BF_ALGO_DENSE) grp[{2, g.M}].push_back(i);
         else single.push_back(i);
     }
-    for (int k = 0; k < 3; k++) {
+    for (const auto& kv : grp) {
+        const int k = kv.first.first;
         std::vector<bf::GemmArgs> sub;
-        for (int i : grp[k]) sub.push_back(gs[i]);
+        for (int i : kv.second) sub.push_back(gs[i]);
         const int n = (int)sub.size();
         const bool ok = n > 1 && (k == 0   ? bf::lds_batched_supports(sub.data(), n)
                                   : k == 1 ? bf::split_batched_supports(sub.data(), n)
                                            : bf::dense_batched_supports(sub.data(), n));
         if (!ok) {
-            single.insert(single.end(), grp[k].begin(), grp[k].end());
+            single.insert(single.end(), kv.second.begin(), kv.second.end());
             continue;
         }
         const bf_status st = k == 0   ? from_hip(bf::gemm_lds_batched(sub.data(), n, hs), "batched launch")

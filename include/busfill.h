@@ -154,11 +154,11 @@ typedef struct {
  * with the results of calling bf_gemm for each (bit-identical).  No GEMM's
  * output may overlap another one's inputs or output: they may run
  * concurrently.  The GEMMs are grouped by the kernel bf_gemm would give each:
- * those on the LDS-staged kernel (batch 1-8, one kernel shape), those on the
- * K-split kernel (9-32 rows whose activations do not fit in LDS) and those on
- * the dense kernel (one batch size, above 32 rows or from 9 rows on large
- * matrices) each share one launch per eight GEMMs (the dense ones one sum
- * launch too), so one GEMM's tail overlaps the next one's weight stream and
+ * those on the LDS-staged kernel (batch 1-8, per batch size), those on the
+ * K-split kernel (9-32 rows whose activations do not fit in LDS; 9-16 and
+ * 17-32 rows apart) and those on the dense kernel (above 32 rows or from 9
+ * rows on large matrices, per batch size) each share one launch per eight
+ * GEMMs (the dense ones one sum launch too), so one GEMM's tail overlaps the next one's weight stream and
  * launch gaps go away (a decoder layer's linears); any other GEMM runs as one
  * bf_gemm call.  No counterpart in the reference, whose only entry point is
  * the single-GEMM kernel (kernels/busfill_v1a.cu:41-46). */

@@ -560,6 +560,27 @@ def test_batched_groups_by_kernel(dev, M, shapes):
                 Ref(ws[i], As[i]).check(got, f"batched q4_k {shapes[i]} M={M}")
 
 
+def test_batched_mixed_batch_sizes(dev):
+    """One bf_gemm_batched call holding GEMMs of several batch sizes: each
+    kernel's group is split by batch size (dense at 32 and 64 rows, the
+    LDS-staged kernel at 1 row, the K-split kernel at 16 rows), and every
+    output is bit-identical to its own bf_gemm call."""
+    descs = [(17408, 5120, 32), (5120, 17408, 32), (17408, 5120, 64), (5120, 17408, 64),
+             (5120, 5120, 1), (7168, 5120, 1), (5120, 5120, 16), (7168, 5120, 16), (2048, 1024, 3)]
+    ws = [O.gen_weights(O.Q4_K, N, K, seed=N + K + M) for N, K, M in descs]
+    dws = [upload(w, dev) for w in ws]
+    As = [O.gen_act(M, K, seed=7 * i + M) for i, (N, K, M) in enumerate(descs)]
+    dAs = [to_dev(A, dev) for A in As]
+    singles = [gpu_gemm(w, A, dev, dw=dw) for w, A, dw in zip(ws, As, dws)]
+    Cs = [torch.full((M, N), float("nan"), device=dev) for N, K, M in descs]
+    bf.gemm_batched(O.Q4_K, [(dw[0], dw[1], dA, C, M, N, K) for dw, dA, C, (N, K, M) in zip(dws, dAs, Cs, descs)])
+    torch.cuda.synchronize()
+    for C, ref, d in zip(Cs, singles, descs):
+        got = C.cpu().numpy().astype(np.float64)
+        assert np.isfinite(got).all(), d
+        assert (got == ref).all(), d
+
+
 @pytest.mark.parametrize("qt", QTS, ids=lambda q: QT_NAME[q])
 def test_full_size_exact_properties(dev, qt):
     """Size-independent checks at the benchmark shape: scaling A by 2 is exact
