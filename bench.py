@@ -7,7 +7,9 @@ matrices already resident in HBM (72 matrices of 14.7 MB at 5120^2, so the
 256 MB Infinity Cache cannot serve them): one GEMM per matrix.  Timing is
 hipEvents recorded on the launch stream around exactly --steps passes (after
 --warmup untimed ones); the timed GEMMs continue the rotation where the warmup
-stopped, so no timed GEMM finds its matrix in a cache.  The GEMMs are issued
+stopped, so no timed GEMM finds its matrix in a cache.  Before a rotation's
+first timed configuration, about 0.1 s of untimed passes let the GPU's clocks
+settle under load (`preheat_s` in the record).  The GEMMs are issued
 back to back by the C++ bench host (bus-fill_amd/host/bench_host.hip) through
 the libbusfill C-ABI.
 
@@ -154,6 +156,19 @@ def time_gemm(L, rot, M, steps, warmup, graph, algo, dev, seed=7):
     return ms.value
 
 
+PREHEAT_S = 0.1   # untimed work before a workload's first timed configuration
+
+
+def preheat(L, rot, M, args, dev):
+    """About PREHEAT_S seconds of untimed passes of the first configuration
+    before anything of a rotation is timed: the GPU raises its clocks under
+    sustained load, and without this the first configuration timed in a run
+    measured 2-7 % slower than the same configuration timed later in it."""
+    ms = time_gemm(L, rot, M, 1, 0, 0, args.algo_id, dev)
+    passes = max(1, min(2000, int(math.ceil(PREHEAT_S * 1e3 / max(ms, 1e-3)))))
+    time_gemm(L, rot, M, passes, 0, 0, args.algo_id, dev)
+
+
 def gemm_record(rot, M, ms, steps, graph):
     """Per-GEMM figures from ms for `steps` passes over the rotation."""
     t = ms / 1e3 / (steps * rot.count)
@@ -278,6 +293,7 @@ def traffic_from_profiles(key):
 def run_gemm_workload(L, fmt, N, K, batches, args, dev):
     rot = Rotation(fmt, N, K, ROTATION_BYTES, seed=11, dev=dev)
     log(f"[bench] {fmt} N={N} K={K}: {rot.count} matrices, {rot.total_bytes / 1e9:.3f} GB rotation")
+    preheat(L, rot, batches[0], args, dev)
     recs = []
     for M in batches:
         for graph in ((0, 1) if args.graph == "both" else (int(args.graph),)):
@@ -497,7 +513,9 @@ def run_sweep(L, args, dev):
     shapes = [tuple(int(v) for v in s.split("x")) for s in (args.shapes or SWEEP_SHAPES).split(",")]
     for (N, K) in shapes:
         rot = Rotation("q4_k", N, K, ROTATION_BYTES, seed=N, dev=dev)
-        for M in [int(x) for x in (args.batches or SWEEP_BATCHES).split(",")]:
+        batches = [int(x) for x in (args.batches or SWEEP_BATCHES).split(",")]
+        preheat(L, rot, batches[0], args, dev)
+        for M in batches:
             ms = time_gemm(L, rot, M, args.steps, args.warmup, int(args.graph == "1"), args.algo_id, dev)
             r = gemm_record(rot, M, ms, args.steps, args.graph == "1")
             r.update({"N": N, "K": K})
@@ -555,6 +573,7 @@ def main():
             "metric": METRIC if fmt == "q4_k" else METRIC.replace("Q4_K", fmt.upper()),
             "value": head["weight_GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": head["ms_per_pass"],
+            "preheat_s": PREHEAT_S,
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
             "data": "synthetic",
             "config": {"workload": f"{fmt} GEMM N=K=5120, batch M={head['M']} (per_batch: M={batches})",
