@@ -57,8 +57,21 @@ def log(*a):
 
 
 # ------------------------------------------------------------------ device data
+def row_layout(fmt, N, K):
+    """Bytes of one matrix's row of the rotation buffer, and where its parts
+    lie in it: (row bytes, W offset, W bytes, aux offset, aux bytes).  Every
+    format keeps a whole matrix in one row, so a read of one matrix's bytes
+    from its row start never leaves the row (the planes layout holds the code
+    plane Wq[N][K/2] and then the scale plane Ws[N][K/32])."""
+    wbytes = N * K * 9 // 16
+    if fmt == "planes":
+        return wbytes, 0, N * K // 2, N * K // 2, N * K // 16
+    return wbytes, 0, wbytes, None, 0
+
+
 class Rotation:
-    """`count` distinct N x K matrices of one format in one device allocation."""
+    """`count` distinct N x K matrices of one format in one device allocation,
+    one matrix per row (row_layout)."""
 
     def __init__(self, fmt, N, K, min_bytes, seed, dev, scales=None, count=None):
         import torch
@@ -69,9 +82,12 @@ class Rotation:
         g.manual_seed(seed)
         lo, hi = scales or SCALE_RANGE[fmt]
         if fmt == "planes":
-            self.W = torch.randint(0, 256, (self.count, N * K // 2), dtype=torch.uint8, device=dev, generator=g)
-            d = torch.rand((self.count, N * K // 32), device=dev, generator=g) * (hi - lo) + lo
-            self.aux = d.half().contiguous()
+            row, w0, wn, a0, an = row_layout(fmt, N, K)
+            self.buf = torch.randint(0, 256, (self.count, row), dtype=torch.uint8, device=dev, generator=g)
+            self.W = self.buf[:, w0:w0 + wn]
+            d = torch.rand((self.count, an // 2), device=dev, generator=g) * (hi - lo) + lo
+            self.aux = self.buf[:, a0:a0 + an].view(torch.float16)
+            self.aux.copy_(d.half())
         else:
             blk = 144 if fmt == "q4_k" else 18
             nblk = N * K // (256 if fmt == "q4_k" else 32)
@@ -81,7 +97,9 @@ class Rotation:
             d = (torch.rand((self.count * nblk, nd), device=dev, generator=g) * (hi - lo) + lo).half()
             v[:, 0:2 * nd] = d.view(torch.uint8).view(self.count * nblk, 2 * nd)
             self.aux = None
+            self.buf = self.W
         torch.cuda.synchronize()
+        assert self.buf.shape == (self.count, self.wbytes) and self.buf.is_contiguous()
 
     @property
     def total_bytes(self):
@@ -188,10 +206,10 @@ def gemm_record(rot, M, ms, steps, graph):
 
 def read_peak(L, rot):
     import torch
-    sink = torch.zeros(1, dtype=torch.int32, device=rot.W.device)
+    sink = torch.zeros(1, dtype=torch.int32, device=rot.buf.device)
     ms = ctypes.c_double()
-    nbytes = rot.W.numel()
-    rc = L.bfb_read_peak(rot.W.data_ptr(), nbytes, 5, sink.data_ptr(), stream_handle(), ctypes.byref(ms))
+    nbytes = rot.buf.numel()
+    rc = L.bfb_read_peak(rot.buf.data_ptr(), nbytes, 5, sink.data_ptr(), stream_handle(), ctypes.byref(ms))
     if rc != 0:
         raise RuntimeError("bench host: " + L.bfb_last_error().decode())
     return 5 * nbytes / (ms.value / 1e3) / 1e9
@@ -205,12 +223,14 @@ def read_floor(L, rot, steps, warmup):
     the rotation like the GEMM: the time a launch of that size needs to read
     its bytes with no other work (best of a few grid shapes)."""
     import torch
-    sink = torch.zeros(1, dtype=torch.int32, device=rot.W.device)
-    W, _ = rot.ptr_arrays()
+    sink = torch.zeros(1, dtype=torch.int32, device=rot.buf.device)
+    rows = (ctypes.c_void_p * rot.count)(*[rot.buf[i].data_ptr() for i in range(rot.count)])
+    nbytes = rot.wbytes // 16 * 16
+    assert nbytes <= rot.buf.shape[1], "the read of one matrix must stay inside its row"
     best_us, best_grid = None, None
     for blocks, threads in READ_GRIDS:
         ms = ctypes.c_double()
-        rc = L.bfb_read_slices(P(W), rot.count, rot.wbytes // 16 * 16, blocks, threads, warmup * rot.count,
+        rc = L.bfb_read_slices(P(rows), rot.count, nbytes, blocks, threads, warmup * rot.count,
                                steps * rot.count, sink.data_ptr(), stream_handle(), ctypes.byref(ms))
         if rc != 0:
             raise RuntimeError("bench host: " + L.bfb_last_error().decode())
@@ -526,6 +546,61 @@ def run_sweep(L, args, dev):
     return res
 
 
+# ------------------------------------------------------------------ kernel traces
+def kernel_key(name):
+    """A dispatch's kernel name without its argument list (template arguments
+    kept): the text before the parenthesis that matches the final one."""
+    name = name.strip()
+    if name.startswith("void "):
+        name = name[5:]
+    if not name.endswith(")"):
+        return name
+    depth = 0
+    for i in range(len(name) - 1, -1, -1):
+        depth += {")": 1, "(": -1}.get(name[i], 0)
+        if depth == 0:
+            return name[:i]
+    return name
+
+
+def trace_summary(path, per_pass, labels):
+    """Per-launch kernel durations from a `rocprofv3 --kernel-trace` CSV.
+
+    The library's dispatches (kernel names in namespace bf) are taken in start
+    order and grouped into runs of consecutive dispatches of one kernel; each
+    run is cut into passes of `per_pass` dispatches (one pass over the weight
+    rotation).  For each run: the mean and median dispatch duration (end -
+    start of each dispatch), and over its passes the median and minimum of
+    (last end - first start) / per_pass, the time per launch with the gaps
+    between launches included -- the figure comparable to HIP events around
+    back-to-back launches.  `labels` names the runs in order."""
+    import csv
+    import statistics as st
+    rows = [r for r in csv.DictReader(open(path)) if "bf::" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    runs = []
+    for r in rows:
+        k = kernel_key(r["Kernel_Name"])
+        if runs and runs[-1][0] == k:
+            runs[-1][1].append(r)
+        else:
+            runs.append((k, [r]))
+    runs = [(k, rs) for k, rs in runs if len(rs) >= per_pass]
+    out = {}
+    for i, (k, rs) in enumerate(runs):
+        d = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rs]
+        spans = [(int(rs[j + per_pass - 1]["End_Timestamp"]) - int(rs[j]["Start_Timestamp"])) / per_pass
+                 for j in range(0, len(rs) - per_pass + 1, per_pass)]
+        gaps = [int(b["Start_Timestamp"]) - int(a["End_Timestamp"]) for a, b in zip(rs, rs[1:])]
+        label = labels[i] if i < len(labels) else f"run{i}"
+        out[label] = {"kernel": k, "dispatches": len(rs), "passes": len(spans), "per_pass": per_pass,
+                      "us_dispatch_mean": round(st.mean(d) / 1e3, 4), "us_dispatch_median": round(st.median(d) / 1e3, 4),
+                      "us_span_per_launch_median": round(st.median(spans) / 1e3, 4),
+                      "us_span_per_launch_min": round(min(spans) / 1e3, 4),
+                      "us_gap_median": round(st.median(gaps) / 1e3, 4) if gaps else 0.0}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -548,7 +623,21 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--out", default=None, help="also write the full record to this JSON file")
+    ap.add_argument("--trace-summary", default=None, metavar="CSV",
+                    help="no GPU work: summarize a rocprofv3 kernel-trace CSV of an earlier bench run "
+                         "(per-launch durations per run of one kernel) as one JSON line")
+    ap.add_argument("--trace-labels", default="q4_k_5120_m1,q4_k_5120_m8,q4_k_5120_m32",
+                    help="--trace-summary: names of the runs, in order")
+    ap.add_argument("--trace-pass", type=int, default=72, help="--trace-summary: dispatches per pass")
     args = ap.parse_args()
+    if args.trace_summary:
+        rec = trace_summary(args.trace_summary, args.trace_pass, args.trace_labels.split(","))
+        line = json.dumps(rec)
+        if args.out:
+            with open(args.out, "w") as f:
+                f.write(line + "\n")
+        print(line, flush=True)
+        return
     args.algo_id = {"auto": 0, "mfma": 1, "dot2": 2, "simple": 3, "lds": 4, "slab": 5, "split": 6,
                     "dense": 7}[args.algo]
 

@@ -31,7 +31,9 @@ FFN_AUTO, FFN_ONE_LAUNCH, FFN_TWO_LAUNCHES, FFN_CALLS = 0, 1, 2, 3
 # bf_algo
 ALGO_AUTO, ALGO_MFMA, ALGO_DOT2, ALGO_SIMPLE, ALGO_LDS, ALGO_SLAB, ALGO_SPLIT, ALGO_DENSE = 0, 1, 2, 3, 4, 5, 6, 7
 
-EXPORTS = ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_noalloc", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
+EXPORTS = ("bf_busfill_q4", "bf_busfill_q4_ws", "bf_gemm", "bf_gemm_ex", "bf_gemm_noalloc", "bf_gemm_ws",
+           "bf_gemm_workspace_bytes", "bf_gemm_batched", "bf_gemm_batched_ws", "bf_gemm_batched_workspace_bytes",
+           "bf_dequant_f16", "bf_gemm_swiglu",
            "bf_swiglu_f16", "bf_ffn_swiglu", "bf_ffn_swiglu_ex", "bf_q8_bytes", "bf_quantize_q8", "bf_gemm_q8",
            "bf_gguf_open", "bf_gguf_close", "bf_gguf_tensor_count", "bf_gguf_tensor_at", "bf_gguf_find",
            "bf_gguf_get_u64", "bf_gguf_get_str", "bf_gguf_upload",
@@ -83,8 +85,16 @@ def lib() -> ctypes.CDLL:
         L.bf_gemm.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
         L.bf_gemm_ex.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, i, vp]
         L.bf_gemm_noalloc.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
+        sz = ctypes.c_size_t
+        L.bf_busfill_q4_ws.argtypes = [vp, vp, vp, vp, i, i, i, vp, sz, vp]
+        L.bf_gemm_ws.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp, sz, vp]
+        L.bf_gemm_workspace_bytes.argtypes = [i, i, i, i, i]
+        L.bf_gemm_workspace_bytes.restype = sz
         L.bf_dequant_f16.argtypes = [i, vp, vp, vp, i, i, vp]
         L.bf_gemm_batched.argtypes = [i, i, i, ctypes.POINTER(GemmDesc), vp]
+        L.bf_gemm_batched_ws.argtypes = [i, i, i, ctypes.POINTER(GemmDesc), vp, sz, vp]
+        L.bf_gemm_batched_workspace_bytes.argtypes = [i, i, i, ctypes.POINTER(GemmDesc)]
+        L.bf_gemm_batched_workspace_bytes.restype = sz
         L.bf_gemm_swiglu.argtypes = [i, vp, vp, vp, i, vp, i, i, i, i, i, vp]
         L.bf_swiglu_f16.argtypes = [vp, i, vp, i, i, i, vp]
         L.bf_ffn_swiglu.argtypes = [i, QWeights, QWeights, QWeights, vp, i, vp, i, vp, i, i, i, i, i, i, vp]
@@ -107,7 +117,8 @@ def lib() -> ctypes.CDLL:
         for f in ("bf_gguf_open", "bf_gguf_tensor_at", "bf_gguf_find", "bf_gguf_get_u64", "bf_gguf_get_str",
                   "bf_gguf_upload"):
             getattr(L, f).restype = i
-        for f in ("bf_busfill_q4", "bf_gemm", "bf_gemm_ex", "bf_gemm_noalloc", "bf_gemm_batched", "bf_dequant_f16", "bf_gemm_swiglu",
+        for f in ("bf_busfill_q4", "bf_busfill_q4_ws", "bf_gemm", "bf_gemm_ex", "bf_gemm_noalloc", "bf_gemm_ws",
+                  "bf_gemm_batched", "bf_gemm_batched_ws", "bf_dequant_f16", "bf_gemm_swiglu",
                   "bf_swiglu_f16", "bf_ffn_swiglu", "bf_ffn_swiglu_ex", "bf_quantize_q8", "bf_gemm_q8"):
             getattr(L, f).restype = i
         L.bf_status_str.argtypes = [i]
@@ -160,6 +171,22 @@ def gemm_noalloc(qtype: int, W, W_aux, A, C, M: int, N: int, K: int, *, lda: int
     _check(st, "bf_gemm_noalloc")
 
 
+def gemm_workspace_bytes(qtype: int, M: int, N: int, K: int, *, otype: int = OUT_F32) -> int:
+    """Bytes of caller-owned workspace gemm_ws needs for this shape (0: none)."""
+    return int(lib().bf_gemm_workspace_bytes(qtype, otype, M, N, K))
+
+
+def gemm_ws(qtype: int, W, W_aux, A, C, M: int, N: int, K: int, workspace, workspace_bytes: int, *,
+            lda: int | None = None, ldc: int | None = None, otype: int = OUT_F32, stream=None) -> None:
+    """bf_gemm_ws: bf_gemm with a caller-owned workspace (a device tensor or
+    address of workspace_bytes, 256-byte aligned; None with 0 bytes when the
+    call needs none)."""
+    st = lib().bf_gemm_ws(qtype, _ptr(W), _ptr(W_aux), _ptr(A), K if lda is None else lda, _ptr(C),
+                          N if ldc is None else ldc, otype, M, N, K, _ptr(workspace), workspace_bytes,
+                          _stream(stream))
+    _check(st, "bf_gemm_ws")
+
+
 def gemm_swiglu(qtype: int, W, W_aux, gate_up, C, M: int, N: int, K: int, *, ld: int | None = None,
                 ldc: int | None = None, otype: int = OUT_F32, stream=None) -> None:
     """C[M][N] = (SiLU(G) * U) . dequant(W)^T with G, U = columns [0, K) and
@@ -208,15 +235,31 @@ def gemm_q8(qtype: int, W, W_aux, Aq, C, M: int, N: int, K: int, *, ldc: int | N
                             M, N, K, _stream(stream)), "bf_gemm_q8")
 
 
-def gemm_batched(qtype: int, gemms, *, otype: int = OUT_F32, stream=None) -> None:
-    """Independent GEMMs in as few launches as the library can: `gemms` is a
-    list of (W, W_aux, A, C, M, N, K) with device tensors or addresses (lda = K,
-    ldc = N); each C is overwritten as by gemm()."""
+def _descs(gemms):
     descs = (GemmDesc * max(1, len(gemms)))()
     for d, (W, W_aux, A, C, M, N, K) in zip(descs, gemms):
         d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, d.M, d.N, d.K = (_ptr(W), _ptr(W_aux), _ptr(A), K, _ptr(C), N,
                                                                M, N, K)
-    _check(lib().bf_gemm_batched(qtype, otype, len(gemms), descs, _stream(stream)), "bf_gemm_batched")
+    return descs
+
+
+def gemm_batched(qtype: int, gemms, *, otype: int = OUT_F32, stream=None) -> None:
+    """Independent GEMMs in as few launches as the library can: `gemms` is a
+    list of (W, W_aux, A, C, M, N, K) with device tensors or addresses (lda = K,
+    ldc = N); each C is overwritten as by gemm()."""
+    _check(lib().bf_gemm_batched(qtype, otype, len(gemms), _descs(gemms), _stream(stream)), "bf_gemm_batched")
+
+
+def gemm_batched_workspace_bytes(qtype: int, gemms, *, otype: int = OUT_F32) -> int:
+    """Bytes of caller-owned workspace gemm_batched_ws needs for these GEMMs."""
+    return int(lib().bf_gemm_batched_workspace_bytes(qtype, otype, len(gemms), _descs(gemms)))
+
+
+def gemm_batched_ws(qtype: int, gemms, workspace, workspace_bytes: int, *, otype: int = OUT_F32,
+                    stream=None) -> None:
+    """gemm_batched with a caller-owned workspace (as gemm_ws)."""
+    _check(lib().bf_gemm_batched_ws(qtype, otype, len(gemms), _descs(gemms), _ptr(workspace), workspace_bytes,
+                                    _stream(stream)), "bf_gemm_batched_ws")
 
 
 class Gguf:
@@ -283,6 +326,12 @@ def busfill_q4(A, Wq, Ws, C, Bsz: int, K: int, N: int, stream=None) -> None:
     """Reference-compatible call: Q4_0 planes, fp32 C[Bsz][N]."""
     _check(lib().bf_busfill_q4(_ptr(A), _ptr(Wq), _ptr(Ws), _ptr(C), Bsz, K, N, _stream(stream)),
            "bf_busfill_q4")
+
+
+def busfill_q4_ws(A, Wq, Ws, C, Bsz: int, K: int, N: int, workspace, workspace_bytes: int, stream=None) -> None:
+    """busfill_q4 with a caller-owned workspace (as gemm_ws)."""
+    _check(lib().bf_busfill_q4_ws(_ptr(A), _ptr(Wq), _ptr(Ws), _ptr(C), Bsz, K, N, _ptr(workspace),
+                                  workspace_bytes, _stream(stream)), "bf_busfill_q4_ws")
 
 
 def dequant_f16(qtype: int, W, W_aux, out, N: int, K: int, stream=None) -> None:

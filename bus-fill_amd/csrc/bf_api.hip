@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <map>
 #include <vector>
 
@@ -113,16 +114,18 @@ bf_status check_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uin
     return BF_OK;
 }
 
-bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
-                   int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream,
-                   const bf::Scratch* scratch = nullptr) {
-    g_last_error[0] = '\0';
-    bf_status st = check_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K);
-    if (st != BF_OK) return st;
-    if (algo < BF_ALGO_AUTO || algo > BF_ALGO_DENSE) return fail(BF_ERR_INVALID, "unknown algo %d", (int)algo);
+// One launch of a bf_gemm call: a slice of batch rows and its kernel.
+struct Planned {
+    bf::GemmArgs g;
+    bf_algo use;
+};
 
+// The launches a call makes, each checked against its kernel's limits before
+// anything is enqueued (BF_ERR_UNSUPPORTED for an explicit kernel family that
+// cannot serve a slice).
+bf_status plan_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C, int ldc,
+                    bf_otype otype, int M, int N, int K, bf_algo algo, std::vector<Planned>& out) {
     const size_t csize = otype == BF_OUT_F32 ? 4 : 2;
-    hipStream_t hs = (hipStream_t)stream;
     // Batches above 32 rows: the dense kernel, all batch rows of a launch per
     // workgroup (the weights streamed once per 128 rows); where it cannot
     // serve the shape, the K-split kernel over slices of 32 rows (the weights
@@ -130,24 +133,7 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
     // kernel, whose activation traffic grows with every 16-row tile.
     int slice = kMaxMPerLaunch;
     bool dense_slices = false;
-    if (algo == BF_ALGO_AUTO && M > kSplitMaxM) {
-        bf::GemmArgs probe;
-        probe.qtype = (int)qtype;
-        probe.W = (const uint8_t*)W;
-        probe.Waux = (const uint8_t*)W_aux;
-        probe.A = A;
-        probe.lda = lda;
-        probe.C = C;
-        probe.ldc = ldc;
-        probe.out_f16 = otype == BF_OUT_F16;
-        probe.M = M < kMaxMPerLaunch ? M : kMaxMPerLaunch;
-        probe.N = N;
-        probe.K = K;
-        dense_slices = fast_eligible(probe) && bf::dense_supports(probe);
-        probe.M = kSplitMaxM;
-        if (!dense_slices && fast_eligible(probe) && bf::split_supports(probe)) slice = kSplitMaxM;
-    }
-    auto slice_args = [&](int m0) {
+    auto args = [&](int m0, int rows) {
         bf::GemmArgs g;
         g.qtype = (int)qtype;
         g.W = (const uint8_t*)W;
@@ -157,86 +143,159 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
         g.C = (char*)C + (size_t)m0 * ldc * csize;
         g.ldc = ldc;
         g.out_f16 = otype == BF_OUT_F16;
-        g.M = M - m0 < slice ? M - m0 : slice;
+        g.M = rows;
         g.N = N;
         g.K = K;
         return g;
     };
-    auto choose = [&](const bf::GemmArgs& g, bool fast) {
-        if (algo != BF_ALGO_AUTO) return algo;
-        if (!fast) return BF_ALGO_SIMPLE;
-        const bf_algo mid = mid_batch_choice(g);
-        if (mid != BF_ALGO_AUTO) return mid;
-        if (bf::lds_supports(g)) return BF_ALGO_LDS;
-        if (bf::split_supports(g)) return BF_ALGO_SPLIT;
-        if (dense_slices && bf::dense_supports(g)) return BF_ALGO_DENSE;
-        if (bf::slab_supports(g)) return BF_ALGO_SLAB;
-        if (g.M <= kDot2MaxM && bf::dot2_supports(g)) return BF_ALGO_DOT2;
-        return BF_ALGO_MFMA;
-    };
-    if (scratch) {
-        // a call with caller-bounded scratch is checked whole before anything is enqueued
-        for (int m0 = 0; m0 < M; m0 += slice) {
-            const bf::GemmArgs g = slice_args(m0);
-            const bool fast = fast_eligible(g);
-            const bf_algo use = choose(g, fast);
-            size_t need = 0;
-            if (use == BF_ALGO_SPLIT && fast && bf::split_supports(g)) need = bf::split_scratch_bytes(g);
-            else if (use == BF_ALGO_DENSE && fast && bf::dense_supports(g)) need = bf::dense_scratch_bytes(g, scratch->bytes);
-            else continue;
-            if (need > scratch->bytes)
-                return fail(BF_ERR_INVALID, "M=%d N=%d K=%d needs %zu bytes of K-split scratch, more than the "
-                            "%zu bytes bf_gemm_noalloc holds per GPU", g.M, N, K, need, scratch->bytes);
-        }
+    if (algo == BF_ALGO_AUTO && M > kSplitMaxM) {
+        bf::GemmArgs probe = args(0, M < kMaxMPerLaunch ? M : kMaxMPerLaunch);
+        dense_slices = fast_eligible(probe) && bf::dense_supports(probe);
+        probe.M = kSplitMaxM;
+        if (!dense_slices && fast_eligible(probe) && bf::split_supports(probe)) slice = kSplitMaxM;
     }
     for (int m0 = 0; m0 < M; m0 += slice) {
-        const bf::GemmArgs g = slice_args(m0);
+        const bf::GemmArgs g = args(m0, M - m0 < slice ? M - m0 : slice);
         const bool fast = fast_eligible(g);
-        const bf_algo use = choose(g, fast);
-        hipError_t e;
+        bf_algo use = algo;
+        if (use == BF_ALGO_AUTO) {
+            const bf_algo mid = mid_batch_choice(g);
+            if (!fast) use = BF_ALGO_SIMPLE;
+            else if (mid != BF_ALGO_AUTO) use = mid;
+            else if (bf::lds_supports(g)) use = BF_ALGO_LDS;
+            else if (bf::split_supports(g)) use = BF_ALGO_SPLIT;
+            else if (dense_slices && bf::dense_supports(g)) use = BF_ALGO_DENSE;
+            else if (bf::slab_supports(g)) use = BF_ALGO_SLAB;
+            else if (g.M <= kDot2MaxM && bf::dot2_supports(g)) use = BF_ALGO_DOT2;
+            else use = BF_ALGO_MFMA;
+        }
         switch (use) {
             case BF_ALGO_MFMA:
                 if (!fast) return fail(BF_ERR_UNSUPPORTED, "MFMA path needs K %% 256 == 0, 16-byte aligned A/W, lda %% 8 == 0");
-                e = bf::gemm_mfma(g, hs);
                 break;
             case BF_ALGO_DOT2:
                 if (!fast || !bf::dot2_supports(g))
                     return fail(BF_ERR_UNSUPPORTED, "dot2 path does not serve M=%d K=%d with these alignments", g.M, K);
-                e = bf::gemm_dot2(g, hs);
                 break;
             case BF_ALGO_SLAB:
                 if (!fast || !bf::slab_supports(g))
                     return fail(BF_ERR_UNSUPPORTED, "slab path does not serve qtype %d M=%d N=%d K=%d",
                                 (int)qtype, g.M, N, K);
-                e = bf::gemm_slab(g, hs);
                 break;
             case BF_ALGO_SPLIT:
                 if (!fast || !bf::split_supports(g))
                     return fail(BF_ERR_UNSUPPORTED, "K-split path does not serve qtype %d M=%d N=%d K=%d",
                                 (int)qtype, g.M, N, K);
-                e = bf::gemm_split(g, scratch, hs);
                 break;
             case BF_ALGO_DENSE:
                 if (!fast || !bf::dense_supports(g))
                     return fail(BF_ERR_UNSUPPORTED, "dense path does not serve qtype %d M=%d N=%d K=%d",
                                 (int)qtype, g.M, N, K);
-                e = bf::gemm_dense(g, scratch, hs);
                 break;
             case BF_ALGO_LDS:
                 if (!fast || !bf::lds_supports(g))
                     return fail(BF_ERR_UNSUPPORTED, "LDS-staged path does not serve M=%d N=%d K=%d with these alignments",
                                 g.M, N, K);
-                e = bf::gemm_lds(g, hs);
                 break;
             default:
-                e = bf::gemm_simple(g, hs);
+                use = BF_ALGO_SIMPLE;
                 break;
         }
-        st = use == BF_ALGO_SPLIT || use == BF_ALGO_DENSE ? from_split(e, "kernel launch")
-                                                           : from_hip(e, "kernel launch");
+        out.push_back(Planned{g, use});
+    }
+    return BF_OK;
+}
+
+// Workspace bytes one launch takes from a caller's buffer (the exchange's
+// counters, cleared on the stream by each launch, and partial sums).
+size_t scratch_need(const Planned& l) {
+    if (l.use == BF_ALGO_SPLIT) return bf::split_scratch_bytes(l.g);
+    if (l.use == BF_ALGO_DENSE) return bf::dense_scratch_bytes(l.g);
+    return 0;
+}
+
+// ... or from the library's workspace for the stream.
+bf::WsNeed ws_need(const Planned& l) {
+    if (l.use == BF_ALGO_SPLIT) return bf::split_ws_need(l.g);
+    if (l.use == BF_ALGO_DENSE) return bf::dense_ws_need(l.g);
+    return bf::WsNeed{};
+}
+
+const char* kernel_name(bf_algo a) { return a == BF_ALGO_SPLIT ? "K-split" : a == BF_ALGO_DENSE ? "dense" : "other"; }
+
+// Before anything is enqueued: a caller's buffer must hold every launch's
+// need (the launches run in stream order, so they share it); otherwise the
+// stream's workspace is made large enough for all of them now, so that no
+// launch of the call can fail for want of it.
+bf_status secure_workspace(const std::vector<Planned>& ls, const bf::Scratch* scratch, hipStream_t hs,
+                           const char* who, const char* holder) {
+    if (scratch) {
+        for (const Planned& l : ls) {
+            const size_t need = scratch_need(l);
+            if (need > scratch->bytes)
+                return fail(BF_ERR_INVALID, "%s: M=%d N=%d K=%d needs %zu bytes for the %s kernel's exchange, "
+                            "more than the %zu bytes of %s", who, l.g.M, l.g.N, l.g.K, need, kernel_name(l.use),
+                            scratch->bytes, holder);
+        }
+        return BF_OK;
+    }
+    bf::WsNeed w;
+    for (const Planned& l : ls) w.merge(ws_need(l));
+    return from_split(bf::reserve_workspace(hs, w), who);
+}
+
+bf_status launch_planned(const Planned& l, const bf::Scratch* scratch, hipStream_t hs) {
+    hipError_t e;
+    switch (l.use) {
+        case BF_ALGO_MFMA: e = bf::gemm_mfma(l.g, hs); break;
+        case BF_ALGO_DOT2: e = bf::gemm_dot2(l.g, hs); break;
+        case BF_ALGO_SLAB: e = bf::gemm_slab(l.g, hs); break;
+        case BF_ALGO_SPLIT: e = bf::gemm_split(l.g, scratch, hs); break;
+        case BF_ALGO_DENSE: e = bf::gemm_dense(l.g, scratch, hs); break;
+        case BF_ALGO_LDS: e = bf::gemm_lds(l.g, hs); break;
+        default: e = bf::gemm_simple(l.g, hs); break;
+    }
+    return l.use == BF_ALGO_SPLIT || l.use == BF_ALGO_DENSE ? from_split(e, "kernel launch") : from_hip(e, "kernel launch");
+}
+
+// scratch: the caller's workspace (bf_gemm_ws, bf_gemm_noalloc) or nullptr
+// (the library's workspace for the stream).
+bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
+                   int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream,
+                   const bf::Scratch* scratch = nullptr, const char* who = "bf_gemm",
+                   const char* holder = "workspace given") {
+    g_last_error[0] = '\0';
+    bf_status st = check_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K);
+    if (st != BF_OK) return st;
+    if (algo < BF_ALGO_AUTO || algo > BF_ALGO_DENSE) return fail(BF_ERR_INVALID, "unknown algo %d", (int)algo);
+    std::vector<Planned> ls;
+    st = plan_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, algo, ls);
+    if (st != BF_OK) return st;
+    hipStream_t hs = (hipStream_t)stream;
+    st = secure_workspace(ls, scratch, hs, who, holder);
+    if (st != BF_OK) return st;
+    for (const Planned& l : ls) {
+        st = launch_planned(l, scratch, hs);
         if (st != BF_OK) return st;
     }
     return BF_OK;
+}
+
+// Workspace bytes of a call with lda = K, ldc = N and aligned operands (the
+// operands' addresses only decide between the fast kernels and the simple one,
+// which needs none).
+size_t gemm_workspace_bytes(bf_qtype qtype, bf_otype otype, int M, int N, int K) {
+    uint8_t* const fake = (uint8_t*)(uintptr_t)4096;      // aligned placeholders, never dereferenced
+    if (check_gemm(qtype, fake, qtype == BF_Q4_0_PLANES ? fake : nullptr, (const uint16_t*)fake, K, fake, N, otype,
+                   M, N, K) != BF_OK)
+        return 0;
+    std::vector<Planned> ls;
+    if (plan_gemm(qtype, fake, qtype == BF_Q4_0_PLANES ? fake : nullptr, (const uint16_t*)fake, K, fake, N, otype, M,
+                  N, K, BF_ALGO_AUTO, ls) != BF_OK)
+        return 0;
+    size_t need = 0;
+    for (const Planned& l : ls) need = std::max(need, scratch_need(l));
+    return need;
 }
 
 // Scratch of bf_gemm_noalloc: the K-split and dense kernels' row-group
@@ -272,32 +331,18 @@ bf_status noalloc_scratch(uint8_t** out) {
     return BF_OK;
 }
 
-}  // namespace
+// A bf_gemm_batched call: its GEMMs grouped by the kernel bf_gemm would give
+// each (the results are then the same bits) -- every group of two or more
+// shares launches: the LDS-staged kernel at batch 1-8 (one batch size, so one
+// kernel shape), the K-split kernel at 9-32 rows (one m-tile count), the
+// dense kernel (one batch size) -- and the launches of the rest, which run
+// one by one as bf_gemm runs them.
+struct BatchedPlan {
+    std::vector<std::pair<int, std::vector<bf::GemmArgs>>> groups;   // 0 LDS / 1 K-split / 2 dense
+    std::vector<Planned> singles;
+};
 
-extern "C" {
-
-bf_status bf_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C, int ldc,
-                  bf_otype otype, int M, int N, int K, void* stream) {
-    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, BF_ALGO_AUTO, stream);
-}
-
-bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
-                     int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream) {
-    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, algo, stream);
-}
-
-bf_status bf_gemm_noalloc(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
-                          int ldc, bf_otype otype, int M, int N, int K, void* stream) {
-    g_last_error[0] = '\0';
-    uint8_t* p = nullptr;
-    const bf_status st = noalloc_scratch(&p);
-    if (st != BF_OK) return st;
-    const bf::Scratch sc{p, kNoallocScratch};
-    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, BF_ALGO_AUTO, stream, &sc);
-}
-
-bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs, void* stream) {
-    g_last_error[0] = '\0';
+bf_status plan_batched(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs, BatchedPlan& bp) {
     if (count < 0) return fail(BF_ERR_INVALID, "count=%d must be >= 0", count);
     if (count > 0 && !descs) return fail(BF_ERR_INVALID, "descs is NULL");
     for (int i = 0; i < count; i++) {
@@ -305,15 +350,8 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
         const bf_status st = check_gemm(qtype, d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, otype, d.M, d.N, d.K);
         if (st != BF_OK) return st;
     }
-    // The GEMMs are grouped by the kernel bf_gemm would launch for each (its
-    // results are then the same bits) and every group of two or more shares
-    // launches: the LDS-staged kernel at batch 1-8 (one batch size, so one
-    // kernel shape), the K-split kernel at 9-32 rows (one m-tile count), the
-    // dense kernel (one batch size); the rest, and any group its batched
-    // launch does not serve, run one by one.
-    hipStream_t hs = (hipStream_t)stream;
     std::vector<bf::GemmArgs> gs(count);
-    std::map<std::pair<int, int>, std::vector<int>> grp;   // (0 LDS / 1 K-split / 2 dense, batch key)
+    std::map<std::pair<int, int>, std::vector<int>> grp;   // (kind, batch key)
     std::vector<int> single;
     for (int i = 0; i < count; i++) {
         const bf_gemm_desc& d = descs[i];
@@ -343,22 +381,142 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
         const bool ok = n > 1 && (k == 0   ? bf::lds_batched_supports(sub.data(), n)
                                   : k == 1 ? bf::split_batched_supports(sub.data(), n)
                                            : bf::dense_batched_supports(sub.data(), n));
-        if (!ok) {
-            single.insert(single.end(), kv.second.begin(), kv.second.end());
-            continue;
-        }
-        const bf_status st = k == 0   ? from_hip(bf::gemm_lds_batched(sub.data(), n, hs), "batched launch")
-                             : k == 1 ? from_split(bf::gemm_split_batched(sub.data(), n, nullptr, hs), "batched launch")
-                                      : from_split(bf::gemm_dense_batched(sub.data(), n, nullptr, hs), "batched launch");
-        if (st != BF_OK) return st;
+        if (ok) bp.groups.emplace_back(k, std::move(sub));
+        else single.insert(single.end(), kv.second.begin(), kv.second.end());
     }
     for (int i : single) {
         const bf_gemm_desc& d = descs[i];
         const bf_status st =
-            run_gemm(qtype, d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, otype, d.M, d.N, d.K, BF_ALGO_AUTO, stream);
+            plan_gemm(qtype, d.W, d.W_aux, d.A, d.lda, d.C, d.ldc, otype, d.M, d.N, d.K, BF_ALGO_AUTO, bp.singles);
         if (st != BF_OK) return st;
     }
     return BF_OK;
+}
+
+// The most workspace any one launch of the call takes from a caller's buffer
+// (the launches run in stream order, so they share it).
+size_t batched_scratch_need(const BatchedPlan& bp) {
+    size_t need = 0;
+    for (const auto& gr : bp.groups) {
+        const int n = (int)gr.second.size();
+        if (gr.first == 1) need = std::max(need, bf::split_batched_scratch_bytes(gr.second.data(), n));
+        if (gr.first == 2) need = std::max(need, bf::dense_batched_scratch_bytes(gr.second.data(), n));
+    }
+    for (const Planned& l : bp.singles) need = std::max(need, scratch_need(l));
+    return need;
+}
+
+bf::WsNeed batched_ws_need(const BatchedPlan& bp) {
+    bf::WsNeed w;
+    for (const auto& gr : bp.groups) {
+        const int n = (int)gr.second.size();
+        if (gr.first == 1) w.merge(bf::split_batched_ws_need(gr.second.data(), n));
+        if (gr.first == 2) w.merge(bf::dense_batched_ws_need(gr.second.data(), n));
+    }
+    for (const Planned& l : bp.singles) w.merge(ws_need(l));
+    return w;
+}
+
+bf_status launch_batched(const BatchedPlan& bp, const bf::Scratch* scratch, hipStream_t hs) {
+    for (const auto& gr : bp.groups) {
+        const bf::GemmArgs* sub = gr.second.data();
+        const int n = (int)gr.second.size();
+        const bf_status st = gr.first == 0   ? from_hip(bf::gemm_lds_batched(sub, n, hs), "batched launch")
+                             : gr.first == 1 ? from_split(bf::gemm_split_batched(sub, n, scratch, hs), "batched launch")
+                                             : from_split(bf::gemm_dense_batched(sub, n, scratch, hs), "batched launch");
+        if (st != BF_OK) return st;
+    }
+    for (const Planned& l : bp.singles) {
+        const bf_status st = launch_planned(l, scratch, hs);
+        if (st != BF_OK) return st;
+    }
+    return BF_OK;
+}
+
+// A caller's workspace: NULL with 0 bytes (for calls that need none), or a
+// 256-byte aligned buffer.
+bf_status check_workspace(const void* ws, size_t bytes) {
+    if (!ws && bytes) return fail(BF_ERR_INVALID, "workspace is NULL but workspace_bytes is %zu", bytes);
+    if (ws && !aligned(ws, 256)) return fail(BF_ERR_INVALID, "workspace is not 256-byte aligned");
+    return BF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+bf_status bf_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C, int ldc,
+                  bf_otype otype, int M, int N, int K, void* stream) {
+    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, BF_ALGO_AUTO, stream);
+}
+
+bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
+                     int ldc, bf_otype otype, int M, int N, int K, bf_algo algo, void* stream) {
+    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, algo, stream);
+}
+
+bf_status bf_gemm_noalloc(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C,
+                          int ldc, bf_otype otype, int M, int N, int K, void* stream) {
+    g_last_error[0] = '\0';
+    uint8_t* p = nullptr;
+    const bf_status st = noalloc_scratch(&p);
+    if (st != BF_OK) return st;
+    const bf::Scratch sc{p, kNoallocScratch};
+    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, BF_ALGO_AUTO, stream, &sc, "bf_gemm_noalloc",
+                    "scratch bf_gemm_noalloc holds per GPU");
+}
+
+size_t bf_gemm_workspace_bytes(bf_qtype qtype, bf_otype otype, int M, int N, int K) {
+    g_last_error[0] = '\0';
+    return gemm_workspace_bytes(qtype, otype, M, N, K);
+}
+
+bf_status bf_gemm_ws(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* A, int lda, void* C, int ldc,
+                     bf_otype otype, int M, int N, int K, void* workspace, size_t workspace_bytes, void* stream) {
+    g_last_error[0] = '\0';
+    const bf_status st = check_workspace(workspace, workspace_bytes);
+    if (st != BF_OK) return st;
+    const bf::Scratch sc{(uint8_t*)workspace, workspace_bytes};
+    return run_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, BF_ALGO_AUTO, stream, &sc, "bf_gemm_ws");
+}
+
+bf_status bf_busfill_q4_ws(const uint16_t* A, const uint8_t* Wq, const uint16_t* Ws, float* C, int Bsz, int K, int N,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    return bf_gemm_ws(BF_Q4_0_PLANES, Wq, Ws, A, K, C, N, BF_OUT_F32, Bsz, N, K, workspace, workspace_bytes, stream);
+}
+
+bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs, void* stream) {
+    g_last_error[0] = '\0';
+    BatchedPlan bp;
+    bf_status st = plan_batched(qtype, otype, count, descs, bp);
+    if (st != BF_OK) return st;
+    hipStream_t hs = (hipStream_t)stream;
+    st = from_split(bf::reserve_workspace(hs, batched_ws_need(bp)), "bf_gemm_batched");
+    if (st != BF_OK) return st;
+    return launch_batched(bp, nullptr, hs);
+}
+
+size_t bf_gemm_batched_workspace_bytes(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs) {
+    g_last_error[0] = '\0';
+    BatchedPlan bp;
+    if (plan_batched(qtype, otype, count, descs, bp) != BF_OK) return 0;
+    return batched_scratch_need(bp);
+}
+
+bf_status bf_gemm_batched_ws(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    g_last_error[0] = '\0';
+    bf_status st = check_workspace(workspace, workspace_bytes);
+    if (st != BF_OK) return st;
+    BatchedPlan bp;
+    st = plan_batched(qtype, otype, count, descs, bp);
+    if (st != BF_OK) return st;
+    const size_t need = batched_scratch_need(bp);
+    if (need > workspace_bytes)
+        return fail(BF_ERR_INVALID, "bf_gemm_batched_ws: the call needs %zu bytes of workspace, %zu given", need,
+                    workspace_bytes);
+    const bf::Scratch sc{(uint8_t*)workspace, workspace_bytes};
+    return launch_batched(bp, need ? &sc : nullptr, (hipStream_t)stream);
 }
 
 bf_status bf_gemm_swiglu(bf_qtype qtype, const void* W, const void* W_aux, const uint16_t* gate_up, int ld,
@@ -429,13 +587,32 @@ bf_status bf_ffn_swiglu_ex(bf_qtype qtype, bf_qweights gate, bf_qweights up, bf_
     if (form == BF_FFN_TWO_LAUNCHES && !two)
         return fail(BF_ERR_UNSUPPORTED, "two-launch feed-forward block: batch 1-2 with the down projection's "
                                         "activations resident in LDS (M=%d F=%d)", M, F);
-    st = bf_gemm_batched(qtype, BF_OUT_F16, 2, d, stream);
+    const bool fused_down = two && form != BF_FFN_CALLS;
+    // every launch of the block is planned, and the stream's workspace made
+    // large enough for all of them, before the first is enqueued
+    BatchedPlan bp;
+    st = plan_batched(qtype, BF_OUT_F16, 2, d, bp);
     if (st != BF_OK) return st;
-    if (two && form != BF_FFN_CALLS) return from_hip(bf::gemm_lds_swiglu(gs[2], hs), "kernel launch");
+    bf::WsNeed need = batched_ws_need(bp);
+    std::vector<Planned> down_l;
+    if (!fused_down) {
+        st = plan_gemm(qtype, down.W, down.W_aux, gate_up, ldgu, C, ldc, otype, M, N, F, BF_ALGO_AUTO, down_l);
+        if (st != BF_OK) return st;
+        for (const Planned& l : down_l) need.merge(ws_need(l));
+    }
+    st = from_split(bf::reserve_workspace(hs, need), "bf_ffn_swiglu");
+    if (st != BF_OK) return st;
+    st = launch_batched(bp, nullptr, hs);
+    if (st != BF_OK) return st;
+    if (fused_down) return from_hip(bf::gemm_lds_swiglu(gs[2], hs), "kernel launch");
     // SiLU(gate) * up in place over the gate half, then the down GEMM
     st = from_hip(bf::swiglu_f16(gate_up, ldgu, gate_up, ldgu, M, F, hs), "kernel launch");
     if (st != BF_OK) return st;
-    return run_gemm(qtype, down.W, down.W_aux, gate_up, ldgu, C, ldc, otype, M, N, F, BF_ALGO_AUTO, stream);
+    for (const Planned& l : down_l) {
+        st = launch_planned(l, nullptr, hs);
+        if (st != BF_OK) return st;
+    }
+    return BF_OK;
 }
 
 bf_status bf_ffn_swiglu(bf_qtype qtype, bf_qweights gate, bf_qweights up, bf_qweights down, const uint16_t* A,

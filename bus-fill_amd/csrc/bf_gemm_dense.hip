@@ -549,11 +549,37 @@ bool dense_supports(const GemmArgs& g) {
     return plan_dense(g, p, device_cus());
 }
 
-size_t dense_scratch_bytes(const GemmArgs& g, size_t limit) {
+size_t dense_scratch_bytes(const GemmArgs& g) {
     DensePlan p;
-    if (!plan_dense(g, p, device_cus())) return ~(size_t)0;
-    const size_t need = dense_partial_bytes(g, p);
-    return need <= limit ? need : ~(size_t)0;
+    if (!plan_dense(g, p, device_cus())) return 0;
+    return dense_partial_bytes(g, p);
+}
+
+WsNeed dense_ws_need(const GemmArgs& g) {
+    WsNeed w;
+    w.p = dense_scratch_bytes(g);
+    return w;
+}
+
+// The largest workspace one launch of gemm_dense_batched takes (the GEMMs in
+// launches of up to kDnMaxJobs, each launch's partials side by side).
+size_t dense_batched_scratch_bytes(const GemmArgs* gs, int n) {
+    size_t worst = 0;
+    for (int i0 = 0; i0 < n; i0 += kDnMaxJobs) {
+        size_t tot = 0;
+        for (int i = i0; i < std::min(n, i0 + kDnMaxJobs); i++) {
+            DensePlan p;
+            if (plan_dense(gs[i], p, device_cus())) tot += dense_partial_bytes(gs[i], p);
+        }
+        worst = std::max(worst, tot);
+    }
+    return worst;
+}
+
+WsNeed dense_batched_ws_need(const GemmArgs* gs, int n) {
+    WsNeed w;
+    w.p = dense_batched_scratch_bytes(gs, n);
+    return w;
 }
 
 bool dense_batched_supports(const GemmArgs* gs, int n) {
@@ -569,6 +595,7 @@ bool dense_batched_supports(const GemmArgs* gs, int n) {
 
 hipError_t gemm_dense_batched(const GemmArgs* gs, int n, const Scratch* scratch, hipStream_t st) {
     if (!dense_batched_supports(gs, n)) return hipErrorInvalidValue;
+    if (scratch && dense_batched_scratch_bytes(gs, n) > scratch->bytes) return hipErrorInvalidValue;
     for (int i0 = 0; i0 < n; i0 += kDnMaxJobs) {
         const int m = std::min(kDnMaxJobs, n - i0);
         DensePlan ps[kDnMaxJobs];

@@ -31,6 +31,7 @@
 #include "bf_device.h"
 #include "bf_formats.h"
 #include "bf_launch.h"
+#include "bf_lds_plan.h"
 
 namespace bf {
 
@@ -525,25 +526,36 @@ hipError_t launch_q8(const Q8Args& g, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Waves per workgroup of the MFMA form with T tiles: as many as registers
+// allow (more super-groups in flight), 16 up to two tiles, 8 above.
+constexpr int q8m_waves(int T) { return T <= 2 ? 16 : 8; }
+
+// LDS of one k_gemm_q8m workgroup: the waves' partial sums, then the batch
+// rows' block scales and sums for all of K.
+size_t q8m_lds_bytes(int K, int T) {
+    return (size_t)q8m_waves(T) * T * 16 * 17 * 4 + (size_t)(K / 32) * 16 * 4 * 2;
+}
+
 template <int QT, int T>
 hipError_t launch_q8m_t(const Q8Args& g, int R, int G, hipStream_t st) {
-    // as many waves as registers allow (more super-groups in flight): 16 up
-    // to two tiles, 8 above
-    constexpr int NW = T <= 2 ? 16 : 8;
+    constexpr int NW = q8m_waves(T);
     const int8_t* q = (const int8_t*)g.Aq;
     const float* d = (const float*)(q + (int64_t)g.M * g.K);
     const int* s = (const int*)(d + (int64_t)g.M * (g.K / 32));
     const int waves = std::min(NW, g.K / 256);
-    const size_t lds = (size_t)NW * T * 16 * 17 * 4 + (size_t)(g.K / 32) * 16 * 4 * 2;
+    const size_t lds = q8m_lds_bytes(g.K, T);
+    if (lds > (size_t)kMaxLds) return hipErrorInvalidValue;     // the dispatcher sends such shapes to k_gemm_q8
     auto k = k_gemm_q8m<QT, T, NW>;
     if (lds > 64 * 1024) {
+        // raised once per device to the most any shape may ask for, so the
+        // limit does not depend on which K came first
         static std::atomic<uint64_t> attr_set{0};     // one bit per device: LDS limit raised
         int dev = 0;
         hipError_t e = hipGetDevice(&dev);
         if (e != hipSuccess) return e;
         const uint64_t bit = 1ull << (dev & 63);
         if (!(attr_set.load(std::memory_order_acquire) & bit)) {
-            e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
             if (e != hipSuccess) return e;
             attr_set.fetch_or(bit, std::memory_order_acq_rel);
         }
@@ -589,7 +601,9 @@ hipError_t dispatch_q8_m(const Q8Args& g, hipStream_t st) {
     // The MFMA form from 3 batch rows (below, the v_dot4 form's fixed cost is
     // lower: 7.4 / 8.5 against 9.6 / 10.1 us at 5120^2, M = 1 / 2); Q4_0's
     // 36-byte block pairs take the most registers: up to 3 tiles
-    if (g.M >= 3 && g.K % 256 == 0 && g.K <= kQ8mMaxK && q8m_rows(g.N) <= (QT == QT_Q4_0 ? 48 : 80))
+    const int R = q8m_rows(g.N);
+    if (g.M >= 3 && g.K % 256 == 0 && g.K <= kQ8mMaxK && R <= (QT == QT_Q4_0 ? 48 : 80) &&
+        q8m_lds_bytes(g.K, (R + 15) / 16) <= (size_t)kMaxLds)
         return launch_q8m<QT>(g, st);
     // batches above 4 run as groups of 4 rows (more batch rows per workgroup
     // cost registers, and with them the second workgroup per CU)

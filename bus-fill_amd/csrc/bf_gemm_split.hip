@@ -63,6 +63,7 @@
 #include <thread>
 #include <tuple>
 #include <utility>
+#include <vector>
 
 #include "bf_launch.h"
 #include "bf_lds.h"
@@ -117,9 +118,16 @@ int device_cus() {
 // Three regions: counters (kept zero between launches by the kernels that use
 // them), partial slots (kept free, every word kSlotFree, between launches by
 // the K-split exchange that uses them) and partials (no state between
-// launches).  Grown on demand: the old buffer is freed once the stream has
-// finished with it.  Never allocated while the stream is being captured into
-// a graph (an allocation cannot be captured): such a call fails with
+// launches).  Grown on demand, each region that is too small to at least
+// twice its old size, so a stream holds at most about twice its largest
+// need.  A buffer that has been replaced is retired, never freed: launches
+// already queued may use it, so may a graph captured from the stream, and so
+// may a call that another host thread is enqueueing on the same stream with
+// the pointer it was handed before the growth (every launch leaves its
+// buffer in the state the next one expects, so a retired buffer stays
+// usable).  Retired buffers are released when the process ends.  Never
+// allocated while the stream is being captured into a graph (an allocation
+// cannot be captured): such a call fails with
 // hipErrorStreamCaptureUnsupported unless a large enough workspace exists.
 hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t sbytes, size_t pbytes, unsigned** counters,
                              float** slots, float** parts) {
@@ -129,6 +137,7 @@ hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t sbytes, size_
     };
     static std::mutex mu;
     static std::map<std::tuple<int, uintptr_t, std::thread::id>, Slot> cache;
+    static std::vector<uint8_t*> retired;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -140,7 +149,10 @@ hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t sbytes, size_
         e = hipStreamIsCapturing(st, &cs);
         if (e != hipSuccess) return e;
         if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
-        const size_t cb = std::max(cbytes, slot.cb), sb = std::max(sbytes, slot.sb), pb = std::max(pbytes, slot.pb);
+        auto grow = [](size_t have, size_t need) {
+            return need <= have ? have : std::max(need, 2 * have);
+        };
+        const size_t cb = grow(slot.cb, cbytes), sb = grow(slot.sb, sbytes), pb = grow(slot.pb, pbytes);
         uint8_t* p = nullptr;
         e = hipMalloc((void**)&p, cb + sb + pb);
         if (e != hipSuccess) return e;
@@ -150,19 +162,20 @@ hipError_t library_workspace(hipStream_t st, size_t cbytes, size_t sbytes, size_
             (void)hipFree(p);
             return e;
         }
-        if (slot.p) {
-            // launches already queued on the stream may still use the old buffer
-            e = hipStreamSynchronize(st);
-            if (e != hipSuccess) return e;
-            e = hipFree(slot.p);
-            if (e != hipSuccess) return e;
-        }
+        if (slot.p) retired.push_back(slot.p);
         slot = Slot{p, cb, sb, pb};
     }
     *counters = (unsigned*)slot.p;
     *slots = (float*)(slot.p + slot.cb);
     *parts = (float*)(slot.p + slot.cb + slot.sb);
     return hipSuccess;
+}
+
+hipError_t reserve_workspace(hipStream_t st, const WsNeed& need) {
+    if (!need.c && !need.s && !need.p) return hipSuccess;
+    unsigned* counters = nullptr;
+    float *slots = nullptr, *parts = nullptr;
+    return library_workspace(st, need.c, need.s, need.p, &counters, &slots, &parts);
 }
 
 // Counters and partials for one launch: carved out of the caller's scratch
@@ -696,16 +709,20 @@ hipError_t launch_split_k(const GemmArgs& g, const SplitPlan& p, const Scratch* 
     return hipGetLastError();
 }
 
+// Whether a single launch leaves its splits to k_split_sum: grids of more
+// than one round but less than two keep the counter-free exchange in the
+// kernel where it is available (7168x5120 at M = 32, 448 workgroups: 17.9 ->
+// 17.1 us); from two full rounds on a second launch (17408x5120 at M = 16,
+// 512 workgroups: 23.1 against 23.8-24.3 us in the kernel).
+bool split_second_launch(const SplitPlan& p, const Scratch* scratch) {
+    const int cus = device_cus() > 0 ? device_cus() : 256;
+    return split_sum2(p) && (!use_slots(p, scratch) || p.grid >= 2 * cus);
+}
+
 template <int QT, int MT>
 hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
-    // grids of more than one round but less than two: the counter-free
-    // exchange in the kernel where it is available (7168x5120 at M = 32, 448
-    // workgroups: 17.9 -> 17.1 us); from two full rounds on a second launch
-    // (17408x5120 at M = 16, 512 workgroups: 23.1 against 23.8-24.3 us in
-    // the kernel)
-    const int cus = device_cus() > 0 ? device_cus() : 256;
-    const bool sum2 = split_sum2(p) && (!use_slots(p, scratch) || p.grid >= 2 * cus);
-    return sum2 ? launch_split_k<QT, MT, true>(g, p, scratch, st) : launch_split_k<QT, MT, false>(g, p, scratch, st);
+    return split_second_launch(p, scratch) ? launch_split_k<QT, MT, true>(g, p, scratch, st)
+                                           : launch_split_k<QT, MT, false>(g, p, scratch, st);
 }
 
 template <int QT>
@@ -782,6 +799,44 @@ size_t split_scratch_bytes(const GemmArgs& g) {
     SplitPlan p;
     if (!plan_split(g, p, device_xcds())) return 0;
     return (split_sum2(p) ? 0 : counter_bytes(p)) + partial_bytes(g, p);
+}
+
+WsNeed split_ws_need(const GemmArgs& g) {
+    WsNeed w;
+    SplitPlan p;
+    if (!plan_split(g, p, device_xcds()) || p.S <= 1) return w;
+    if (split_second_launch(p, nullptr)) w.p = partial_bytes(g, p);
+    else if (use_slots(p, nullptr)) w.s = partial_bytes(g, p);
+    else {
+        w.c = counter_bytes(p);
+        w.p = partial_bytes(g, p);
+    }
+    return w;
+}
+
+WsNeed split_batched_ws_need(const GemmArgs* gs, int n) {
+    WsNeed w;
+    const int nx = device_xcds();
+    for (int i0 = 0; i0 < n; i0 += kSpMaxJobs) {
+        size_t ctot = 0, ptot = 0;
+        int bnx = 0;
+        for (int i = i0; i < std::min(n, i0 + kSpMaxJobs); i++) {
+            SplitPlan p;
+            if (!plan_split(gs[i], p, nx)) continue;
+            ctot += counter_bytes(p);
+            ptot += partial_bytes(gs[i], p);
+            if (p.nx) bnx = p.nx;
+        }
+        if (!ctot) continue;
+        WsNeed one;
+        if (bnx > 0) one.s = ptot;
+        else {
+            one.c = ctot;
+            one.p = ptot;
+        }
+        w.merge(one);
+    }
+    return w;
 }
 
 bool split_batched_supports(const GemmArgs* gs, int n) {

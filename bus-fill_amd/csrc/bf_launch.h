@@ -45,6 +45,22 @@ bool slab_supports(const GemmArgs& g);
 int device_xcds();
 // CUs of the current device, 0 if unknown.
 int device_cus();
+// Bytes of the library's per-stream workspace a launch needs, per region:
+// counters (kept zero between launches), partial slots (kept free between
+// launches) and partials.
+struct WsNeed {
+    size_t c = 0, s = 0, p = 0;
+    void merge(const WsNeed& o) {
+        c = c > o.c ? c : o.c;
+        s = s > o.s ? s : o.s;
+        p = p > o.p ? p : o.p;
+    }
+};
+// Makes the stream's workspace at least `need` (allocating it now unless it
+// already is; hipErrorStreamCaptureUnsupported while the stream is
+// capturing), so that the launches that follow on the stream allocate
+// nothing.
+hipError_t reserve_workspace(hipStream_t st, const WsNeed& need);
 // Counters and partials of a cross-workgroup exchange: carved out of `scratch`
 // (its counters cleared by a kernel on the stream first) or the library's
 // workspace for the stream (allocated on first use; never while the stream is
@@ -62,25 +78,30 @@ hipError_t split_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes
 hipError_t gemm_split(const GemmArgs& g, const Scratch* scratch, hipStream_t st);
 bool split_supports(const GemmArgs& g);
 size_t split_scratch_bytes(const GemmArgs& g);      // 0 when the plan does not split K
+WsNeed split_ws_need(const GemmArgs& g);            // of a launch on the library's workspace
 // Independent GEMMs of one format, one output type and one side of M = 16, in
 // launches of up to eight (their grids back to back).
 hipError_t gemm_split_batched(const GemmArgs* gs, int n, const Scratch* scratch, hipStream_t st);
 bool split_batched_supports(const GemmArgs* gs, int n);
 size_t split_batched_scratch_bytes(const GemmArgs* gs, int n);
+WsNeed split_batched_ws_need(const GemmArgs* gs, int n);
 bool dot2_supports(const GemmArgs& g);
 // The dense kernel (33-128 batch rows per launch, the weights streamed once):
 // 64 weight rows x all batch rows per workgroup, K split with the exchange
 // above when that balances the grid.
 hipError_t gemm_dense(const GemmArgs& g, const Scratch* scratch, hipStream_t st);
 bool dense_supports(const GemmArgs& g);
-// Workspace bytes of the plan chosen under a workspace limit (0 when it does
-// not split K; SIZE_MAX when no plan fits the limit).
-size_t dense_scratch_bytes(const GemmArgs& g, size_t limit);
+// Workspace bytes of the dense plan's partial pieces (0 when no row group is
+// split between workgroups).
+size_t dense_scratch_bytes(const GemmArgs& g);
+WsNeed dense_ws_need(const GemmArgs& g);
 // Independent dense-kernel GEMMs of one format, one batch size and one output
 // type, in launches of up to eight (their grids back to back, each with the
 // ranges of a launch of its own) and one sum launch each.
 hipError_t gemm_dense_batched(const GemmArgs* gs, int n, const Scratch* scratch, hipStream_t st);
 bool dense_batched_supports(const GemmArgs* gs, int n);
+size_t dense_batched_scratch_bytes(const GemmArgs* gs, int n);
+WsNeed dense_batched_ws_need(const GemmArgs* gs, int n);
 
 hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
                        int N, int K, hipStream_t st);

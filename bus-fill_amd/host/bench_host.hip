@@ -110,6 +110,10 @@ int time_seq(const std::vector<Launch>& seq, int otype, int algo, int warmup, in
             HCK(hipGraphDestroy(g));
             return 0;
         };
+        // one uncaptured call first, so that the stream's workspace exists
+        // before the capture (the library allocates none while capturing)
+        if (issue(0)) return -1;
+        HCK(hipStreamSynchronize(st));
         hipGraphExec_t gw = nullptr, gs = nullptr;
         if (warmup > 0 && capture(0, warmup, &gw)) return -1;
         if (capture(warmup, steps, &gs)) return -1;

@@ -12,27 +12,35 @@
  * describes in RESULTS.md:84-96) with a host-callable function.
  *
  * Conventions
- *   - All pointers are DEVICE pointers owned by the caller.  The one device
- *     memory the library allocates itself is the workspace of its
- *     cross-workgroup exchanges: the K-split kernel's (BF_ALGO_SPLIT, which
- *     bf_gemm picks for 9-32 batch rows per launch when the activations do not
- *     fit in LDS) partial sums (and row-group counters where the splits of a
- *     row group cannot be kept on one XCD), and the dense kernel's
+ *   - All pointers are DEVICE pointers owned by the caller.  Two kernels
+ *     exchange partial sums between workgroups and need a workspace: the
+ *     K-split kernel (BF_ALGO_SPLIT, which bf_gemm picks for 9-32 batch rows
+ *     per launch when the activations do not fit in LDS) and the dense kernel
  *     (BF_ALGO_DENSE, above 32 rows, and from 9 or 17 rows on matrices of
- *     3 * 2^24 weights or more) partial sums, one workspace per (device, stream)
- *     -- per host thread for hipStreamPerThread -- allocated by the first such
- *     call on the stream, grown (the old buffer freed once the stream has
- *     passed it) and kept until the process ends.  It is never allocated while
- *     the stream is being captured into a graph: such a call returns
- *     BF_ERR_UNSUPPORTED; make one uncaptured call of the shape on the stream
- *     first, or use bf_gemm_noalloc.  The one-launch feed-forward block
- *     (bf_ffn_swiglu_ex, BF_FFN_ONE_LAUNCH) keeps its hand-over words in the
- *     same workspace.  A captured graph holds the workspace of
- *     the stream it was captured on: replaying it while other exchanging work
- *     runs on that stream (or another replay of it) races, and a later call
- *     on the stream that grows the workspace frees the buffer the graph
- *     refers to -- capture after the stream has run its largest shape, or
- *     use bf_gemm_noalloc in graphs.
+ *     3 * 2^24 weights or more).  Three ways to provide it:
+ *       * bf_gemm_ws / bf_gemm_batched_ws / bf_busfill_q4_ws: the caller owns
+ *         it (size from bf_gemm_workspace_bytes / bf_gemm_batched_workspace_bytes);
+ *         the library allocates nothing and keeps no state between calls.
+ *       * bf_gemm_noalloc: a fixed array in device memory per GPU.
+ *       * bf_gemm, bf_gemm_batched, bf_busfill_q4, bf_ffn_swiglu: the
+ *         library's workspace for the (device, stream) -- per host thread for
+ *         hipStreamPerThread -- allocated by the first call on the stream that
+ *         needs it and grown by a later call that needs more (each region that
+ *         is too small to at least twice its size).  A replaced buffer is
+ *         retired, never freed before the process ends, so launches already
+ *         queued, graphs captured earlier and calls racing on the same stream
+ *         from other host threads keep valid memory.  Nothing is allocated
+ *         while the stream is being captured into a graph: a call that would
+ *         need to returns BF_ERR_UNSUPPORTED and enqueues nothing; make one
+ *         uncaptured call of the largest shape on the stream first, or use a
+ *         caller-owned workspace.  The one-launch feed-forward block
+ *         (bf_ffn_swiglu_ex, BF_FFN_ONE_LAUNCH) keeps its hand-over words in
+ *         the same workspace.  A captured graph holds the buffer of the
+ *         stream it was captured on: replaying it while other exchanging work
+ *         that uses that buffer runs (on another stream, or another replay)
+ *         races.
+ *     Every call plans all its launches and secures their workspace before
+ *     it enqueues the first, so a call that fails enqueues nothing.
  *   - fp16 values travel as uint16_t bit patterns.
  *   - A is [M][lda] row-major fp16, C is [M][ldc] row-major (fp32 or fp16),
  *     W is [N][K] in the chosen block format: C = A . dequant(W)^T.
@@ -48,6 +56,7 @@
 #ifndef BUSFILL_H
 #define BUSFILL_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -139,6 +148,34 @@ bf_status bf_gemm_noalloc(bf_qtype qtype, const void* W, const void* W_aux,
                           const uint16_t* A, int lda, void* C, int ldc, bf_otype otype,
                           int M, int N, int K, void* stream);
 
+/* Bytes of caller-owned workspace bf_gemm_ws needs for a GEMM of this format,
+ * output type and shape (0: none); computed for lda = K and ldc = N with
+ * 16-byte aligned operands, the case that runs the exchanging kernels.
+ * The same bytes serve bf_busfill_q4_ws (BF_Q4_0_PLANES, BF_OUT_F32, M = Bsz).
+ * No counterpart in the reference, whose kernel needs no scratch
+ * (kernels/busfill_v1a.cu:41-46). */
+size_t bf_gemm_workspace_bytes(bf_qtype qtype, bf_otype otype, int M, int N, int K);
+
+/* bf_gemm with a caller-owned workspace: the call allocates nothing and the
+ * library keeps no state between calls (the exchange's counters are cleared
+ * on the stream by each launch).  workspace: 256-byte aligned device memory
+ * of workspace_bytes >= bf_gemm_workspace_bytes(...) (NULL and 0 when that is
+ * 0); BF_ERR_INVALID, enqueueing nothing, when it is too small.  The result is
+ * bit-identical to bf_gemm's.  Calls that overlap in time (other streams, or
+ * graph replays) must not share a workspace; calls in one stream may.
+ * Replaces the busfill_q4 launch (kernels/busfill_v1a.cu:154,169) for
+ * callers that own every device allocation, as the reference's caller does
+ * (kernels/busfill_v1a.cu:140-145). */
+bf_status bf_gemm_ws(bf_qtype qtype, const void* W, const void* W_aux,
+                     const uint16_t* A, int lda, void* C, int ldc, bf_otype otype,
+                     int M, int N, int K, void* workspace, size_t workspace_bytes, void* stream);
+
+/* bf_busfill_q4 with a caller-owned workspace (as bf_gemm_ws).  Replaces the
+ * busfill_q4<<<N/32,128>>> launch of kernels/busfill_v1a.cu:154,169 with the
+ * reference's argument order and meaning, plus the workspace and the stream. */
+bf_status bf_busfill_q4_ws(const uint16_t* A, const uint8_t* Wq, const uint16_t* Ws, float* C,
+                           int Bsz, int K, int N, void* workspace, size_t workspace_bytes, void* stream);
+
 /* One GEMM of a batch: bf_gemm's arguments C[0:M][0:N] = A[0:M][0:K] . dequant(W)^T. */
 typedef struct {
     const void* W;
@@ -163,6 +200,17 @@ typedef struct {
  * bf_gemm call.  No counterpart in the reference, whose only entry point is
  * the single-GEMM kernel (kernels/busfill_v1a.cu:41-46). */
 bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs, void* stream);
+
+/* Bytes of caller-owned workspace bf_gemm_batched_ws needs for these GEMMs (0:
+ * none; 0 also for invalid descriptors, which bf_gemm_batched_ws rejects). */
+size_t bf_gemm_batched_workspace_bytes(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs);
+
+/* bf_gemm_batched with a caller-owned workspace, as bf_gemm_ws: the call
+ * allocates nothing, keeps no state between calls and gives bf_gemm_batched's
+ * bits.  No counterpart in the reference (kernels/busfill_v1a.cu:41-46 is its
+ * only entry point). */
+bf_status bf_gemm_batched_ws(bf_qtype qtype, bf_otype otype, int count, const bf_gemm_desc* descs,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bit-exact fp16 dequant: W_f16[N][K] = RN_fp16(value), value computed in fp32
  * exactly as kernels/busfill_v0.cu:74,78-81 ((q-8)*fp32(d)) for the Q4_0

@@ -207,3 +207,20 @@ def test_q8_entries_reject_before_any_launch():
     assert L.bf_gemm_q8(bf.Q4_K, FAKE, None, FAKE, FAKE, N - 1, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
     assert L.bf_gemm_q8(bf.Q4_0_PLANES, FAKE, None, FAKE, FAKE, N, bf.OUT_F32, 1, N, K, None) == bf.ERR_INVALID
     assert L.bf_gemm_q8(bf.Q4_K, FAKE, None, FAKE, FAKE, N, 7, 1, N, K, None) == bf.ERR_INVALID
+
+
+def test_workspace_entries_validate_before_any_launch():
+    """The caller-owned workspace entries reject a NULL or misaligned workspace
+    (and the size queries answer 0 for invalid requests) before any HIP call."""
+    L = bf.lib()
+    st = L.bf_gemm_ws(bf.Q4_K, FAKE, None, FAKE, 5120, FAKE, 5120, bf.OUT_F32, 32, 5120, 5120, None, 4096, None)
+    assert st == bf.ERR_INVALID and b"NULL" in L.bf_last_error()
+    st = L.bf_gemm_ws(bf.Q4_K, FAKE, None, FAKE, 5120, FAKE, 5120, bf.OUT_F32, 32, 5120, 5120, FAKE + 64, 4096, None)
+    assert st == bf.ERR_INVALID and b"256-byte" in L.bf_last_error()
+    st = L.bf_busfill_q4_ws(FAKE, FAKE, FAKE, FAKE, 32, 5120, 5120, FAKE + 8, 1 << 20, None)
+    assert st == bf.ERR_INVALID
+    st = L.bf_gemm_batched_ws(bf.Q4_K, bf.OUT_F32, -1, None, None, 0, None)
+    assert st == bf.ERR_INVALID and b"count" in L.bf_last_error()
+    assert L.bf_gemm_batched_workspace_bytes(bf.Q4_K, bf.OUT_F32, -1, None) == 0
+    assert L.bf_gemm_workspace_bytes(bf.Q4_K, bf.OUT_F32, 32, 5120, 5000) == 0      # K % 256 != 0
+    assert L.bf_gemm_workspace_bytes(7, bf.OUT_F32, 32, 5120, 5120) == 0            # unknown format

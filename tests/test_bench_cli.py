@@ -19,3 +19,54 @@ def test_world_size_above_one_is_refused():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py")], capture_output=True, text=True,
                        timeout=120, cwd=ROOT, env=env)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_rotation_rows_hold_whole_matrices():
+    """Every format's rotation row holds one whole matrix (the planes layout:
+    code plane, then scale plane), so the streaming-read yardstick, which
+    reads one matrix's bytes from each row start, stays inside the row -- and,
+    for the last row, inside the allocation."""
+    sys.path.insert(0, ROOT)
+    import bench
+    for fmt in ("q4_k", "q4_0", "planes"):
+        for N, K in ((5120, 5120), (17408, 5120), (5120, 17408), (7168, 5120)):
+            row, w0, wn, a0, an = bench.row_layout(fmt, N, K)
+            assert row == N * K * 9 // 16
+            assert (N * K * 9 // 16) // 16 * 16 <= row
+            assert w0 == 0 and w0 + wn <= row
+            if fmt == "planes":
+                assert wn == N * K // 2 and an == N * K // 16 and a0 == wn and a0 + an == row
+                assert a0 % 256 == 0 and row % 256 == 0       # the scale plane 16-byte aligned in every row
+            else:
+                assert wn == row and a0 is None
+
+
+def test_trace_summary_groups_runs_and_passes(tmp_path):
+    """--trace-summary on a synthetic kernel trace: runs of one kernel, passes
+    of --trace-pass dispatches, dispatch means and per-pass spans."""
+    import csv
+    path = tmp_path / "kt.csv"
+    cols = ["Kind", "Kernel_Name", "Start_Timestamp", "End_Timestamp"]
+    t, rows = 1000, []
+    for name, dur, gap, n in (("void bf::k_a<1, true>(int, float*)", 600, 100, 8),
+                              ("void other_kernel(int)", 50, 0, 1),
+                              ("void bf::k_b<2>(int)", 900, 0, 4)):
+        for _ in range(n):
+            rows.append({"Kind": "KERNEL_DISPATCH", "Kernel_Name": name, "Start_Timestamp": t,
+                         "End_Timestamp": t + dur})
+            t += dur + gap
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=cols)
+        w.writeheader()
+        w.writerows(rows)
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--trace-summary", str(path),
+                        "--trace-pass", "4", "--trace-labels", "a,b"], capture_output=True, text=True, timeout=120,
+                       cwd=ROOT)
+    assert r.returncode == 0, r.stderr
+    import json
+    rec = json.loads(r.stdout)
+    assert rec["a"]["kernel"] == "bf::k_a<1, true>" and rec["a"]["dispatches"] == 8 and rec["a"]["passes"] == 2
+    assert rec["a"]["us_dispatch_mean"] == 0.6
+    # a pass of 4 dispatches spans 4 * 600 + 3 * 100 ns
+    assert abs(rec["a"]["us_span_per_launch_median"] - (4 * 600 + 3 * 100) / 4 / 1000) < 1e-9
+    assert rec["b"]["passes"] == 1 and rec["b"]["us_gap_median"] == 0.0

@@ -855,6 +855,44 @@ def test_gemm_q8_mfma_row_tiles(dev, qt, N):
         assert (np.abs(Cg - ref) <= tol).all(), (QT_NAME[qt], N, M, float((np.abs(Cg - ref) / tol).max()))
 
 
+def rows_of(w, idx):
+    """The weight rows idx of w as a matrix of their own (every output row
+    depends on its weight row only)."""
+    W = w.W.reshape(w.N, -1)[idx]
+    aux = None if w.W_aux is None else w.W_aux.reshape(w.N, -1)[idx]
+    return O.QWeights(w.qtype, len(idx), w.K, np.ascontiguousarray(W), aux)
+
+
+@pytest.mark.parametrize("N,Ks", [(5120, (17408,)), (12300, (8192, 30208)), (16384, (32768,)), (17408, (30208,))])
+def test_gemm_q8_large_k(dev, N, Ks):
+    """The integer-dot GEMM at K = 17408-32768, checked on 96 rows against the
+    oracle's integer restatement at M = 3, 8 and 16: the down projection's
+    K = 17408; a larger K after a smaller one on the same kernel instance
+    (12300 rows: four 16-row tiles, 67 KB then 156 KB of LDS, so the LDS limit
+    must not stay at the first call's size); and shapes whose block-scale
+    table does not fit next to the tiles' sums in 160 KB (four and five tiles
+    at K >= 30208 or 32768), which take the v_dot4 form instead of failing."""
+    rng = np.random.default_rng(N)
+    idx = np.unique(np.concatenate([[0, N - 1], rng.choice(N, 94, replace=False)]))
+    for K in Ks:
+        w = O.gen_weights(O.Q4_K, N, K, 500 + K)
+        ws = rows_of(w, idx)
+        Wd, auxd = upload(w, dev)
+        for M in (3, 8, 16):
+            A = O.gen_act(M, K, 600 + M)
+            Aq = gpu_quantize_q8(A, dev)
+            C = torch.full((M, N), float("nan"), device=dev)
+            bf.gemm_q8(O.Q4_K, Wd, auxd, Aq, C, M, N, K)
+            torch.cuda.synchronize()
+            Cg = C.cpu().numpy().astype(np.float64)
+            assert np.isfinite(Cg).all(), (N, K, M)
+            q, d, s = O.quantize_q8(A)
+            ref, mag = O.gemm_q8(ws, q, d, s)
+            tol = (K / 32 + 32) * 2.0 ** -24 * mag + 1e-30
+            err = np.abs(Cg[:, idx] - ref)
+            assert (err <= tol).all(), (N, K, M, float((err / tol).max()))
+
+
 def test_gemm_q8_full_size_strided_f16_and_deterministic(dev):
     """Q4_K 5120 x 5120 at batch 16 into an fp16 output with ldc > N: rows
     beyond M and columns beyond N untouched, values within the oracle's bound
