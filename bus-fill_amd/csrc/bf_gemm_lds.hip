@@ -764,14 +764,23 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     }
 }
 
+// The single-GEMM kernel's arguments fit in 14 dwords, all of which arrive in
+// SGPRs at wave launch (kernel-argument preloading: 16 user SGPRs less the
+// argument segment's address), so no argument is fetched with a scalar load.
+// One that were would hold up the workgroup's barrier: the wait for the
+// flags' LDS writes before it (lgkmcnt) also counts scalar loads, and at that
+// moment a scalar load queues behind the weight stream the loaders have just
+// started, so the loaders' second group of steps and every step marker would
+// wait for it.  mo = M | out_f16 << 8 | nsub << 16 | win << 24, sl = nslot |
+// na << 16 (lds_packed_args).
 template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC = false, bool SW = false>
 __global__ __launch_bounds__(64 * (NC + NL))
-void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
-                int nsub, int nslot, int na, int win, const uint8_t* __restrict__ Waux, void* __restrict__ C,
-                int ldc, int out_f16) {
+void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, const uint8_t* __restrict__ Waux,
+                void* __restrict__ C, int lda, int ldc, int N, int K, uint32_t mo, uint32_t sl) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    lds_body<QT, G, MT, NC, NL, BD, RG, AC, SW>((int)blockIdx.x, lds, W, A, lda, M, N, K, nsub, nslot, na, win, Waux, C, ldc,
-                                    out_f16);
+    lds_body<QT, G, MT, NC, NL, BD, RG, AC, SW>((int)blockIdx.x, lds, W, A, lda, (int)(mo & 0xFFu), N, K,
+                                                (int)((mo >> 16) & 0xFFu), (int)(sl & 0xFFFFu), (int)(sl >> 16),
+                                                (int)(mo >> 24), Waux, C, ldc, (int)((mo >> 8) & 1u));
 }
 
 // Several independent GEMMs of one kernel shape in one launch (their grids
@@ -807,6 +816,18 @@ constexpr int kNC = 12, kNL = 4;      // compute and loader waves per workgroup
 
 LdsShape lds_shape(const GemmArgs& g) { return LdsShape{g.M, g.N, g.K, g.qtype == QT_Q4_K}; }
 
+// The kernel's packed arguments (k_gemm_lds); false if a field does not fit
+// (no plan makes such a field: M <= 16, nsub <= 128, win <= 96, nslot <= 240,
+// na <= 96).
+bool lds_packed_args(const GemmArgs& g, const LdsPlan& p, uint32_t& mo, uint32_t& sl) {
+    if (g.M < 0 || g.M > 255 || p.nsub < 0 || p.nsub > 255 || p.win < 0 || p.win > 255 || p.nslot < 0 ||
+        p.nslot > 0xFFFF || p.na < 0 || p.na > 0xFFFF)
+        return false;
+    mo = (uint32_t)g.M | (uint32_t)(g.out_f16 ? 1 : 0) << 8 | (uint32_t)p.nsub << 16 | (uint32_t)p.win << 24;
+    sl = (uint32_t)p.nslot | (uint32_t)p.na << 16;
+    return true;
+}
+
 template <int QT, int G, int MT, bool BD = false, bool RG = false, bool AC = false, bool SW = false>
 hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
     auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG, AC, SW>;
@@ -820,8 +841,10 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
         if (e != hipSuccess) return e;
         attr_set.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kNC + kNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K, p.nsub,
-                       p.nslot, p.na, p.win, g.Waux, g.C, g.ldc, g.out_f16);
+    uint32_t mo = 0, sl = 0;
+    if (!lds_packed_args(g, p, mo, sl)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kNC + kNL)), p.lds, st, g.W, g.A, g.Waux, g.C, g.lda, g.ldc, g.N,
+                       g.K, mo, sl);
     return hipGetLastError();
 }
 

@@ -23,39 +23,27 @@
 //   (u = c / nt, U = number of waves on that tile), accumulating all batch rows
 //   (MT m-tiles of 16) in registers.  The other waves of a tile park their sums
 //   in LDS and the tile's first wave adds them in wave order.
-// * With S > 1 the tile sums are written to a workspace; the split that
-//   finishes last (a counter per row group) adds the S partials in split order
-//   and writes C.  The order never depends on timing, so results are
-//   deterministic; the last split resets the counter, so the workspace is
-//   ready for the next launch that uses it.  A writer's stores are complete
-//   (s_waitcnt vmcnt(0)) before its workgroup counts itself, and the last
-//   split reads only after its own count.
-// * XCD-local exchange (nx > 0): the dispatcher hands the workgroups of a
-//   launch to the nx XCDs round robin, starting from an XCD that depends on
-//   the hardware queue of the stream (measured: 0 on the null stream, 6 and 7
-//   on two created streams), so each round of nx consecutive workgroups
-//   covers every XCD once.  A workgroup takes its row group from the XCD it
-//   finds itself on (XCC id x) and its round (b / nx): XCD x holds row groups
-//   x, x + nx, ..., each as S consecutive rounds, so all S splits of a row
-//   group share one L2 whatever the starting XCD.  Partials are then plain
-//   (L2 write-back) stores that the last split's device-scope reads find in
-//   that L2 (those reads miss only the L1), instead of stores written through
-//   to memory.  The counter stays a device-scope atomic; each split adds
-//   1 + 2^(8 + s), so the last arrival sees exactly S + (2^S - 1) 2^8 unless
-//   a split came twice (a placement that was not round robin) or a split was
-//   poisoned (2^7): its row group's C is then NaN, never a silently wrong
-//   sum.  With nx = 0 the partials are written with device-scope (sc1)
-//   stores, which reach the point of coherence of all XCDs' L2s.
-// * Counter-free exchange (XCD-local, library workspace): the partials go to
-//   slots that hold kSlotFree (a signaling NaN, never an arithmetic result)
-//   between launches.  The splits other than the last store their tile sums
-//   and are done; the row group's last split (s = S - 1) reads all S slots of
-//   each of its elements from the L2 until no word is free, adds them in
-//   split order (the same bits as the counted exchange and k_split_sum),
-//   writes C and frees the slots.  This drops the store acknowledgement and
-//   the counter's round trip from the exchange.  A slot still free after the
-//   bound (a protocol bug) makes the element NaN; a poisoned split's sums are
-//   NaN and so is the row group's C.
+// * XCD-local exchange: the dispatcher hands the workgroups of a launch to
+//   the nx XCDs round robin, starting from an XCD that depends on the
+//   hardware queue of the stream (measured: 0 on the null stream, 6 and 7 on
+//   two created streams), so each round of nx consecutive workgroups covers
+//   every XCD once.  A workgroup takes its row group from the XCD it finds
+//   itself on (XCC id x) and its round (b / nx): XCD x holds row groups x,
+//   x + nx, ..., each as S consecutive rounds, so all S splits of a row group
+//   share one L2 whatever the starting XCD.
+// * Exchange through free slots (S > 1): the tile sums go to workspace slots
+//   that hold kSlotFree (a signaling NaN, never an arithmetic result) between
+//   launches, as plain (L2 write-back) stores; the row group's last split
+//   reads every split's slots of each of its elements from its XCD's L2 until
+//   no word is free, adds them in split order, writes C and frees the slots.
+//   No counter and no store acknowledgement.  The order never depends on
+//   timing, so results are deterministic (k_split_sum, the second-launch sum,
+//   adds in the same order).  The row group's reader swaps its tag from free
+//   to taken at its start and frees it at its end, so a placement that is not
+//   round robin (a moved workgroup keeps its split: a row group then misses a
+//   split, or has a second reader) shows as NaN in C and a poison word in the
+//   workspace that makes every later launch on it NaN (split_body); a
+//   poisoned split (a bounded LDS wait gave up) writes NaN sums, and so NaN C.
 #include <algorithm>
 #include <atomic>
 #include <map>
@@ -80,6 +68,9 @@ __global__ void k_init_workspace(unsigned* p, int nzero, int nfree) {
         p[i] = i < nzero ? 0u : kSlotFree;
 }
 }  // namespace
+
+// Bytes before a launch's partial slots: the poison word and padding.
+constexpr size_t kSlotHeader = 256;
 
 // XCDs of the current device: the workgroup round robin the XCD-local exchange
 // lays its grid out for (1 on a device with one XCD per agent).
@@ -178,14 +169,27 @@ hipError_t reserve_workspace(hipStream_t st, const WsNeed& need) {
     return library_workspace(st, need.c, need.s, need.p, &counters, &slots, &parts);
 }
 
-// Counters and partials for one launch: carved out of the caller's scratch
-// (bytes == 0: none given) or the library's workspace for the stream.
-// Free partial slots for one launch of the counter-free exchange: only in the
-// library's workspace for the stream (a caller's scratch has no slot region).
-hipError_t slot_workspace(hipStream_t st, size_t sbytes, float** slots) {
-    unsigned* counters = nullptr;
-    float* parts = nullptr;
-    return library_workspace(st, 0, sbytes, 0, &counters, slots, &parts);
+// Partial slots of one launch of the shared exchange, behind a 256-byte
+// header whose first word is the workspace's poison word (kSlotFree while
+// clean).  In the library's workspace for the stream the region is free
+// between launches (every launch frees each slot it fills); a caller's
+// scratch may hold anything, so there it is filled with kSlotFree by a small
+// kernel on the stream before each launch (a kernel, not a memset node, so
+// that a captured call replays correctly).
+hipError_t slot_workspace(const Scratch* scratch, hipStream_t st, size_t sbytes, float** slots) {
+    if (!scratch) {
+        unsigned* counters = nullptr;
+        float *region = nullptr, *parts = nullptr;
+        const hipError_t e = library_workspace(st, 0, kSlotHeader + sbytes, 0, &counters, &region, &parts);
+        if (e != hipSuccess) return e;
+        *slots = (float*)((uint8_t*)region + kSlotHeader);
+        return hipSuccess;
+    }
+    if (kSlotHeader + sbytes > scratch->bytes) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_init_workspace, dim3(256), dim3(256), 0, st, (unsigned*)scratch->base, 0,
+                       (int)((kSlotHeader + sbytes) / 4));
+    *slots = (float*)(scratch->base + kSlotHeader);
+    return hipGetLastError();
 }
 
 hipError_t split_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes, size_t pbytes,
@@ -202,25 +206,35 @@ hipError_t split_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes
     return hipGetLastError();
 }
 
+// Partials that a second launch sums (no state between launches).
+hipError_t partial_workspace(const Scratch* scratch, hipStream_t st, size_t pbytes, float** parts) {
+    unsigned* counters = nullptr;
+    return split_workspace(scratch, st, 0, pbytes, &counters, parts);
+}
+
 namespace {
 
-// LDS: [0, 2048) flags: owners-done counter at 4, is-last word at 8, poison
-// word at 12 (a bounded wait gave up), unit markers of loader j for unit i at
-// 64 + 16 i + 4 j, park flag of compute wave c at 1024 + 4 c; then the units;
-// then the parked sums.
+// LDS: [0, 2048) flags: tag-check word at 4, tag-check count at 8, poison
+// word at 12 (a bounded wait gave up), unit
+// markers of loader j for unit i at 64 + 16 i + 4 j, park flag of compute wave
+// c at 1024 + 4 c; then the units; then the parked sums.
+constexpr int kSpTagCheck = 1;                          // the reader's own tag swap: 1 free, 2 taken
+constexpr int kSpTagCount = 2;                          // the reader's compute waves done with the tags
 constexpr int kSpPoison = 3;
-// Row-group counters (64-bit): arrivals in bits 0-6, split s adds bit 8 + s,
-// and a workgroup that counts itself with a poisoned result adds bit 7 too, so
-// the split that finishes last writes NaN.
-constexpr uint64_t kSpPoisonBit = 1ull << 7;
-constexpr int kSpMaxS = 56;                             // splits of a row group (one count bit each)
+constexpr int kSpMaxS = 56;                             // splits of a row group
+constexpr int kSpRq = 4;                                // quads a reader wave keeps summed before the tag check
 constexpr int kSpFlags = 2048;
 constexpr int kSpMaxUnits = (1024 - 64) / 16;
 constexpr int kSpNC = 12, kSpNL = 4;    // compute and loader waves per workgroup
 constexpr int kSpQS = 12;               // instruction slots per loader and unit
 constexpr int kSpMaxPieces = 64 * kSpNL * kSpQS;
-constexpr int kSpCounterStride = 64;    // one row-group counter per 256-byte line: no shared lines
 constexpr int kCoherent = 16;           // buffer access cache policy: sc1 (device scope: misses the L1)
+
+// Byte offset of the exchange's tags (one dword per row group: its reader's)
+// after the partial slots [S][N][Mp] fp32, at a 256-byte boundary.
+__host__ __device__ __forceinline__ int tag_offset(int S, int N, int Mp) {
+    return (int)(((int64_t)S * N * Mp * 4 + 255) & ~(int64_t)255);
+}
 
 // Buffer resource over the split partials [S][N][Mp] (fp32).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t workspace_rsrc(float* ws, int S, int N, int Mp) {
@@ -228,14 +242,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t workspace_rsrc(float* ws, int 
 }
 
 // One GEMM's share of a launch: workgroup `bid` of its grid.  SUM2: the
-// splits' partials are left for k_split_sum (a second launch) instead of being
-// counted and summed by the row group's last split.
+// splits' partials are left for k_split_sum (a second launch); otherwise
+// (slots) the row group's splits exchange them through the workspace's free
+// slots, each split summing a share of the row group (poison: the
+// workspace's poison word).
 template <int QT, int MT, bool SUM2>
 __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                            const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nt,
                                            int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux,
                                            void* __restrict__ C, int ldc, int out_f16, float* __restrict__ ws,
-                                           unsigned* __restrict__ counters, int nx, int slots) {
+                                           unsigned* __restrict__ poison, int nx, int slots) {
     constexpr int NC = kSpNC, NL = kSpNL;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -313,6 +329,17 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
     // ---------------------------------------------------------------- compute wave
     clear_flags_and_meet();
     const int c = wave - NL;
+    const bool exchange = !SUM2 && S > 1 && slots;
+    // the row group's last split (wave 0) swaps its tag from free to taken
+    // now and loads the workspace's poison word (an earlier launch's exchange
+    // that gave up leaves it set); both answers are looked at after the
+    // compute
+    uint32_t* const tags = exchange ? (uint32_t*)((uint8_t*)ws + tag_offset(S, N, Mp)) : nullptr;
+    uint32_t tag_old = kSlotFree, pword = kSlotFree;
+    if (exchange && s == S - 1 && c == 0 && lane == 0) {
+        tag_old = __hip_atomic_exchange(tags + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pword = __hip_atomic_load(poison, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     const int t = c % nt, u = c / nt;
     const int U = (NC - 1 - t) / nt + 1;                 // waves on tile t
     const Magic mg = make_magic();
@@ -371,8 +398,7 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
                 const int m4 = mt * 16 + 4 * kg;
                 if (m4 < Mp && n < N) {
                     const int off = (int)((((int64_t)s * N + n) * Mp + m4) * 4);
-                    if (SUM2 || nx > 0) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr, off, 0, 0);
-                    else __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr, off, 0, kCoherent);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt]), wr, off, 0, 0);
                 }
             }
         } else {
@@ -387,154 +413,163 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
                     }
                 }
         }
-        if (SUM2) return;
-        if (!slots) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            if (lane == 0) asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[1])), "v"(1) : "memory");
-        }
     }
-    if (SUM2 || S == 1) return;
+    if (!exchange) return;
 
-    if (slots) {
-        // --------------------------------------- counter-free exchange (slots)
-        // The row group's last split reads every split's slots (its own too)
-        // until no word is free, adds them in split order, writes C and frees
-        // the slots for the next launch; the other splits are done.
-        if (s != S - 1) return;
+    // -------------------------------------------------------- the exchange
+    // The row group's last split (s = S - 1, dispatched after the others,
+    // so it waits only for workgroups that started before it) reads every
+    // split's slots of each of its elements from its XCD's L2 until no word
+    // is free (bounded), adds them in split order (k_split_sum's order: the
+    // same bits), writes C and frees the slots for the next launch.  Each
+    // reader swapped its row group's tag from free to taken at its start: it
+    // writes C only if the swap found the tag free (a second reader of the row
+    // group does not, while the first still runs) and the workspace is not
+    // poisoned.  A missing split leaves its slots free, so the reader gives
+    // up; so does a second reader that starts after the first has freed the
+    // slots.  A reader that gives up writes NaN over all of C (a row group
+    // whose reader went missing to a duplicate's role has no other writer)
+    // and sets the workspace's poison word, after which every launch on the
+    // workspace writes NaN (a duplicated split may refill slots after the
+    // reader freed them).  Exchange plans fill whole XCD rounds (no padding
+    // workgroups), and a workgroup moved off its XCD keeps its split, so it
+    // lands on the role of another row group's same split: a missing split,
+    // or a missing reader beside a second one.
+    {
         const int rows = nt * 16, nq = rows * (Mp / 4);
         const int64_t n0 = (int64_t)rg * rows;
-        const __amdgpu_buffer_rsrc_t wr = workspace_rsrc(ws, S, N, Mp);
-        const int sstride = N * Mp * 4;                  // bytes between two splits' slots
-        const u4 freev = u4{kSlotFree, kSlotFree, kSlotFree, kSlotFree};
-        bool late = false;                               // a slot stayed free past the bound
-        for (int b = c * 64; b < nq; b += NC * 64) {
-            const int v = b + lane;
-            const int nl = v / (Mp / 4), m4 = 4 * (v - nl * (Mp / 4));
-            const bool ok = v < nq && n0 + nl < N;
-            const int off = ok ? (int)(((n0 + nl) * Mp + m4) * 4) : 0;
-            f4 sum = f4{0.f, 0.f, 0.f, 0.f};
-            for (int s0 = 0; s0 < S && !late; s0 += 4) {
-                u4 x[4];
-                for (int it = 0;; it++) {
-                    bool miss = false;
+        bool late = false;                               // give up: NaN over C
+        if (s == S - 1) {
+            const __amdgpu_buffer_rsrc_t wr = workspace_rsrc(ws, S, N, Mp);
+            const int sstride = N * Mp * 4;              // bytes between two splits' slots
+            const u4 freev = u4{kSlotFree, kSlotFree, kSlotFree, kSlotFree};
+            // wave 0 publishes its own swap's answer and the poison word (1: the
+            // tag was free and the workspace clean, 2: not) to the other waves
+            if (c == 0 && lane == 0)
+                asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kSpTagCheck])),
+                             "v"(tag_old == kSlotFree && pword == kSlotFree ? 1 : 2) : "memory");
+            // the quads this wave sums: up to kSpRq in registers, the rest written as summed
+            f4 kept[kSpRq];
+            int koff[kSpRq];
+            auto poll_sum = [&, S](int off, bool ok, f4& sum) __attribute__((always_inline)) {
+                sum = f4{0.f, 0.f, 0.f, 0.f};
+                if (late) return;
+                for (int s0 = 0; s0 < S; s0 += 4) {
+                    u4 x[4];
+                    for (int it = 0;; it++) {
+                        bool miss = false;
 #pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        x[k] = ok && s0 + k < S ? __builtin_amdgcn_raw_buffer_load_b128(wr, off + (s0 + k) * sstride, 0,
-                                                                                          kCoherent)
-                                                : u4{0u, 0u, 0u, 0u};
-                    }
+                        for (int k = 0; k < 4; k++)
+                            x[k] = ok && s0 + k < S ? __builtin_amdgcn_raw_buffer_load_b128(wr, off + (s0 + k) * sstride,
+                                                                                              0, kCoherent)
+                                                    : u4{0u, 0u, 0u, 0u};
 #pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const u4 w = x[k];
-                        miss = miss || w[0] == kSlotFree || w[1] == kSlotFree || w[2] == kSlotFree || w[3] == kSlotFree;
+                        for (int k = 0; k < 4; k++) {
+                            const u4 w = x[k];
+                            miss = miss || w[0] == kSlotFree || w[1] == kSlotFree || w[2] == kSlotFree ||
+                                   w[3] == kSlotFree;
+                        }
+                        if (__builtin_amdgcn_ballot_w64(miss) == 0) break;
+                        if (it == kDeviceWaitBound) {
+                            late = true;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
                     }
-                    if (__builtin_amdgcn_ballot_w64(miss) == 0) break;
-                    if (it == kDeviceWaitBound) {
-                        late = true;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(2);
+                    if (late) break;
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        if (s0 + k < S) sum += __builtin_bit_cast(f4, x[k]);   // splits in order
                 }
+            };
+            bool checked = false;
+            auto check_tag = [&]() __attribute__((always_inline)) {
+                if (checked) return;
+                checked = true;
+                wait_flag(&flags[kSpTagCheck], flags + kSpPoison);
+                if (flags[kSpTagCheck] != 1) late = true;
+            };
+            auto write_c = [&, S, M](int off, const f4& sum) __attribute__((always_inline)) {
+                const int q = off / 16, n = q / (Mp / 4), m4 = 4 * (q - n * (Mp / 4));
+                for (int k = 0; k < S; k++) __builtin_amdgcn_raw_buffer_store_b128(freev, wr, off + k * sstride, 0, 0);
+                const bool bad = late || poisoned(flags + kSpPoison);
 #pragma unroll
-                for (int k = 0; k < 4; k++)
-                    if (s0 + k < S) sum += __builtin_bit_cast(f4, x[k]);      // splits in order
+                for (int i = 0; i < 4; i++) {
+                    if (m4 + i >= M) break;
+                    const float y = bad ? __builtin_nanf("") : sum[i];
+                    if (out_f16) ((_Float16*)C)[(int64_t)(m4 + i) * ldc + n] = (_Float16)y;
+                    else ((float*)C)[(int64_t)(m4 + i) * ldc + n] = y;
+                }
+            };
+            // the first kSpRq quads of this wave, summed in registers (unrolled:
+            // fixed register slots), then every quad beyond them summed and
+            // written one by one after the check
+            auto quad_off = [&, nq, N](int b, bool& ok) __attribute__((always_inline)) {
+                const int v = b + lane;
+                const int nl = v / (Mp / 4), m4 = 4 * (v - nl * (Mp / 4));
+                ok = v < nq && n0 + nl < N;
+                return ok ? (int)(((n0 + nl) * Mp + m4) * 4) : 0;
+            };
+#pragma unroll
+            for (int r = 0; r < kSpRq; r++) {
+                const int b = c * 64 + r * NC * 64;
+                koff[r] = -1;
+                if (b < nq) {
+                    bool ok;
+                    const int off = quad_off(b, ok);
+                    poll_sum(off, ok, kept[r]);
+                    if (ok) koff[r] = off;
+                }
             }
-            if (!ok) continue;
-            for (int k = 0; k < S; k++) __builtin_amdgcn_raw_buffer_store_b128(freev, wr, off + k * sstride, 0, 0);
-            const bool bad = late || poisoned(flags + kSpPoison);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                if (m4 + i >= M) break;
-                const float y = bad ? __builtin_nanf("") : sum[i];
-                if (out_f16) ((_Float16*)C)[(int64_t)(m4 + i) * ldc + n0 + nl] = (_Float16)y;
-                else ((float*)C)[(int64_t)(m4 + i) * ldc + n0 + nl] = y;
+            for (int b = c * 64 + kSpRq * NC * 64; b < nq; b += NC * 64) {
+                bool ok;
+                const int off = quad_off(b, ok);
+                f4 sum;
+                poll_sum(off, ok, sum);
+                check_tag();
+                if (ok) write_c(off, sum);
             }
+            check_tag();
+#pragma unroll
+            for (int r = 0; r < kSpRq; r++)
+                if (koff[r] >= 0) write_c(koff[r], kept[r]);
+            // the last wave done frees the row group's tag
+            uint32_t seen = 0;
+            if (lane == 0)
+                asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+                             : "=v"(seen) : "v"(lds_addr(&flags[kSpTagCount])), "v"(1u) : "memory");
+            if ((uint32_t)__builtin_amdgcn_readfirstlane(seen) == (uint32_t)(NC - 1) && lane == 0)
+                __hip_atomic_store(tags + rg, kSlotFree, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        return;
-    }
-
-    // --------------------------------------------------------- cross-split sum
-    if (c == 0) {
-        wait_flags(&flags[1], 1, lane, flags + kSpPoison, min(nt, NC));
-        // the count carries this split's bit and its poison (a tile whose sums
-        // it did not see stored leaves a stale partial behind)
-        const uint64_t add = 1ull + (1ull << (8 + s)) + (poisoned(flags + kSpPoison) ? kSpPoisonBit : 0ull);
-        uint64_t old = 0;
-        uint64_t* const cnt = (uint64_t*)(counters + rg * kSpCounterStride);
-        if (lane == 0) old = __hip_atomic_fetch_add(cnt, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint64_t fin = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(old >> 32)) << 32 |
-                              (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)old)) + add;
-        const int last = (fin & 0x7Full) == (uint64_t)S;
-        if (last && lane == 0) __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // 1: last and clean, 3: last with a poisoned or repeated split, 2: not last
-        const int word = !last ? 2 : fin == ((uint64_t)S | (((1ull << S) - 1ull) << 8)) ? 1 : 3;
-        if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[2])), "v"(word) : "memory");
-    }
-    wait_flags(&flags[2], 1, lane, flags + kSpPoison);
-    const int word = flags[2];
-    if (word != 1 && word != 3) return;
-    const bool bad = word == 3 || poisoned(flags + kSpPoison);
-    // each lane takes up to four quads (one row n, rows m4 .. m4+3) at a time and
-    // issues all of their partial loads (up to 16) before the first add
-    const int rows = nt * 16, nq = rows * (Mp / 4);
-    const int64_t n0 = (int64_t)rg * rows;
-    const __amdgpu_buffer_rsrc_t wr = workspace_rsrc(ws, S, N, Mp);
-    for (int v0 = c * 64 + lane; v0 < nq; v0 += 4 * NC * 64) {
-        int off[4];
-        bool ok[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int v = v0 + q * NC * 64;
-            const int nl = v / (Mp / 4), m4 = 4 * (v - nl * (Mp / 4));
-            ok[q] = v < nq && n0 + nl < N;
-            off[q] = ok[q] ? (int)(((n0 + nl) * Mp + m4) * 4) : 0;
-        }
-        f4 sum[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) sum[q] = f4{0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < S; s0 += 4) {
-            f4 x[4][4];
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    x[q][k] = ok[q] && s0 + k < S
-                                  ? __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                               wr, off[q] + (int)((int64_t)(s0 + k) * N * Mp * 4), 0,
-                                                               kCoherent))
-                                  : f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    if (s0 + k < S) sum[q] += x[q][k];           // splits in order
-        }
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            if (!ok[q]) continue;
-            const int v = v0 + q * NC * 64;
-            const int nl = v / (Mp / 4), m4 = 4 * (v - nl * (Mp / 4));
-            const int64_t n = n0 + nl;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                if (m4 + i >= M) break;
-                const float y = bad ? __builtin_nanf("") : sum[q][i];
-                if (out_f16) ((_Float16*)C)[(int64_t)(m4 + i) * ldc + n] = (_Float16)y;
-                else ((float*)C)[(int64_t)(m4 + i) * ldc + n] = y;
+        if (late) {
+            // NaN over all of C: a row group whose reader went missing has no other writer
+            for (int64_t e = lane; e < (int64_t)M * N; e += 64) {
+                const int64_t m = e / N, n = e - m * N;
+                if (out_f16) ((_Float16*)C)[m * ldc + n] = (_Float16)__builtin_nanf("");
+                else ((float*)C)[m * ldc + n] = __builtin_nanf("");
             }
+            if (lane == 0) __hip_atomic_store(poison, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
 
+// The single-launch kernel's arguments fit in the 14 dwords preloaded into
+// SGPRs at wave launch (no scalar load of an argument, which the first wait
+// for the flags' LDS writes would also wait for, queued behind the weight
+// stream): X = N | (M - 1) << 24 | out_f16 << 29 | slots << 30, Y = K / 256 |
+// nt << 12 | S << 16 | nx << 22 (split_packed_args); the workspace's poison
+// word sits kSlotHeader bytes before the slots.
 template <int QT, int MT, bool SUM2>
-__global__ __launch_bounds__(64 * (kSpNC + kSpNL))
-void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, int lda, int M, int N, int K,
-                  int nt, int S, int nsgS, int unit_bytes, const uint8_t* __restrict__ Waux, void* __restrict__ C,
-                  int ldc, int out_f16, float* __restrict__ ws, unsigned* __restrict__ counters, int nx,
-                  int slots) {
+__global__ __launch_bounds__(64 * (kSpNC + kSpNL)) __attribute__((amdgpu_waves_per_eu(1, 4)))
+void k_gemm_split(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, const uint8_t* __restrict__ Waux,
+                  void* __restrict__ C, float* __restrict__ ws, int lda, int ldc, uint32_t X, uint32_t Y) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    split_body<QT, MT, SUM2>((int)blockIdx.x, lds, W, A, lda, M, N, K, nt, S, nsgS, unit_bytes, Waux, C, ldc, out_f16,
-                             ws, counters, nx, slots);
+    const int N = (int)(X & 0xFFFFFFu), M = (int)((X >> 24) & 31u) + 1, out_f16 = (int)((X >> 29) & 1u);
+    const int slots = (int)((X >> 30) & 1u);
+    const int nsg = (int)(Y & 0xFFFu), nt = (int)((Y >> 12) & 15u), S = (int)((Y >> 16) & 63u), nx = (int)((Y >> 22) & 31u);
+    unsigned* const poison = slots ? (unsigned*)((uint8_t*)ws - kSlotHeader) : nullptr;
+    split_body<QT, MT, SUM2>((int)blockIdx.x, lds, W, A, lda, M, N, nsg << 8, nt, S, nsg / S, (M * 33 + nt * 144) * 16,
+                             Waux, C, ldc, out_f16, ws, poison, nx, slots);
 }
 
 // C of a single K-split launch: the S partials [s][n][Mp] of each element
@@ -586,17 +621,17 @@ struct SplitJob {
     const uint16_t* A;
     void* C;
     float* ws;
-    unsigned* counters;
     int lda, ldc, M, N, K, nt, S, nsgS, unit_bytes, grid0;
 };
 struct SplitJobs {
     SplitJob job[kSpMaxJobs];
+    unsigned* poison;                    // the workspace's poison word (the slots' header)
     int n, out_f16, nx;                  // nx: XCD-local exchange (every job's grid0 a multiple of nx)
-    int slots;                           // counter-free exchange through free slots
+    int slots;                           // the shared exchange through free slots
 };
 
 template <int QT, int MT>
-__global__ __launch_bounds__(64 * (kSpNC + kSpNL))
+__global__ __launch_bounds__(64 * (kSpNC + kSpNL)) __attribute__((amdgpu_waves_per_eu(1, 4)))
 void k_gemm_split_batched(const SplitJobs jobs) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     // the last job whose grid starts at or before this workgroup (uniform
@@ -605,8 +640,12 @@ void k_gemm_split_batched(const SplitJobs jobs) {
 #pragma unroll
     for (int i = 1; i < kSpMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
-    split_body<QT, MT, false>((int)blockIdx.x - j.grid0, lds, j.W, j.A, j.lda, j.M, j.N, j.K, j.nt, j.S, j.nsgS,
-                       j.unit_bytes, j.Waux, j.C, j.ldc, jobs.out_f16, j.ws, j.counters, jobs.nx, jobs.slots);
+    // (read into SGPRs one by one: kept as a struct, a field was once
+    // spilled to scratch and reloaded through a selected address)
+    const auto u = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+    split_body<QT, MT, false>((int)blockIdx.x - u(j.grid0), lds, j.W, j.A, u(j.lda), u(j.M), u(j.N), u(j.K), u(j.nt),
+                              u(j.S), u(j.nsgS), u(j.unit_bytes), j.Waux, j.C, u(j.ldc), jobs.out_f16, j.ws,
+                              jobs.poison, jobs.nx, jobs.slots);
 }
 
 
@@ -626,6 +665,8 @@ int split_lds_bytes(int M, int nt, int nsgS, int MT) {
 // ceil(rgs / nx) * nx row groups (whole rounds of the XCD round robin).
 bool plan_split(const GemmArgs& g, SplitPlan& p, int nx) {
     if (g.M > 32 || g.K % 256) return false;
+    if (g.N >= (1 << 24) || g.K / 256 > 0xFFF) return false;            // the packed kernel arguments
+    if (nx > 31) nx = 0;
     if ((int64_t)g.K / 256 * g.N * 32 * 4 >= (1LL << 31)) return false;   // partials addressed by 32-bit offsets
     const int nsg = g.K / 256, T = (g.N + 15) / 16;
     const int MT = g.M <= 16 ? 1 : 2;
@@ -655,28 +696,42 @@ bool plan_split(const GemmArgs& g, SplitPlan& p, int nx) {
     return best < 1e300;
 }
 
-// Workspace of one K-split GEMM: row-group counters (256 bytes each, kept zero
-// between launches by the kernel) then the partials [S][N][Mp], at 256-byte
-// offsets.  0 when the plan does not split K.
-size_t counter_bytes(const SplitPlan& p) { return p.S > 1 ? (size_t)p.rgs * kSpCounterStride * 4 : 0; }
+// Partials of one K-split GEMM, [S][N][Mp] fp32 (0 when the plan does not
+// split K), rounded up to 256 bytes.
 size_t partial_bytes(const GemmArgs& g, const SplitPlan& p) {
     return p.S > 1 ? ((size_t)p.S * g.N * ((g.M + 3) & ~3) * 4 + 255) & ~(size_t)255 : 0;
 }
 
-// A single launch's splits are summed by k_split_sum (a second launch) when its
-// grid takes more than one workgroup per CU: the row groups' last splits then
-// run in the last round and sum after everyone else (17408x5120 at M = 9-16:
-// 24-25 -> 22.5 us).  In one round the in-kernel sum is cheaper than the second
-// launch (5120^2 at M = 16-32: 10.3-11.6 against 11.3-12.0 us).
-bool split_sum2(const SplitPlan& p) {
-    const int cus = device_cus();
-    return p.S > 1 && p.grid > (cus > 0 ? cus : 256);
+// The exchange's slots of one K-split GEMM: its partials, then its readers' tags.
+size_t slot_bytes(const GemmArgs& g, const SplitPlan& p) {
+    if (p.S <= 1) return 0;
+    return (size_t)tag_offset(p.S, g.N, (g.M + 3) & ~3) + (((size_t)p.rgs * 4 + 255) & ~(size_t)255);
 }
 
-// The in-kernel exchange goes through free slots (no counter round trip) where
-// the splits of a row group share an XCD's L2 and the library's workspace is
-// used; with a caller's scratch (no slot region) it counts arrivals.
-bool use_slots(const SplitPlan& p, const Scratch* scratch) { return !scratch && p.nx > 0 && p.S > 1; }
+// A single launch's splits are summed by k_split_sum (a second launch) where
+// the XCD count is unknown (no XCD-local exchange), where the row groups do not
+// fill whole XCD rounds (the exchange's placement check needs every workgroup
+// to hold a role: no padding), and where the grid takes two or more full
+// rounds of one workgroup per CU: the row groups' readers then
+// run after everyone else (17408x5120 at M = 16, 512 workgroups: 23.1 against
+// 23.8-24.3 us in the kernel).  A grid of more than one round but less than two
+// keeps the exchange in the kernel (7168x5120 at M = 32, 448 workgroups: 17.9
+// -> 17.1 us), and so does one round (5120^2 at M = 16-32: the second launch
+// cost 0.4-1 us).
+bool split_second_launch(const SplitPlan& p) {
+    const int cus = device_cus() > 0 ? device_cus() : 256;
+    return p.S > 1 && (p.nx == 0 || p.rgs % p.nx != 0 || p.grid >= 2 * cus);
+}
+
+// The single-launch kernel's packed arguments (k_gemm_split).
+bool split_packed_args(const GemmArgs& g, const SplitPlan& p, int slots, uint32_t& X, uint32_t& Y) {
+    if (g.N < 1 || g.N >= (1 << 24) || g.M < 1 || g.M > 32 || g.K / 256 > 0xFFF || p.nt > 15 || p.S > 63 ||
+        p.nx > 31)
+        return false;
+    X = (uint32_t)g.N | (uint32_t)(g.M - 1) << 24 | (uint32_t)(g.out_f16 ? 1 : 0) << 29 | (uint32_t)(slots ? 1 : 0) << 30;
+    Y = (uint32_t)(g.K / 256) | (uint32_t)p.nt << 12 | (uint32_t)p.S << 16 | (uint32_t)p.nx << 22;
+    return true;
+}
 
 template <int QT, int MT, bool SUM2>
 hipError_t launch_split_k(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
@@ -691,17 +746,17 @@ hipError_t launch_split_k(const GemmArgs& g, const SplitPlan& p, const Scratch* 
         if (e != hipSuccess) return e;
         attr_set.fetch_or(bit, std::memory_order_acq_rel);
     }
-    unsigned* counters = nullptr;
     float* parts = nullptr;
-    const int slots = use_slots(p, scratch) && !SUM2;
+    const int slots = !SUM2 && p.S > 1;
     if (p.S > 1) {
-        // summed by k_split_sum: partials only, no counters
-        e = slots ? slot_workspace(st, partial_bytes(g, p), &parts)
-                  : split_workspace(scratch, st, SUM2 ? 0 : counter_bytes(p), partial_bytes(g, p), &counters, &parts);
+        e = slots ? slot_workspace(scratch, st, slot_bytes(g, p), &parts)
+                  : partial_workspace(scratch, st, partial_bytes(g, p), &parts);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kSpNC + kSpNL)), p.lds, st, g.W, g.A, g.lda, g.M, g.N, g.K,
-                       p.nt, p.S, p.nsgS, p.unit_bytes, g.Waux, g.C, g.ldc, g.out_f16, parts, counters, p.nx, slots);
+    uint32_t X = 0, Y = 0;
+    if (!split_packed_args(g, p, slots, X, Y)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k, dim3(p.grid), dim3(64 * (kSpNC + kSpNL)), p.lds, st, g.W, g.A, g.Waux, g.C, parts, g.lda,
+                       g.ldc, X, Y);
     e = hipGetLastError();
     if (e != hipSuccess || !SUM2) return e;
     hipLaunchKernelGGL(k_split_sum, dim3((g.N + 31) / 32), dim3(256), 0, st, (const float*)parts, g.C, g.ldc,
@@ -709,20 +764,10 @@ hipError_t launch_split_k(const GemmArgs& g, const SplitPlan& p, const Scratch* 
     return hipGetLastError();
 }
 
-// Whether a single launch leaves its splits to k_split_sum: grids of more
-// than one round but less than two keep the counter-free exchange in the
-// kernel where it is available (7168x5120 at M = 32, 448 workgroups: 17.9 ->
-// 17.1 us); from two full rounds on a second launch (17408x5120 at M = 16,
-// 512 workgroups: 23.1 against 23.8-24.3 us in the kernel).
-bool split_second_launch(const SplitPlan& p, const Scratch* scratch) {
-    const int cus = device_cus() > 0 ? device_cus() : 256;
-    return split_sum2(p) && (!use_slots(p, scratch) || p.grid >= 2 * cus);
-}
-
 template <int QT, int MT>
 hipError_t launch_split(const GemmArgs& g, const SplitPlan& p, const Scratch* scratch, hipStream_t st) {
-    return split_second_launch(p, scratch) ? launch_split_k<QT, MT, true>(g, p, scratch, st)
-                                           : launch_split_k<QT, MT, false>(g, p, scratch, st);
+    return split_second_launch(p) ? launch_split_k<QT, MT, true>(g, p, scratch, st)
+                                  : launch_split_k<QT, MT, false>(g, p, scratch, st);
 }
 
 template <int QT>
@@ -745,37 +790,36 @@ hipError_t launch_split_batched(const GemmArgs* gs, const SplitPlan* ps, int n, 
         if (e != hipSuccess) return e;
         attr_set.fetch_or(bit, std::memory_order_acq_rel);
     }
-    // one workspace for the launch: every job's counters (kept zero between
-    // launches), then every job's partials, at 256-byte offsets
-    size_t cb[kSpMaxJobs] = {}, pb[kSpMaxJobs] = {}, ctot = 0, ptot = 0;
+    // one workspace for the launch: the poison word's header, then every
+    // job's partial slots at 256-byte offsets
+    size_t pb[kSpMaxJobs] = {}, ptot = 0;
+    bool any = false;
     for (int i = 0; i < n; i++) {
-        cb[i] = counter_bytes(ps[i]);
-        pb[i] = partial_bytes(gs[i], ps[i]);
-        ctot += cb[i];
+        pb[i] = slot_bytes(gs[i], ps[i]);
         ptot += pb[i];
+        any = any || ps[i].S > 1;
     }
-    unsigned* counters = nullptr;
     float* parts = nullptr;
-    const bool slots = !scratch && nx > 0;
-    if (ctot) {
-        e = slots ? slot_workspace(st, ptot, &parts) : split_workspace(scratch, st, ctot, ptot, &counters, &parts);
+    unsigned* poison = nullptr;
+    if (any) {
+        if (nx == 0) return hipErrorInvalidValue;        // no XCD-local exchange: split_batched_supports refuses
+        e = slot_workspace(scratch, st, ptot, &parts);
         if (e != hipSuccess) return e;
+        poison = (unsigned*)((uint8_t*)parts - kSlotHeader);
     }
     SplitJobs jobs = {};
     jobs.n = n;
     jobs.out_f16 = gs[0].out_f16;
     jobs.nx = nx;
-    jobs.slots = slots;
+    jobs.slots = any;
+    jobs.poison = poison;
     int grid = 0, lds = 0;
-    size_t co = 0, po = 0;
+    size_t po = 0;
     for (int i = 0; i < n; i++) {
         const GemmArgs& g = gs[i];
         const SplitPlan& p = ps[i];
-        jobs.job[i] = SplitJob{g.W, g.Waux, g.A, g.C,
-                               p.S > 1 ? (float*)((uint8_t*)parts + po) : nullptr,
-                               p.S > 1 && !slots ? (unsigned*)((uint8_t*)counters + co) : nullptr,
+        jobs.job[i] = SplitJob{g.W, g.Waux, g.A, g.C, p.S > 1 ? (float*)((uint8_t*)parts + po) : nullptr,
                                g.lda, g.ldc, g.M, g.N, g.K, p.nt, p.S, p.nsgS, p.unit_bytes, grid};
-        co += cb[i];
         po += pb[i];
         // with the XCD-local exchange every job starts on XCD 0 (its grid is
         // padded to whole rounds of the XCD round robin; for S = 1 the padding
@@ -797,45 +841,42 @@ bool split_supports(const GemmArgs& g) {
 
 size_t split_scratch_bytes(const GemmArgs& g) {
     SplitPlan p;
-    if (!plan_split(g, p, device_xcds())) return 0;
-    return (split_sum2(p) ? 0 : counter_bytes(p)) + partial_bytes(g, p);
+    if (!plan_split(g, p, device_xcds()) || p.S <= 1) return 0;
+    return split_second_launch(p) ? partial_bytes(g, p) : kSlotHeader + slot_bytes(g, p);
 }
 
 WsNeed split_ws_need(const GemmArgs& g) {
     WsNeed w;
     SplitPlan p;
     if (!plan_split(g, p, device_xcds()) || p.S <= 1) return w;
-    if (split_second_launch(p, nullptr)) w.p = partial_bytes(g, p);
-    else if (use_slots(p, nullptr)) w.s = partial_bytes(g, p);
-    else {
-        w.c = counter_bytes(p);
-        w.p = partial_bytes(g, p);
-    }
+    if (split_second_launch(p)) w.p = partial_bytes(g, p);
+    else w.s = kSlotHeader + slot_bytes(g, p);
     return w;
+}
+
+// The slots one launch of gemm_split_batched takes for each launch of up to
+// kSpMaxJobs GEMMs (the header, then every job's partials side by side); the
+// largest of them.
+size_t split_batched_slot_bytes(const GemmArgs* gs, int n) {
+    const int nx = device_xcds();
+    size_t worst = 0;
+    for (int i0 = 0; i0 < n; i0 += kSpMaxJobs) {
+        size_t tot = 0;
+        bool any = false;
+        for (int i = i0; i < std::min(n, i0 + kSpMaxJobs); i++) {
+            SplitPlan p;
+            if (!plan_split(gs[i], p, nx)) continue;
+            tot += slot_bytes(gs[i], p);
+            any = any || p.S > 1;
+        }
+        if (any) worst = std::max(worst, kSlotHeader + tot);
+    }
+    return worst;
 }
 
 WsNeed split_batched_ws_need(const GemmArgs* gs, int n) {
     WsNeed w;
-    const int nx = device_xcds();
-    for (int i0 = 0; i0 < n; i0 += kSpMaxJobs) {
-        size_t ctot = 0, ptot = 0;
-        int bnx = 0;
-        for (int i = i0; i < std::min(n, i0 + kSpMaxJobs); i++) {
-            SplitPlan p;
-            if (!plan_split(gs[i], p, nx)) continue;
-            ctot += counter_bytes(p);
-            ptot += partial_bytes(gs[i], p);
-            if (p.nx) bnx = p.nx;
-        }
-        if (!ctot) continue;
-        WsNeed one;
-        if (bnx > 0) one.s = ptot;
-        else {
-            one.c = ctot;
-            one.p = ptot;
-        }
-        w.merge(one);
-    }
+    w.s = split_batched_slot_bytes(gs, n);
     return w;
 }
 
@@ -848,23 +889,13 @@ bool split_batched_supports(const GemmArgs* gs, int n) {
         if ((gs[i].M <= 16) != (gs[0].M <= 16)) return false;      // one m-tile count per launch
         if (gs[i].qtype == QT_PLANES && ((uintptr_t)gs[i].Waux & 15)) return false;
         if (!plan_split(gs[i], p, nx)) return false;
+        // the exchange needs the XCD round robin, and whole rounds of row groups
+        if (p.S > 1 && (p.nx == 0 || p.rgs % p.nx != 0)) return false;
     }
     return true;
 }
 
-size_t split_batched_scratch_bytes(const GemmArgs* gs, int n) {
-    const int nx = device_xcds();
-    size_t worst = 0;
-    for (int i0 = 0; i0 < n; i0 += kSpMaxJobs) {
-        size_t tot = 0;
-        for (int i = i0; i < std::min(n, i0 + kSpMaxJobs); i++) {
-            SplitPlan p;
-            if (plan_split(gs[i], p, nx)) tot += counter_bytes(p) + partial_bytes(gs[i], p);
-        }
-        worst = std::max(worst, tot);
-    }
-    return worst;
-}
+size_t split_batched_scratch_bytes(const GemmArgs* gs, int n) { return split_batched_slot_bytes(gs, n); }
 
 hipError_t gemm_split_batched(const GemmArgs* gs, int n, const Scratch* scratch, hipStream_t st) {
     if (!split_batched_supports(gs, n)) return hipErrorInvalidValue;

@@ -1,23 +1,41 @@
-"""The K-split kernel's counter-free exchange (bus-fill_amd/csrc/bf_gemm_split.hip)
-modelled on the CPU, for every plan its planner makes over a grid of shapes:
+"""The K-split kernel's exchange (bus-fill_amd/csrc/bf_gemm_split.hip)
+modelled on the CPU, for every plan its planner makes over a grid of shapes.
 
-* roles: with the dispatcher handing workgroups to the 8 XCDs round robin from
+* Roles: with the dispatcher handing workgroups to the 8 XCDs round robin from
   any starting XCD, each workgroup's (row group, split) taken from the XCD it
-  runs on and its round covers every (row group, split) exactly once, and all
-  splits of a row group sit on one XCD (one L2);
-* slots: the words the splits store (tile-first waves: rows of their tiles,
+  runs on and its round covers every (row group, split) exactly once, all
+  splits of a row group sit on one XCD (one L2), every workgroup sees the same
+  placement offset, and the last split of a row group is its last-dispatched
+  workgroup (the reader waits only for workgroups that started before it).
+  Exchange plans fill whole XCD rounds (no padding workgroups).
+* Slots: the words the splits store (tile-first waves: rows of their tiles,
   whole batch-row quads) are exactly the words the row group's last split
-  reads and frees, and that split writes every C element of its row group
-  once;
-* the workspace invariant: over a sequence of launches of different shapes
-  (single and batched, each GEMM's slots at its own 256-byte offset) every
-  slot read holds a written partial, and the region is all free again after
-  each launch, so no launch can read a stale partial of an earlier one.
+  reads and frees, and it writes every C element of its row group once.
+* The workspace invariant: over a sequence of launches of different shapes,
+  placed round robin from any starting XCD, under random interleavings of
+  the workgroups' steps, every C element is correct and the region (slots and
+  tags) is all free again after each launch.
+* Broken placements -- a duplicated split, a missing split, a missing last
+  split, an XCD that gets no workgroup, a dispatcher that skips one XCD once
+  (every later workgroup shifted by one), single workgroups moved to another
+  XCD, random placements -- under random interleavings (late duplicates
+  included): every C element ends correct or NaN, never stale or wrong; the
+  call's output holds NaN and the workspace's poison word is set; every later
+  launch on the workspace writes NaN.  A moved workgroup keeps its split, so
+  it takes another row group's role of the same split: a row group then misses
+  that split (its reader gives up) or, for the last split, has a second reader
+  (caught by the reader's tag swap, or by its poll of slots the first reader
+  freed).  Not caught: every one of a row group's splits moved onto the same
+  other row group, the duplicates running only after that row group's first
+  reader has finished; the test below checks that moving all but one of them
+  is caught.
 
-Plans with planted mistakes (a reader that rounds the batch rows down, a
-planner whose XCD count differs from the dispatcher's) must each be caught.
-The index arithmetic restates the kernel's (split_body: roles, the partial
-stores of the tile's first wave, the last split's reads)."""
+Planted mistakes (a reader that rounds the batch rows down, roles laid out
+for 4 XCDs on 8, a give-up that writes NaN over its own row group only, a
+reader that skips the tag check) must each be caught.  The index arithmetic
+and the steps restate the kernel's (split_body: roles, the reader's tag swap
+at its start, the partial stores of the tile's first wave, the last split's
+reads, the give-up, which writes NaN over all of C)."""
 import numpy as np
 import pytest
 
@@ -26,6 +44,7 @@ MAX_UNITS = (1024 - 64) // 16     # kSpMaxUnits
 MAX_PIECES = 64 * 4 * 12          # kSpMaxPieces
 MAX_LDS = 160 * 1024
 MAX_S = 56
+CUS = 256
 
 
 def lds_bytes(M, nt, nsgS, MT):
@@ -36,7 +55,7 @@ def lds_bytes(M, nt, nsgS, MT):
 
 def plan(M, N, K, nx=NX):
     """plan_split: (S, nt, nsgS, MT, grid, rgs) or None."""
-    if M > 32 or K % 256:
+    if M > 32 or K % 256 or N >= 1 << 24 or K // 256 > 0xFFF:
         return None
     nsg, T = K // 256, (N + 15) // 16
     MT = 1 if M <= 16 else 2
@@ -62,16 +81,27 @@ def plan(M, N, K, nx=NX):
     return p
 
 
-def roles(grid, S, nt, N, start, nx_plan=NX, nx_hw=NX):
-    """(rg, s) of every workgroup that works, for a dispatcher starting at XCD `start`."""
+def in_kernel_exchange(p):
+    """split_second_launch is false: the splits exchange in the kernel."""
+    S, nt, nsgS, MT, grid, rgs = p
+    return S > 1 and grid < 2 * CUS and rgs % NX == 0
+
+
+def round_robin(start, nx=NX):
+    return lambda b: (b + start) % nx
+
+
+def roles(grid, S, nt, N, xcd_of, nx_plan=NX):
+    """(b, rg, s, place) of every workgroup that works (the kernel's role and
+    placement offset from the XCD it runs on)."""
     out = []
     for b in range(grid):
-        x = (b + start) % nx_hw % nx_plan
+        x = xcd_of(b) % nx_plan
         jx = b // nx_plan
         q = jx // S
         rg, s = x + nx_plan * q, jx - q * S
         if rg * nt * 16 < N:
-            out.append((rg, s, (b + start) % nx_hw))
+            out.append((b, rg, s, (x - b % nx_plan) % nx_plan))
     return out
 
 
@@ -86,12 +116,14 @@ def written(rg, s, nt, MT, M, N):
 
 
 def read_by_last(rg, S, nt, M, N, mp_round=lambda M: (M + 3) & ~3):
-    """Slot words the last split reads (and frees), and the C elements it writes."""
+    """Quads (n, m4) the row group's last split reads (all S slots of each)
+    and frees, and the C elements (m, n) it writes, as its compute waves'
+    loop visits them."""
     Mp = mp_round(M)
     rows = nt * 16
     nq = rows * (Mp // 4)
     n0 = rg * rows
-    reads, cs = set(), []
+    quads, cs = [], []
     for c in range(NC):
         for b in range(c * 64, nq, NC * 64):
             v = b + np.arange(64)
@@ -99,41 +131,45 @@ def read_by_last(rg, S, nt, M, N, mp_round=lambda M: (M + 3) & ~3):
             m4 = 4 * (v - nl * (Mp // 4))
             ok = (v < nq) & (n0 + nl < N)
             for a, m in zip(nl[ok], m4[ok]):
-                for s in range(S):
-                    reads.add((s, int(n0 + a), int(m)))
-                for i in range(4):
-                    if m + i < M:
-                        cs.append((int(m + i), int(n0 + a)))
-    return reads, cs
+                quads.append((int(n0 + a), int(m)))
+                cs += [(int(m + i), int(n0 + a)) for i in range(4) if m + i < M]
+    return quads, cs
 
 
 SHAPES = [(M, N, K) for M in (9, 16, 17, 31, 32) for N in (200, 1000, 5120) for K in (2048, 5120)] + \
-    [(32, 7168, 5120), (13, 17408, 5120), (16, 5120, 17408), (20, 3000, 4096)]
+    [(32, 7168, 5120), (13, 17408, 5120), (16, 5120, 17408), (20, 3000, 4096), (24, 4096, 4096), (12, 8192, 4096),
+     (32, 1024, 8192), (20, 2560, 2560)]
 
 
 def exchange_plans():
     out = []
     for M, N, K in SHAPES:
         p = plan(M, N, K)
-        if p and p[0] > 1:
+        if p and in_kernel_exchange(p):
             out.append((M, N, K) + p)
     return out
 
 
 def check_plan(M, N, K, S, nt, nsgS, MT, grid, rgs, mp_round=lambda M: (M + 3) & ~3, nx_plan=NX):
     """Raise AssertionError on the first broken invariant."""
+    assert grid == rgs * S, ("padding workgroups", grid, rgs, S)
     for start in range(NX):
-        got = roles(grid, S, nt, N, start, nx_plan=nx_plan)
-        pairs = sorted((rg, s) for rg, s, _ in got)
+        got = roles(grid, S, nt, N, round_robin(start), nx_plan=nx_plan)
+        pairs = sorted((rg, s) for _, rg, s, _ in got)
         assert pairs == [(rg, s) for rg in range(rgs) for s in range(S)], ("roles", start)
-        for rg, s, xcd in got:
-            assert xcd == rg % NX, ("row group off its XCD", rg, s, xcd)
+        assert len({pl for *_, pl in got}) == 1, ("placement offsets differ", start)
+        last = {}
+        for b, rg, s, _ in got:
+            assert round_robin(start)(b) == rg % NX, ("row group off its XCD", rg, s)
+            last[rg] = max(last.get(rg, (-1, -1)), (b, s))
+        assert all(s == S - 1 for _, s in last.values()), "the reader is not its row group's last workgroup"
     cover = []
     for rg in range(rgs):
         w = set()
         for s in range(S):
             w |= written(rg, s, nt, MT, M, N)
-        r, cs = read_by_last(rg, S, nt, M, N, mp_round)
+        quads, cs = read_by_last(rg, S, nt, M, N, mp_round)
+        r = {(ss, n, m4) for n, m4 in quads for ss in range(S)}
         assert r == w, ("slots written != slots read", rg, len(w), len(r))
         cover += cs
     assert len(cover) == len(set(cover)) == M * N, ("C coverage", len(cover), len(set(cover)), M * N)
@@ -141,7 +177,7 @@ def check_plan(M, N, K, S, nt, nsgS, MT, grid, rgs, mp_round=lambda M: (M + 3) &
 
 def test_planner_makes_exchange_plans():
     plans = exchange_plans()
-    assert len(plans) >= 20, plans
+    assert len(plans) >= 16, plans
     assert len({p[3] for p in plans}) >= 3, plans     # several split counts
 
 
@@ -150,39 +186,205 @@ def test_exchange_plan(p):
     check_plan(*p)
 
 
-def test_workspace_stays_free_across_launches():
-    """A sequence of single and batched launches over one slot region: every
-    read sees a written partial and every launch leaves the region free."""
-    FREE = -1
-    plans = exchange_plans()
+# ------------------------------------------------------------------ the protocol, step by step
+FREE = None
+
+
+class Workspace:
+    """The slot region (slots and the readers' tags; absent = free) and its poison word."""
+
+    def __init__(self):
+        self.slots, self.tags, self.poisoned = {}, {}, False
+
+    def free(self):
+        return not self.slots and not self.tags
+
+
+def run_launch(ws, job, launch_id, xcd_of, rng, give_up_all=True, check_tags=True):
+    """One launch of one GEMM through the exchange, its workgroups' steps
+    interleaved at random (a reader's poll is taken only when its slots are
+    all there, or when nothing else can run: then it gives up).  Returns C, a
+    dict (m, n) -> "ok" | "nan" | "stale" | "wrong"."""
+    M, N, K, S, nt, nsgS, MT, grid, rgs = job
+    C = {(m, n): "stale" for m in range(M) for n in range(N)}
+    sticky = ws.poisoned
+
+    def give_up(rg):
+        for e in (list(C) if give_up_all else
+                  [e for e in C if rg * nt * 16 <= e[1] < (rg + 1) * nt * 16]):
+            C[e] = "nan"
+        ws.poisoned = True
+
+    def writer(b, rg, s, place):
+        yield
+        for w in written(rg, s, nt, MT, M, N):                  # the partial stores
+            ws.slots[w] = launch_id
+
+    def reader(b, rg, s, place):
+        old = ws.tags.get(rg, FREE)                             # the tag swap at the start
+        ws.tags[rg] = "taken"
+        yield
+        for w in written(rg, s, nt, MT, M, N):                  # its own partial stores
+            ws.slots[w] = launch_id
+        yield
+        quads, cs = read_by_last(rg, S, nt, M, N)
+        late = False
+        while any(ws.slots.get((ss, n, m4)) is FREE for n, m4 in quads for ss in range(S)):
+            yield "wait"                                        # the bounded poll
+            if state["stuck"]:
+                late = True
+                break
+        vals = [ws.slots.get((ss, n, m4)) for n, m4 in quads for ss in range(S)]
+        yield
+        if not late and check_tags and (old is not FREE or sticky):   # own swap, poison word
+            late = True
+        if not check_tags and sticky:
+            late = True
+        for n, m4 in quads:                                     # write C, free the slots
+            for ss in range(S):
+                ws.slots.pop((ss, n, m4), None)
+        fresh = all(v == launch_id for v in vals)
+        for e in cs:
+            C[e] = "nan" if late else ("ok" if fresh else "wrong")
+        ws.tags.pop(rg, None)                                   # the last wave frees the tag
+        if late:
+            give_up(rg)
+
+    present = roles(grid, S, nt, N, xcd_of)
+    gens = [(writer if s < S - 1 else reader)(b, rg, s, place) for b, rg, s, place in present]
+    # workgroups start in dispatch order (a random prefix of them may be
+    # running); a waiting reader wakes when another step made progress, and
+    # gives up only when nothing else can run
+    state = {"stuck": False}
+    active, waiting = [], []
+    pending = list(gens)
+    while pending or active or waiting:
+        while pending and (not active or rng.random() < 0.3):
+            active.append(pending.pop(0))
+        if not active:
+            state["stuck"] = True
+            active, waiting = waiting, []
+        g = active.pop(int(rng.integers(len(active))))
+        try:
+            r = next(g)
+        except StopIteration:
+            r = "done"
+        if r == "wait" and not state["stuck"]:
+            waiting.append(g)
+            continue
+        if r != "done":
+            active.append(g)
+        if r != "wait":
+            state["stuck"] = False
+            active.extend(waiting)
+            waiting.clear()
+    return C
+
+
+def broken_placements(job, rng):
+    """xcd_of functions that are not round robin, with a name."""
+    M, N, K, S, nt, nsgS, MT, grid, rgs = job
+    rr = round_robin(0)
+    out = []
+    # a duplicated split (and so a missing one): workgroup 0 on workgroup 1's XCD
+    out.append(("duplicate", lambda b: rr(1) if b == 0 else rr(b)))
+    # the last split of row group 0 missing: its workgroup lands on the XCD of the next one
+    last = next(b for b, rg, s, _ in roles(grid, S, nt, N, rr) if rg == 0 and s == S - 1)
+    out.append(("missing last split", lambda b, last=last: rr(last + 1) if b == last else rr(b)))
+    # an XCD that gets no workgroup (the dispatcher round robin over 7 of 8)
+    out.append(("XCD 3 skipped", lambda b: [0, 1, 2, 4, 5, 6, 7][b % 7]))
+    # the dispatcher skips one XCD once inside a round of NX workgroups: every
+    # workgroup from k on one XCD further (a skip between rounds only changes
+    # the placement offset: a valid placement)
+    k = int(rng.integers(0, grid // NX)) * NX + int(rng.integers(1, NX))
+    out.append(("one skip", lambda b, k=k: rr(b + 1) if b >= k else rr(b)))
+    # single workgroups moved to another XCD
+    for b0, d in zip(rng.integers(0, grid, size=3), rng.integers(1, NX, size=3)):
+        out.append((f"moved {int(b0)}+{int(d)}",
+                    lambda b, b0=int(b0), d=int(d): rr(b + d) if b == b0 else rr(b)))
+    perm = [int(x) for x in rng.integers(0, NX, size=grid)]
+    out.append(("random", lambda b, perm=perm: perm[b]))
+    return out
+
+
+def small_jobs(count=2):
+    """The smallest exchange plans (step-by-step simulation), several split
+    counts among them."""
+    plans = sorted(exchange_plans(), key=lambda p: p[0] * p[1])
+    out = []
+    for p in plans:
+        if len(out) < count and (p[3], p[4]) not in {(q[3], q[4]) for q in out}:
+            out.append(p)
+    return out
+
+
+def test_round_robin_launches_leave_workspace_free():
+    """A sequence of launches with round-robin placements from every
+    starting XCD under random interleavings: every C element correct, the
+    region free after each launch, the poison word never set."""
     rng = np.random.default_rng(5)
-    size = 0
-    for _ in range(24):
-        k = int(rng.integers(1, 4))
-        jobs = [plans[int(i)] for i in rng.choice(len(plans), k)]
-        need, offs = 0, []
-        for M, N, K, S, nt, nsgS, MT, grid, rgs in jobs:
-            offs.append(need)
-            need += (S * N * ((M + 3) & ~3) * 4 + 255) // 256 * 256
-        if need > size:                     # the workspace grows: a new region, all free
-            size = need
-            region = np.full(size // 4, FREE, np.int64)
-        assert (region == FREE).all()
-        stamp = int(rng.integers(1, 1 << 30))
-        for (M, N, K, S, nt, nsgS, MT, grid, rgs), o in zip(jobs, offs):
-            Mp = (M + 3) & ~3
-            word = lambda s, n, m4: o // 4 + (s * N + n) * Mp + m4
-            for rg in range(rgs):
-                for s in range(S):
-                    for (ss, n, m4) in written(rg, s, nt, MT, M, N):
-                        region[word(ss, n, m4):word(ss, n, m4) + 4] = stamp
-            for rg in range(rgs):
-                r, _ = read_by_last(rg, S, nt, M, N)
-                for (ss, n, m4) in r:
-                    w = word(ss, n, m4)
-                    assert (region[w:w + 4] == stamp).all(), "the last split would read a free or stale slot"
-                    region[w:w + 4] = FREE
-        assert (region == FREE).all(), "a launch left a slot written"
+    ws = Workspace()
+    jobs = small_jobs()
+    assert len(jobs) == 2, jobs
+    for i in range(30):
+        job = jobs[int(rng.integers(len(jobs)))]
+        C = run_launch(ws, job, i, round_robin(int(rng.integers(NX))), rng)
+        assert all(v == "ok" for v in C.values())
+        assert ws.free() and not ws.poisoned
+
+
+def test_skip_between_rounds_is_a_valid_placement():
+    """A dispatcher that skips an XCD between two rounds of NX workgroups
+    shifts the placement offset of the later rounds only: every role is still
+    taken once on its XCD, and the result is correct."""
+    rng = np.random.default_rng(23)
+    ws = Workspace()
+    for job in small_jobs():
+        grid = job[7]
+        for k in (NX, grid // 2 // NX * NX, grid - NX):
+            C = run_launch(ws, job, k, lambda b, k=k: (b + 1) % NX if b >= k else b % NX, rng)
+            assert all(v == "ok" for v in C.values()), k
+            assert ws.free() and not ws.poisoned
+
+
+def test_broken_placements_show_as_nan():
+    """Each broken placement under several random interleavings: every C
+    element correct or NaN (never stale or wrong), NaN somewhere, the poison
+    word set; the next launch, with a round-robin placement, is NaN
+    everywhere."""
+    rng = np.random.default_rng(11)
+    seen = set()
+    for job in small_jobs():
+        for name, xcd_of in broken_placements(job, rng):
+            for rep in range(3):
+                ws = Workspace()
+                C = run_launch(ws, job, 1, xcd_of, rng)
+                assert all(v in ("ok", "nan") for v in C.values()), (name, job[:3], rep)
+                assert any(v == "nan" for v in C.values()), (name, job[:3], rep)
+                assert ws.poisoned, name
+                C2 = run_launch(ws, job, 2, round_robin(0), rng)
+                assert all(v == "nan" for v in C2.values()), name
+            seen.add(name)
+    assert {"duplicate", "missing last split", "XCD 3 skipped", "one skip", "random"} <= seen
+    assert sum(n.startswith("moved") for n in seen) >= 3
+
+
+def test_all_but_one_split_moved_is_caught():
+    """Row group 0's splits but one moved onto row group 1's XCD (their
+    duplicates late or early): the row group left without that split gives up,
+    the output holds NaN and the workspace is poisoned."""
+    rng = np.random.default_rng(17)
+    for job in small_jobs():
+        M, N, K, S, nt, nsgS, MT, grid, rgs = job
+        rr = round_robin(0)
+        for keep in (0, S // 2, S - 1):
+            moved = {b for b, rg, s, _ in roles(grid, S, nt, N, rr) if rg == 0 and s != keep}
+            xcd_of = lambda b, moved=moved: rr(b + 1) if b in moved else rr(b)
+            for rep in range(2):
+                ws = Workspace()
+                C = run_launch(ws, job, 1, xcd_of, rng)
+                assert all(v in ("ok", "nan") for v in C.values()), (keep, rep)
+                assert any(v == "nan" for v in C.values()) and ws.poisoned, (keep, rep)
 
 
 def test_planted_mistakes_are_caught():
@@ -191,3 +393,13 @@ def test_planted_mistakes_are_caught():
         check_plan(*p, mp_round=lambda M: M & ~3)                 # reader drops the last quad
     with pytest.raises(AssertionError):
         check_plan(*p, nx_plan=4)                                 # roles laid out for 4 XCDs on 8
+    rng = np.random.default_rng(3)
+    caught = {"own row group": False, "no tag check": False}
+    for job in small_jobs():
+        for name, xcd_of in broken_placements(job, rng):
+            for rep in range(3):
+                C = run_launch(Workspace(), job, 1, xcd_of, rng, give_up_all=False)
+                caught["own row group"] |= any(v not in ("ok", "nan") for v in C.values())
+                C = run_launch(Workspace(), job, 1, xcd_of, rng, check_tags=False)
+                caught["no tag check"] |= any(v not in ("ok", "nan") for v in C.values())
+    assert all(caught.values()), caught
