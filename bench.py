@@ -16,7 +16,9 @@ the libbusfill C-ABI.
 Prints ONE JSON line.  `value` is the weight-stream GB/s at M = 1
 (N*K*9/16 bytes / time per GEMM); `per_batch` carries M = 8 and 32; `roofline`
 prices the algorithmic bytes (weights + A + C) per launch against the 8 TB/s
-HBM peak; `cpu_baseline` is the oracle's CPU dequantize-then-matmul timed on
+HBM peak, over the per-launch time committed in profiles/kernel_time.json (the
+same event timing from a recorded run of this command), with this run's own
+figures beside it (`*_events`); `cpu_baseline` is the oracle's CPU dequantize-then-matmul timed on
 this host on a bounded sample of the same workload.
 
 Other workloads (--workload): q4_0 (18-byte blocks), planes (the reference
@@ -307,6 +309,39 @@ def traffic_from_profiles(key):
         return json.load(open(path)).get(key)
     except (OSError, ValueError):
         return None
+
+
+KERNEL_TIME = os.path.join("profiles", "kernel_time.json")
+
+
+def kernel_time_from_profiles(key):
+    """The committed per-launch time of one configuration (an entry that
+    --kernel-time-out wrote), or None."""
+    try:
+        e = json.load(open(os.path.join(ROOT, KERNEL_TIME))).get(key)
+    except (OSError, ValueError):
+        return None
+    return e if isinstance(e, dict) and e.get("us_per_launch", 0) > 0 else None
+
+
+def write_kernel_time(path, fmt, N, K, recs, batches, argv):
+    """Merges this run's per-launch times (the best launch mode of each batch
+    size: HIP events around the timed passes, divided by the GEMMs timed) into
+    the JSON file at path, one entry per configuration."""
+    try:
+        data = json.load(open(path))
+    except (OSError, ValueError):
+        data = {}
+    for M in batches:
+        r = best(recs, M)
+        data[f"{fmt}_{N}_m{M}" if N == K else f"{fmt}_{N}x{K}_m{M}"] = {
+            "us_per_launch": r["us_per_gemm"], "launch": r["launch"], "gemms_timed": r["gemms_timed"],
+            "ms_per_pass": r["ms_per_pass"],
+            "how": "HIP events on the launch stream around the timed passes, / GEMMs timed",
+            "command": "python3 bench.py " + " ".join(argv)}
+    with open(path, "w") as f:
+        json.dump(data, f, indent=1, sort_keys=True)
+        f.write("\n")
 
 
 # ------------------------------------------------------------------ workloads
@@ -601,6 +636,47 @@ def trace_summary(path, per_pass, labels):
     return out
 
 
+def roofline_record(key, alg_bytes, t_live):
+    """The roofline of the dominant kernel: algorithmic bytes per launch over
+    the per-launch time committed in profiles/kernel_time.json for this
+    configuration (the basis of `frac`), beside the same figures from this
+    run's HIP events (`*_events`).  Without a committed entry the basis is this
+    run's time, and `duration_source` says so."""
+    kt = kernel_time_from_profiles(key)
+    t = kt["us_per_launch"] / 1e6 if kt else t_live
+    return {"bound": "hbm", "achieved": round(alg_bytes / t / 1e9, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(alg_bytes / t / 1e9 / HBM_PEAK_GBPS, 4),
+            "traffic": traffic_from_profiles(key),
+            "algorithmic_bytes_per_launch": alg_bytes,
+            "us_per_launch": round(t * 1e6, 4),
+            "duration_source": f"{KERNEL_TIME} [{key}]" if kt else "this run's HIP events",
+            "us_per_launch_events": round(t_live * 1e6, 4),
+            "achieved_events": round(alg_bytes / t_live / 1e9, 2),
+            "frac_events": round(alg_bytes / t_live / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def counter_summary(path):
+    """Per-dispatch means of the counters in a `rocprofv3 --pmc` CSV, per
+    kernel of this library (namespace bf) and the bench's own kernels: each
+    dispatch's Counter_Value summed over the rows it has for one counter, then
+    averaged over the kernel's dispatches."""
+    import csv
+    import statistics as st
+    per = {}
+    for r in csv.DictReader(open(path)):
+        name = kernel_key(r["Kernel_Name"])
+        if "bf::" not in r["Kernel_Name"] and "k_stream" not in name:
+            continue
+        d = per.setdefault(name, {}).setdefault(r["Counter_Name"], {})
+        d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    out = {}
+    for name, counters in per.items():
+        out[name] = {"dispatches": max(len(v) for v in counters.values())}
+        for c, v in sorted(counters.items()):
+            out[name][c] = round(st.mean(v.values()), 2)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -623,15 +699,22 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--out", default=None, help="also write the full record to this JSON file")
+    ap.add_argument("--kernel-time-out", default=None, metavar="JSON",
+                    help="q4_k / q4_0 / planes: merge this run's per-launch times (one entry per batch size) into "
+                         "this JSON file (" + KERNEL_TIME + " is the roofline's committed basis)")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="no GPU work: summarize a rocprofv3 kernel-trace CSV of an earlier bench run "
                          "(per-launch durations per run of one kernel) as one JSON line")
+    ap.add_argument("--counter-summary", default=None, metavar="CSV",
+                    help="no GPU work: per-dispatch counter means per kernel of a rocprofv3 --pmc CSV, as one JSON "
+                         "line")
     ap.add_argument("--trace-labels", default="q4_k_5120_m1,q4_k_5120_m8,q4_k_5120_m32",
                     help="--trace-summary: names of the runs, in order")
     ap.add_argument("--trace-pass", type=int, default=72, help="--trace-summary: dispatches per pass")
     args = ap.parse_args()
-    if args.trace_summary:
-        rec = trace_summary(args.trace_summary, args.trace_pass, args.trace_labels.split(","))
+    if args.trace_summary or args.counter_summary:
+        rec = (trace_summary(args.trace_summary, args.trace_pass, args.trace_labels.split(","))
+               if args.trace_summary else counter_summary(args.counter_summary))
         line = json.dumps(rec)
         if args.out:
             with open(args.out, "w") as f:
@@ -677,11 +760,10 @@ def main():
             "all_runs": recs,
             "hbm_read_measured_GBps": round(peak, 1),
             "same_bytes_read_per_launch": rot.floor,
-            "roofline": {"bound": "hbm", "achieved": round(alg_bytes / t / 1e9, 2), "peak": HBM_PEAK_GBPS,
-                         "unit": "GB/s", "frac": round(alg_bytes / t / 1e9 / HBM_PEAK_GBPS, 4),
-                         "traffic": traffic_from_profiles(f"{fmt}_5120_m{head['M']}"),
-                         "algorithmic_bytes_per_launch": alg_bytes},
+            "roofline": roofline_record(f"{fmt}_5120_m{head['M']}", alg_bytes, t),
         }
+        if args.kernel_time_out:
+            write_kernel_time(args.kernel_time_out, fmt, 5120, 5120, recs, batches, sys.argv[1:])
         del rot
         torch.cuda.empty_cache()
         if not args.no_cpu:

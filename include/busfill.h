@@ -138,8 +138,9 @@ bf_status bf_gemm_ex(bf_qtype qtype, const void* W, const void* W_aux,
  * device's array (hipGetSymbolAddress).  Every call on one GPU shares the
  * array: calls that overlap on one GPU (concurrent streams, or a captured
  * graph replayed while another such call runs) race and may return wrong
- * results.  Each K-split launch first clears the array's counters with a
- * small kernel on the stream (no memset node in a captured graph).  Returns
+ * results.  Each K-split launch that exchanges partials in the kernel first
+ * marks its slots free with a small kernel on the stream (no memset node in a
+ * captured graph).  Returns
  * BF_ERR_INVALID, enqueueing nothing, for a shape whose launches need more
  * than 34 MiB of scratch (K-split partials of S splits x N x M rows in fp32,
  * 11 MB at the 27B-class layer's largest shapes at M = 32; dense partials of
@@ -157,8 +158,9 @@ bf_status bf_gemm_noalloc(bf_qtype qtype, const void* W, const void* W_aux,
 size_t bf_gemm_workspace_bytes(bf_qtype qtype, bf_otype otype, int M, int N, int K);
 
 /* bf_gemm with a caller-owned workspace: the call allocates nothing and the
- * library keeps no state between calls (the exchange's counters are cleared
- * on the stream by each launch).  workspace: 256-byte aligned device memory
+ * library keeps no state between calls (each launch that exchanges partials
+ * in the kernel first marks its slots free with a small kernel on the
+ * stream).  workspace: 256-byte aligned device memory
  * of workspace_bytes >= bf_gemm_workspace_bytes(...) (NULL and 0 when that is
  * 0); BF_ERR_INVALID, enqueueing nothing, when it is too small.  The result is
  * bit-identical to bf_gemm's.  Calls that overlap in time (other streams, or

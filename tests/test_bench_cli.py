@@ -70,3 +70,54 @@ def test_trace_summary_groups_runs_and_passes(tmp_path):
     # a pass of 4 dispatches spans 4 * 600 + 3 * 100 ns
     assert abs(rec["a"]["us_span_per_launch_median"] - (4 * 600 + 3 * 100) / 4 / 1000) < 1e-9
     assert rec["b"]["passes"] == 1 and rec["b"]["us_gap_median"] == 0.0
+
+
+def test_roofline_basis_is_the_committed_kernel_time(tmp_path, monkeypatch):
+    """roofline.frac = algorithmic bytes / the committed per-launch time / peak;
+    this run's figures sit beside it; without an entry the basis is this run's."""
+    sys.path.insert(0, ROOT)
+    import bench
+    alg = 14_776_320
+    committed = bench.kernel_time_from_profiles("q4_k_5120_m1")
+    r = bench.roofline_record("q4_k_5120_m1", alg, 6.5e-6)
+    assert r["us_per_launch_events"] == 6.5 and abs(r["frac_events"] - alg / 6.5e-6 / 8e12) < 1e-4
+    if committed:
+        assert r["us_per_launch"] == round(committed["us_per_launch"], 4)
+        assert abs(r["frac"] - alg / (committed["us_per_launch"] * 1e-6) / 8e12) < 1e-4
+        assert r["duration_source"].startswith("profiles/kernel_time.json")
+    r = bench.roofline_record("no_such_key", alg, 6.5e-6)
+    assert r["us_per_launch"] == 6.5 and r["frac"] == r["frac_events"] and "this run" in r["duration_source"]
+    # the writer keeps other entries and stores the best launch mode per batch size
+    path = tmp_path / "kt.json"
+    path.write_text('{"other": {"us_per_launch": 1.0}}')
+    recs = [{"M": 1, "us_per_gemm": 6.2, "launch": "stream", "gemms_timed": 72, "ms_per_pass": 0.4464},
+            {"M": 1, "us_per_gemm": 6.1, "launch": "graph", "gemms_timed": 72, "ms_per_pass": 0.4392}]
+    bench.write_kernel_time(str(path), "q4_k", 5120, 5120, recs, [1], ["--no-cpu"])
+    import json
+    d = json.loads(path.read_text())
+    assert d["other"]["us_per_launch"] == 1.0
+    assert d["q4_k_5120_m1"]["us_per_launch"] == 6.1 and d["q4_k_5120_m1"]["launch"] == "graph"
+
+
+def test_counter_summary_means_per_dispatch(tmp_path):
+    """--counter-summary: a dispatch's rows of one counter summed, then the
+    mean over the kernel's dispatches; other processes' kernels left out."""
+    import csv
+    import json
+    path = tmp_path / "pmc.csv"
+    cols = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    rows = []
+    for d, (k, vals) in enumerate((("void bf::k_x<1>(int)", (10, 20)), ("void bf::k_x<1>(int)", (30, 40)),
+                                   ("(anonymous namespace)::k_stream_copy(int)", (5,)), ("void at::foo(int)", (99,)))):
+        for v in vals:
+            rows.append({"Dispatch_Id": d, "Kernel_Name": k, "Counter_Name": "FETCH_SIZE", "Counter_Value": v})
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=cols)
+        w.writeheader()
+        w.writerows(rows)
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--counter-summary", str(path)],
+                       capture_output=True, text=True, timeout=120, cwd=ROOT)
+    assert r.returncode == 0, r.stderr
+    rec = json.loads(r.stdout)
+    assert rec["bf::k_x<1>"] == {"dispatches": 2, "FETCH_SIZE": 50.0}
+    assert rec["(anonymous namespace)::k_stream_copy"]["FETCH_SIZE"] == 5.0 and "at::foo" not in rec
