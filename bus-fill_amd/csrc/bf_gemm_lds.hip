@@ -157,6 +157,10 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
     auto wait_dep = [&]() {
         if (wave == NL) {
             wait_device_count(dep + kDepLine0 + 64 * (bid % kDepLines), 1u, lane, flags + kPoison);
+            // an earlier launch's consumer gave up: this launch's results are NaN
+            unsigned sticky = 0;
+            if (lane == 0) sticky = __hip_atomic_load(dep + kDepPoison, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((unsigned)__builtin_amdgcn_readfirstlane(sticky) != 0u) mark_poison(flags + kPoison);
             if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kDepFlag])), "v"(1) : "memory");
         } else {
             wait_flag(&flags[kDepFlag], flags + kPoison);
@@ -325,6 +329,10 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             // launch
             if (wave == 0) {
                 wait_flag(&flags[kDepFlag], flags + kPoison);
+                // this workgroup's wait gave up (or found the word set): keep
+                // every later launch on the workspace from trusting its flags
+                if (poisoned(flags + kPoison) && lane == 0)
+                    __hip_atomic_store(dep + kDepPoison, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 unsigned old = 0;
                 if (lane == 0) old = __hip_atomic_fetch_add(dep + 64, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if ((unsigned)__builtin_amdgcn_readfirstlane(old) == dep_users - 1u) {

@@ -184,9 +184,13 @@ constexpr int kDeviceScope = 16;
 // producer raises kDepLines release flags (words kDepLine0 + 64 i), which the
 // consumers poll round robin, so that no one line takes every consumer's polls
 // (polls of a single line from every CU queue behind each other for several
-// microseconds).  The last consumer past its wait clears everything.
+// microseconds).  The last consumer past its wait clears everything.  Word
+// kDepPoison is sticky: a consumer whose wait gave up sets it (a producer that
+// arrives after the clear would leave the release flags raised for the next
+// launch), and every later consumer that finds it set writes NaN.
 constexpr int kDepLines = 32, kDepLine0 = 128;
-constexpr int kDepWords = kDepLine0 + 64 * kDepLines;
+constexpr int kDepPoison = kDepLine0 + 64 * kDepLines;
+constexpr int kDepWords = kDepPoison + 64;
 
 // Spin until the device-scope word *cnt is at least n (lane 0 polls with
 // agent-scope atomic loads, which bypass the XCD's L2; a short s_sleep
