@@ -73,7 +73,14 @@ bf_status check_weights(bf_qtype qt, const void* W, const void* W_aux, int N, in
 // kernel's all-of-A form is not (31 us at M = 9).  Smaller matrices keep the
 // automatic order (7168x5120 at M = 16: K-split 11.7 against dense 18.5 us).
 bf_algo mid_batch_choice(const bf::GemmArgs& g) {
-    if (g.M < 9 || g.M > kSplitMaxM || (int64_t)g.N * g.K < 3 * (int64_t(1) << 24)) return BF_ALGO_AUTO;
+    if (g.M < 9 || g.M > kSplitMaxM) return BF_ALGO_AUTO;
+    // 17-32 rows whose K-split plan takes more than one round of workgroups
+    // (the activations leave room for fewer tiles per workgroup): the dense
+    // kernel (7168 x 5120 at M = 32: 15.1 against 17.3 us; at M = 24 the
+    // split plan fits one round and stays, 12.1 against 14.9)
+    if (g.M > 16 && (int64_t)g.N * g.K < 3 * (int64_t(1) << 24))
+        return bf::split_multi_round(g) && bf::dense_supports(g) ? BF_ALGO_DENSE : BF_ALGO_AUTO;
+    if ((int64_t)g.N * g.K < 3 * (int64_t(1) << 24)) return BF_ALGO_AUTO;
     if (g.N > g.K && g.M <= 16) return bf::split_supports(g) ? BF_ALGO_SPLIT : BF_ALGO_AUTO;
     return bf::dense_supports(g) ? BF_ALGO_DENSE : BF_ALGO_AUTO;
 }

@@ -839,6 +839,12 @@ bool split_supports(const GemmArgs& g) {
     return plan_split(g, p, device_xcds());
 }
 
+bool split_multi_round(const GemmArgs& g) {
+    SplitPlan p;
+    const int cus = device_cus();
+    return plan_split(g, p, device_xcds()) && cus > 0 && p.grid > cus;
+}
+
 size_t split_scratch_bytes(const GemmArgs& g) {
     SplitPlan p;
     if (!plan_split(g, p, device_xcds()) || p.S <= 1) return 0;

@@ -77,6 +77,8 @@ hipError_t split_workspace(const Scratch* scratch, hipStream_t st, size_t cbytes
 // small.
 hipError_t gemm_split(const GemmArgs& g, const Scratch* scratch, hipStream_t st);
 bool split_supports(const GemmArgs& g);
+// The K-split plan takes more than one round of one workgroup per CU.
+bool split_multi_round(const GemmArgs& g);
 size_t split_scratch_bytes(const GemmArgs& g);      // 0 when the plan does not split K
 WsNeed split_ws_need(const GemmArgs& g);            // of a launch on the library's workspace
 // Independent GEMMs of one format, one output type and one side of M = 16, in
