@@ -49,6 +49,15 @@
 //   weight slot), then per 16-k step decodes one fragment in registers (the
 //   fp16 weights of bf_formats.h, bit-exact with the oracle's fp16 dequant)
 //   and multiplies it against every m-tile's activation fragment.
+// * Two compute waves per row block (NCW = 8, where the activation ring holds
+//   at least five half-slabs): the wave of parity p takes the units v with
+//   v % 2 == p, so each SIMD runs two waves working on different units and
+//   one's VALU work issues while the other's MFMAs run (a single wave issues
+//   them in turn: one 32x32x16 MFMA followed by eight independent VALU
+//   instructions takes 64 cycles in one wave, 40 per wave with four waves on a
+//   SIMD).  At the end of each piece parity 1 hands its sums to parity 0
+//   through LDS, one m-tile at a time; parity 0 adds them (its own first, a
+//   fixed order) and stores.
 // * Bounded waits poison the workgroup's results to NaN if a producer were
 //   ever missing (bf_lds.h): its C stores and partials are NaN, and so is
 //   every sum a poisoned partial enters.
@@ -62,7 +71,7 @@ namespace bf {
 namespace {
 
 // Loader waves: kDnNLW stream the weights, kDnNLA the activations.
-constexpr int kDnNC = 4;                 // compute waves per workgroup
+constexpr int kDnNCU = 4;                // compute waves that consume one unit (32 rows each)
 constexpr int kDnNLW = 1, kDnNLA = 2;    // loader waves of the weight and of the activation stream
 constexpr int kDnNL = kDnNLW + kDnNLA;
 constexpr int kDnMaxUnits = 80;          // units per workgroup
@@ -75,7 +84,11 @@ constexpr int kDnMaxUnits = 80;          // units per workgroup
 constexpr int kDnPoison = 2;
 constexpr int kDnWReady = 16, kDnWCons = kDnWReady + kDnNLW * kDnMaxUnits, kDnAReady = kDnWCons + kDnMaxUnits,
               kDnACons = kDnAReady + 2 * kDnNLA * kDnMaxUnits;
-constexpr int kDnFlags = ((kDnACons + 2 * kDnMaxUnits) * 4 + 255) & ~255;   // bytes
+// two compute waves per row block (NCW = 8): the words of their piece-end
+// hand-over, and the LDS it goes through (one m-tile of one parity's sums)
+constexpr int kDnCombW = kDnACons + 2 * kDnMaxUnits, kDnCombR = kDnCombW + kDnNCU;
+constexpr int kDnFlags = ((kDnCombR + kDnNCU) * 4 + 255) & ~255;   // bytes
+constexpr int kDnComb = kDnNCU * 64 * 16 * 4;
 constexpr int kDnRows = 128;             // weight rows per row group (32 per compute wave)
 constexpr int kDnWSlot = kDnRows * 144;  // bytes of one weight unit
 constexpr int kDnARow = 272;             // LDS bytes of one activation row of a half-slab (256 + 16)
@@ -90,12 +103,12 @@ __host__ __device__ __forceinline__ int range_owner(int t, int T, int G) {
 }
 
 // One GEMM's share of a launch: workgroup p of its G.
-template <int QT, int MT>
+template <int QT, int MT, int NCW>
 __device__ __forceinline__ void dense_body(int p, uint8_t* lds, const uint8_t* __restrict__ W,
                                            const uint8_t* __restrict__ Waux, const uint16_t* __restrict__ A, int lda,
                                            void* __restrict__ C, int ldc, int out_f16, int M, int N, int K, int T,
                                            int G, int DW, int DA, float* __restrict__ ws) {
-    constexpr int NC = kDnNC, NL = kDnNL, ROWS = kDnRows;
+    constexpr int NC = NCW, NL = kDnNL, ROWS = kDnRows;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsg = K >> 8;
@@ -148,7 +161,7 @@ __device__ __forceinline__ void dense_body(int p, uint8_t* lds, const uint8_t* _
                 }
                 for (int sg = s0; sg < s1; sg++, v++) {
                     // the slot's previous unit must be consumed by every compute wave
-                    if (v >= DW) wait_count(&flags[kDnWCons + v - DW], NC, flags + kDnPoison);
+                    if (v >= DW) wait_count(&flags[kDnWCons + v - DW], kDnNCU, flags + kDnPoison);
                     const uint32_t wb = lds0 + (uint32_t)(kDnFlags + (v % DW) * kDnWSlot);
 #pragma unroll
                     for (int q2 = 0; q2 < kDnWQS; q2++) {
@@ -180,7 +193,7 @@ __device__ __forceinline__ void dense_body(int p, uint8_t* lds, const uint8_t* _
             for (int t = t0, u = 0; t < t1; t++) {
                 const int sg = t % nsg;
                 for (int h = 0; h < 2; h++, u++) {
-                    if (u >= DA) wait_count(&flags[kDnACons + u - DA], NC, flags + kDnPoison);
+                    if (u >= DA) wait_count(&flags[kDnACons + u - DA], kDnNCU, flags + kDnPoison);
                     const uint32_t ab = lds0 + (uint32_t)(kDnFlags + DW * kDnWSlot + (u % DA) * a_slot);
                     const uint32_t off = 512u * (uint32_t)sg + 128u * (uint32_t)h;
 #pragma unroll
@@ -201,7 +214,12 @@ __device__ __forceinline__ void dense_body(int p, uint8_t* lds, const uint8_t* _
 
     // ---------------------------------------------------------------- compute wave
     clear_flags_and_meet();
-    const int c = wave - NL;
+    // compute wave: row block c (rows 32 c .. 32 c + 31 of the row group) and,
+    // with NCW = 8, parity par: the waves of parity p take the units v with
+    // v % 2 == p, so two waves of different units share each SIMD
+    const int cw = wave - NL, c = cw & (kDnNCU - 1), par = NCW == 8 ? cw / kDnNCU : 0;
+    uint8_t* const comb = a_ring + DA * a_slot;
+    int chunk = 0;                                     // piece-end hand-overs so far
     const Magic mg = make_magic();
     const int n = lane & 31, g = lane >> 5;
     int arow[MT];
@@ -216,6 +234,7 @@ __device__ __forceinline__ void dense_body(int p, uint8_t* lds, const uint8_t* _
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[mt][e] = 0.f;
         for (int sg = s0; sg < s1; sg++, v++) {
+            if (NCW == 8 && (v & 1) != par) continue;
             wait_flags(flags + kDnWReady + kDnNLW * v, kDnNLW, lane, flags + kDnPoison);
             const uint8_t* wrow = w_ring + (v % DW) * kDnWSlot + (32 * c + n) * 144;
             Raw<QT> raw0, raw1;
@@ -257,6 +276,42 @@ __device__ __forceinline__ void dense_body(int p, uint8_t* lds, const uint8_t* _
                 // every LDS read of the half-slab has completed: count it consumed
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 if (lane == 0) asm volatile("ds_add_u32 %0, %1" :: "v"(lds_addr(&flags[kDnACons + u])), "v"(1) : "memory");
+            }
+        }
+        if constexpr (NCW == 8) {
+            // the two parities' sums of the piece: parity 1 hands its m-tiles
+            // over through LDS one at a time, parity 0 adds them (its own
+            // first: a fixed order) and stores
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                chunk++;
+                float* const cb = (float*)(comb + c * 4096) + lane * 16;
+                if (par == 1) {
+                    if (chunk > 1) wait_flags(flags + kDnCombR + c, 1, lane, flags + kDnPoison, chunk - 1);
+#pragma unroll
+                    for (int e = 0; e < 16; e += 4)
+                        *(f4*)(cb + e) = f4{acc[mt][e], acc[mt][e + 1], acc[mt][e + 2], acc[mt][e + 3]};
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    if (lane == 0)
+                        asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kDnCombW + c])), "v"(chunk) : "memory");
+                } else {
+                    wait_flags(flags + kDnCombW + c, 1, lane, flags + kDnPoison, chunk);
+#pragma unroll
+                    for (int e = 0; e < 16; e += 4) {
+                        const f4 q = *(const f4*)(cb + e);
+                        acc[mt][e] += q[0];
+                        acc[mt][e + 1] += q[1];
+                        acc[mt][e + 2] += q[2];
+                        acc[mt][e + 3] += q[3];
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    if (lane == 0)
+                        asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kDnCombR + c])), "v"(chunk) : "memory");
+                }
+            }
+            if (par == 1) {
+                t += s1 - s0;
+                continue;
             }
         }
         // this lane's outputs: weight row rg * 128 + 32 c + n, batch rows
@@ -320,14 +375,15 @@ __device__ __forceinline__ void dense_body(int p, uint8_t* lds, const uint8_t* _
     }
 }
 
-// One workgroup per CU (the rings fill the LDS), so at most two waves per SIMD.
-template <int QT, int MT>
-__global__ __launch_bounds__(64 * (kDnNC + kDnNL)) __attribute__((amdgpu_waves_per_eu(1, 2)))
+// One workgroup per CU (the rings fill the LDS): 4 + 3 waves (NCW = 4) or
+// 8 + 3 (NCW = 8, at most three per SIMD).
+template <int QT, int MT, int NCW>
+__global__ __launch_bounds__(64 * (NCW + kDnNL)) __attribute__((amdgpu_waves_per_eu(NCW == 8 ? 3 : 1, NCW == 8 ? 3 : 2)))
 void k_gemm_dense(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Waux, const uint16_t* __restrict__ A,
                   int lda, void* __restrict__ C, int ldc, int out_f16, int M, int N, int K, int T, int G, int DW,
                   int DA, float* __restrict__ ws) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    dense_body<QT, MT>((int)blockIdx.x, lds, W, Waux, A, lda, C, ldc, out_f16, M, N, K, T, G, DW, DA, ws);
+    dense_body<QT, MT, NCW>((int)blockIdx.x, lds, W, Waux, A, lda, C, ldc, out_f16, M, N, K, T, G, DW, DA, ws);
 }
 
 // Several independent GEMMs of one batch size in one launch, their grids back
@@ -348,8 +404,8 @@ struct DenseJobs {
     int n, M, out_f16, DW, DA;
 };
 
-template <int QT, int MT>
-__global__ __launch_bounds__(64 * (kDnNC + kDnNL)) __attribute__((amdgpu_waves_per_eu(1, 2)))
+template <int QT, int MT, int NCW>
+__global__ __launch_bounds__(64 * (NCW + kDnNL)) __attribute__((amdgpu_waves_per_eu(NCW == 8 ? 3 : 1, NCW == 8 ? 3 : 2)))
 void k_gemm_dense_batched(const DenseJobs jobs) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     // the last job whose grid starts at or before this workgroup (uniform
@@ -358,7 +414,7 @@ void k_gemm_dense_batched(const DenseJobs jobs) {
 #pragma unroll
     for (int i = 1; i < kDnMaxJobs; i++)
         if (i < jobs.n && (int)blockIdx.x >= jobs.job[i].grid0) j = jobs.job[i];
-    dense_body<QT, MT>((int)blockIdx.x - j.grid0, lds, j.W, j.Waux, j.A, j.lda, j.C, j.ldc, jobs.out_f16, jobs.M, j.N,
+    dense_body<QT, MT, NCW>((int)blockIdx.x - j.grid0, lds, j.W, j.Waux, j.A, j.lda, j.C, j.ldc, jobs.out_f16, jobs.M, j.N,
                        j.K, j.T, j.G, jobs.DW, jobs.DA, j.ws);
 }
 
@@ -420,7 +476,7 @@ __global__ __launch_bounds__(256) void k_dense_sum_batched(const DenseJobs jobs)
 }
 
 struct DensePlan {
-    int MT, T, G, DW, DA, rgs, lds;
+    int MT, T, G, DW, DA, rgs, lds, nc;                // nc: compute waves (4 or 8)
     bool split;                                        // some row group is split between workgroups
 };
 
@@ -437,8 +493,17 @@ bool plan_dense(const GemmArgs& g, DensePlan& p, int cus) {
     if ((int64_t)g.M * g.ldc * (g.out_f16 ? 2 : 4) >= (1LL << 31)) return false;   // C by 32-bit offsets
     const int MT = (g.M + 31) / 32;                    // 32-row m-tiles
     if ((g.M * 17 + 63) / 64 > kDnNLA * kDnAQS || (kDnRows * 9 + 63) / 64 > kDnNLW * kDnWQS) return false;
+    // Eight compute waves (two per SIMD, on alternate units) where the
+    // activation ring holds at least five half-slabs beside the hand-over
+    // area (M <= 64); otherwise four, one per SIMD.  5120 x 17408 at
+    // M = 24 / 32 / 64: 23.3-23.6 / 23.2 / 28.7-29.3 -> 21.7-21.9 / 22.1 /
+    // 28.0-28.5 us, the 27B-class layer at M = 32 in one batched call
+    // 88.0-91.8 -> 82.4-83.8 us; with four half-slabs (M = 96) eight waves were
+    // 1-2.5 % slower, with three (M = 128) 6 %.
     const int DW = 2, a_slot = g.M * kDnARow;
-    const int DA = std::min(6, (kMaxLds - kDnFlags - DW * kDnWSlot) / a_slot);
+    const int DA8 = std::min(6, (kMaxLds - kDnFlags - DW * kDnWSlot - kDnComb) / a_slot);
+    const int nc = DA8 >= 5 ? 8 : 4;
+    const int DA = nc == 8 ? DA8 : std::min(6, (kMaxLds - kDnFlags - DW * kDnWSlot) / a_slot);
     if (DA < 2) return false;
     const int64_t rgs = (g.N + kDnRows - 1) / kDnRows, nsg = g.K / 256;
     if (rgs * nsg >= (1LL << 30)) return false;
@@ -448,13 +513,14 @@ bool plan_dense(const GemmArgs& g, DensePlan& p, int cus) {
     bool split = false;
     for (int rg = 0; rg < (int)rgs && !split; rg++)
         split = range_owner(rg * (int)nsg, T, G) != range_owner(rg * (int)nsg + (int)nsg - 1, T, G);
-    p = DensePlan{MT, T, G, DW, DA, (int)rgs, kDnFlags + DW * kDnWSlot + DA * a_slot, split};
+    p = DensePlan{MT, T, G, DW, DA, (int)rgs, kDnFlags + DW * kDnWSlot + DA * a_slot + (nc == 8 ? kDnComb : 0), nc,
+                  split};
     return true;
 }
 
-template <int QT, int MT>
+template <int QT, int MT, int NCW>
 hipError_t launch_dense(const GemmArgs& g, const DensePlan& p, const Scratch* scratch, hipStream_t st) {
-    auto k = k_gemm_dense<QT, MT>;
+    auto k = k_gemm_dense<QT, MT, NCW>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -469,7 +535,7 @@ hipError_t launch_dense(const GemmArgs& g, const DensePlan& p, const Scratch* sc
     float* parts = nullptr;
     e = split_workspace(scratch, st, 0, dense_partial_bytes(g, p), &counters, &parts);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3(p.G), dim3(64 * (kDnNC + kDnNL)), p.lds, st, g.W, g.Waux, g.A, g.lda, g.C, g.ldc,
+    hipLaunchKernelGGL(k, dim3(p.G), dim3(64 * (NCW + kDnNL)), p.lds, st, g.W, g.Waux, g.A, g.lda, g.C, g.ldc,
                        g.out_f16, g.M, g.N, g.K, p.T, p.G, p.DW, p.DA, parts);
     e = hipGetLastError();
     if (e != hipSuccess || !p.split) return e;
@@ -480,10 +546,10 @@ hipError_t launch_dense(const GemmArgs& g, const DensePlan& p, const Scratch* sc
 
 // Up to kDnMaxJobs GEMMs of one format, one batch size and one output type:
 // one launch of their grids back to back, one sum launch.
-template <int QT, int MT>
+template <int QT, int MT, int NCW>
 hipError_t launch_dense_batched(const GemmArgs* gs, const DensePlan* ps, int n, const Scratch* scratch,
                                 hipStream_t st) {
-    auto k = k_gemm_dense_batched<QT, MT>;
+    auto k = k_gemm_dense_batched<QT, MT, NCW>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -521,7 +587,7 @@ hipError_t launch_dense_batched(const GemmArgs* gs, const DensePlan* ps, int n, 
         lds = std::max(lds, p.lds);
         split = split || p.split;
     }
-    hipLaunchKernelGGL(k, dim3(grid), dim3(64 * (kDnNC + kDnNL)), lds, st, jobs);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(64 * (NCW + kDnNL)), lds, st, jobs);
     e = hipGetLastError();
     if (e != hipSuccess || !split) return e;
     hipLaunchKernelGGL(k_dense_sum_batched, dim3(rgs, (jobs.M + 7) / 8), dim3(256), 0, st, jobs);
@@ -531,18 +597,30 @@ hipError_t launch_dense_batched(const GemmArgs* gs, const DensePlan* ps, int n, 
 template <int QT>
 hipError_t dispatch_dense_batched(const GemmArgs* gs, const DensePlan* ps, int n, const Scratch* scratch,
                                   hipStream_t st) {
-    if (ps[0].MT == 1) return launch_dense_batched<QT, 1>(gs, ps, n, scratch, st);
-    if (ps[0].MT == 2) return launch_dense_batched<QT, 2>(gs, ps, n, scratch, st);
-    if (ps[0].MT == 3) return launch_dense_batched<QT, 3>(gs, ps, n, scratch, st);
-    return launch_dense_batched<QT, 4>(gs, ps, n, scratch, st);
+    if (ps[0].nc == 8) {
+        if (ps[0].MT == 1) return launch_dense_batched<QT, 1, 8>(gs, ps, n, scratch, st);
+        if (ps[0].MT == 2) return launch_dense_batched<QT, 2, 8>(gs, ps, n, scratch, st);
+        if (ps[0].MT == 3) return launch_dense_batched<QT, 3, 8>(gs, ps, n, scratch, st);
+        return launch_dense_batched<QT, 4, 8>(gs, ps, n, scratch, st);
+    }
+    if (ps[0].MT == 1) return launch_dense_batched<QT, 1, 4>(gs, ps, n, scratch, st);
+    if (ps[0].MT == 2) return launch_dense_batched<QT, 2, 4>(gs, ps, n, scratch, st);
+    if (ps[0].MT == 3) return launch_dense_batched<QT, 3, 4>(gs, ps, n, scratch, st);
+    return launch_dense_batched<QT, 4, 4>(gs, ps, n, scratch, st);
 }
 
 template <int QT>
 hipError_t dispatch_dense(const GemmArgs& g, const DensePlan& p, const Scratch* scratch, hipStream_t st) {
-    if (p.MT == 1) return launch_dense<QT, 1>(g, p, scratch, st);
-    if (p.MT == 2) return launch_dense<QT, 2>(g, p, scratch, st);
-    if (p.MT == 3) return launch_dense<QT, 3>(g, p, scratch, st);
-    return launch_dense<QT, 4>(g, p, scratch, st);
+    if (p.nc == 8) {
+        if (p.MT == 1) return launch_dense<QT, 1, 8>(g, p, scratch, st);
+        if (p.MT == 2) return launch_dense<QT, 2, 8>(g, p, scratch, st);
+        if (p.MT == 3) return launch_dense<QT, 3, 8>(g, p, scratch, st);
+        return launch_dense<QT, 4, 8>(g, p, scratch, st);
+    }
+    if (p.MT == 1) return launch_dense<QT, 1, 4>(g, p, scratch, st);
+    if (p.MT == 2) return launch_dense<QT, 2, 4>(g, p, scratch, st);
+    if (p.MT == 3) return launch_dense<QT, 3, 4>(g, p, scratch, st);
+    return launch_dense<QT, 4, 4>(g, p, scratch, st);
 }
 
 }  // namespace
