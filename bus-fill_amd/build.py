@@ -17,7 +17,7 @@ LIB = os.path.join(LIBDIR, "libbusfill.so")
 BENCH_LIB = os.path.join(LIBDIR, "libbusfill_bench.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["bf_api.hip", "bf_gemm_mfma.hip", "bf_gemm_dot2.hip", "bf_gemm_lds.hip", "bf_gemm_slab.hip", "bf_gemm_split.hip", "bf_gemm_dense.hip", "bf_simple.hip", "bf_gemm_q8.hip",
+SOURCES = ["bf_api.hip", "bf_gemm_mfma.hip", "bf_gemm_dot2.hip", "bf_gemm_lds.hip", "bf_gemm_slab.hip", "bf_gemm_split.hip", "bf_gemm_dense.hip", "bf_simple.hip", "bf_gemm_q8.hip", "bf_ggml.hip",
            "bf_gguf.cpp"]
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 anywhere in the device code.

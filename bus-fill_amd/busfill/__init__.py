@@ -37,6 +37,7 @@ EXPORTS = ("bf_busfill_q4", "bf_busfill_q4_ws", "bf_gemm", "bf_gemm_ex", "bf_gem
            "bf_swiglu_f16", "bf_ffn_swiglu", "bf_ffn_swiglu_ex", "bf_q8_bytes", "bf_quantize_q8", "bf_gemm_q8",
            "bf_gguf_open", "bf_gguf_close", "bf_gguf_tensor_count", "bf_gguf_tensor_at", "bf_gguf_find",
            "bf_gguf_get_u64", "bf_gguf_get_str", "bf_gguf_upload",
+           "bf_ggml_mul_mat", "bf_ggml_mul_mat_workspace_bytes", "bf_ggml_mul_mat_ws",
            "bf_status_str", "bf_last_error", "bf_version")
 
 
@@ -57,6 +58,42 @@ class GgufTensor(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("ggml_type", ctypes.c_uint32), ("qtype", ctypes.c_int32),
                 ("n_dims", ctypes.c_uint32), ("dims", ctypes.c_uint64 * 4), ("offset", ctypes.c_uint64),
                 ("nbytes", ctypes.c_uint64), ("data", ctypes.c_void_p)]
+
+
+# ggml type codes (bf_ggml_type)
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q4_K = 0, 1, 2, 12
+
+
+class GgmlTensor(ctypes.Structure):
+    """bf_ggml_tensor: ggml's type code, device address, ne[4] and nb[4]."""
+    _fields_ = [("type", ctypes.c_int32), ("data", ctypes.c_void_p), ("ne", ctypes.c_int64 * 4),
+                ("nb", ctypes.c_uint64 * 4)]
+
+
+def ggml_tensor(type_: int, data, ne, nb) -> GgmlTensor:
+    """A bf_ggml_tensor from ggml-order ne / nb (ne[0] innermost; missing
+    outer dimensions are 1, their strides the whole tensor's span)."""
+    ne = list(ne) + [1] * (4 - len(ne))
+    nb = list(nb)
+    while len(nb) < 4:
+        nb.append(nb[-1] * ne[len(nb) - 1])
+    return GgmlTensor(type_, _ptr(data), (ctypes.c_int64 * 4)(*ne), (ctypes.c_uint64 * 4)(*nb))
+
+
+def ggml_view(t, type_: int | None = None) -> GgmlTensor:
+    """The ggml view of a torch tensor (shape and strides reversed into ne and
+    nb).  type_ defaults to F32 / F16 from the dtype; quantized weights pass
+    their type and a uint8 tensor of shape [..., rows, row bytes]."""
+    import torch
+    if type_ is None:
+        type_ = {torch.float32: GGML_F32, torch.float16: GGML_F16}[t.dtype]
+    es = t.element_size()
+    shape, strides = list(t.shape)[::-1], [s * es for s in t.stride()][::-1]
+    if type_ in (GGML_Q4_0, GGML_Q4_K):
+        blk, bb = (32, 18) if type_ == GGML_Q4_0 else (256, 144)
+        assert shape[0] % bb == 0 and strides[0] == 1, "quantized rows: whole contiguous blocks"
+        shape[0], strides[0] = shape[0] // bb * blk, bb
+    return ggml_tensor(type_, t, shape, strides)
 
 
 class BusfillError(RuntimeError):
@@ -121,6 +158,13 @@ def lib() -> ctypes.CDLL:
                   "bf_gemm_batched", "bf_gemm_batched_ws", "bf_dequant_f16", "bf_gemm_swiglu",
                   "bf_swiglu_f16", "bf_ffn_swiglu", "bf_ffn_swiglu_ex", "bf_quantize_q8", "bf_gemm_q8"):
             getattr(L, f).restype = i
+        gp = ctypes.POINTER(GgmlTensor)
+        L.bf_ggml_mul_mat.argtypes = [gp, gp, gp, vp]
+        L.bf_ggml_mul_mat.restype = i
+        L.bf_ggml_mul_mat_workspace_bytes.argtypes = [gp, gp, gp]
+        L.bf_ggml_mul_mat_workspace_bytes.restype = sz
+        L.bf_ggml_mul_mat_ws.argtypes = [gp, gp, gp, vp, sz, vp]
+        L.bf_ggml_mul_mat_ws.restype = i
         L.bf_status_str.argtypes = [i]
         L.bf_status_str.restype = ctypes.c_char_p
         L.bf_last_error.restype = ctypes.c_char_p
@@ -338,6 +382,22 @@ def dequant_f16(qtype: int, W, W_aux, out, N: int, K: int, stream=None) -> None:
     """out[N][K] (fp16 bits) = bit-exact dequant of W."""
     _check(lib().bf_dequant_f16(qtype, _ptr(W), _ptr(W_aux), _ptr(out), N, K, _stream(stream)),
            "bf_dequant_f16")
+
+
+def ggml_mul_mat(src0: GgmlTensor, src1: GgmlTensor, dst: GgmlTensor, stream=None) -> None:
+    """dst = ggml_mul_mat(src0, src1) (ggml's semantics; bf_ggml_tensor views)."""
+    _check(lib().bf_ggml_mul_mat(ctypes.byref(src0), ctypes.byref(src1), ctypes.byref(dst), _stream(stream)),
+           "bf_ggml_mul_mat")
+
+
+def ggml_mul_mat_workspace_bytes(src0: GgmlTensor, src1: GgmlTensor, dst: GgmlTensor) -> int:
+    return lib().bf_ggml_mul_mat_workspace_bytes(ctypes.byref(src0), ctypes.byref(src1), ctypes.byref(dst))
+
+
+def ggml_mul_mat_ws(src0: GgmlTensor, src1: GgmlTensor, dst: GgmlTensor, workspace, workspace_bytes: int,
+                    stream=None) -> None:
+    _check(lib().bf_ggml_mul_mat_ws(ctypes.byref(src0), ctypes.byref(src1), ctypes.byref(dst), _ptr(workspace),
+                                    workspace_bytes, _stream(stream)), "bf_ggml_mul_mat_ws")
 
 
 def version() -> int:

@@ -448,6 +448,123 @@ bf_status check_workspace(const void* ws, size_t bytes) {
     return BF_OK;
 }
 
+
+// ------------------------------------------------------------ ggml mul_mat hook
+// ggml_mul_mat's operands checked and cut into one GEMM per (i2, i3) slice of
+// dst (ggml.c's ggml_can_mul_mat and ggml_mul_mat fix the shapes; src0 is
+// broadcast over src1's outer dimensions by i02 = i2 / r2, i03 = i3 / r3).
+struct GgmlCall {
+    bf_qtype qt = BF_Q4_0;
+    int64_t K = 0, N = 0, M = 0, ne2 = 1, ne3 = 1, r2 = 1, r3 = 1;
+    bool stage = false;            // src1 goes through the fp16 staging buffer
+    size_t stage_bytes = 0;
+};
+
+constexpr size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+bf_status check_ggml(const bf_ggml_tensor* s0, const bf_ggml_tensor* s1, const bf_ggml_tensor* d, GgmlCall& c) {
+    if (!s0 || !s1 || !d) return fail(BF_ERR_INVALID, "ggml mul_mat: a tensor is NULL");
+    const bf_ggml_tensor* ts[3] = {s0, s1, d};
+    const char* nm[3] = {"src0", "src1", "dst"};
+    for (int t = 0; t < 3; t++) {
+        if (!ts[t]->data) return fail(BF_ERR_INVALID, "ggml mul_mat: %s data is NULL", nm[t]);
+        for (int i = 0; i < 4; i++)
+            if (ts[t]->ne[i] < 1) return fail(BF_ERR_INVALID, "ggml mul_mat: %s ne[%d]=%lld must be >= 1", nm[t], i,
+                                              (long long)ts[t]->ne[i]);
+    }
+    if (s0->type != BF_GGML_Q4_0 && s0->type != BF_GGML_Q4_K)
+        return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: src0 type %d (the hook serves Q4_0 = 2 and Q4_K = 12)",
+                    (int)s0->type);
+    if (s1->type != BF_GGML_F32 && s1->type != BF_GGML_F16)
+        return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: src1 type %d (the hook serves F32 and F16)", (int)s1->type);
+    if (d->type != BF_GGML_F32)
+        return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: dst type %d (the hook writes F32)", (int)d->type);
+    // the shapes ggml_mul_mat accepts and the one it gives dst
+    if (s0->ne[0] != s1->ne[0])
+        return fail(BF_ERR_INVALID, "ggml mul_mat: src0 ne[0]=%lld != src1 ne[0]=%lld", (long long)s0->ne[0],
+                    (long long)s1->ne[0]);
+    if (s1->ne[2] % s0->ne[2] || s1->ne[3] % s0->ne[3])
+        return fail(BF_ERR_INVALID, "ggml mul_mat: src1 ne[2], ne[3] must be multiples of src0's (broadcast)");
+    if (d->ne[0] != s0->ne[1] || d->ne[1] != s1->ne[1] || d->ne[2] != s1->ne[2] || d->ne[3] != s1->ne[3])
+        return fail(BF_ERR_INVALID, "ggml mul_mat: dst ne must be {src0 ne[1], src1 ne[1], src1 ne[2], src1 ne[3]}");
+    c.qt = s0->type == BF_GGML_Q4_K ? BF_Q4_K : BF_Q4_0;
+    const int64_t blk = c.qt == BF_Q4_K ? 256 : 32, bb = c.qt == BF_Q4_K ? 144 : 18;
+    c.K = s0->ne[0];
+    c.N = s0->ne[1];
+    c.M = s1->ne[1];
+    c.ne2 = s1->ne[2];
+    c.ne3 = s1->ne[3];
+    c.r2 = s1->ne[2] / s0->ne[2];
+    c.r3 = s1->ne[3] / s0->ne[3];
+    if (c.K % blk) return fail(BF_ERR_INVALID, "ggml mul_mat: src0 ne[0]=%lld is not whole blocks", (long long)c.K);
+    if (c.K > INT32_MAX || c.N > INT32_MAX || c.M > INT32_MAX || c.ne2 > (1 << 20) || c.ne3 > (1 << 20) ||
+        c.ne2 * c.ne3 > (1 << 20) || c.M * c.ne2 * c.ne3 > (int64_t(1) << 40) / c.K)
+        return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: a dimension exceeds 2^31 - 1, more than 2^20 slices, or more "
+                                        "than 2^40 activations");
+    // src0: whole rows of blocks, one after the other (a matrix per slice)
+    if (s0->nb[0] != (uint64_t)bb || s0->nb[1] != (uint64_t)(c.K / blk * bb))
+        return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: src0 rows must be contiguous blocks (nb[0]=%lld, nb[1]=%lld)",
+                    (long long)bb, (long long)(c.K / blk * bb));
+    if (c.qt == BF_Q4_0 && (((uintptr_t)s0->data | s0->nb[2] | s0->nb[3]) & 1))
+        return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: Q4_0 matrices must start 2-byte aligned");
+    // dst: F32 rows, slices that do not overlap
+    const uint64_t ldc = d->nb[1] / 4;
+    if (d->nb[0] != 4 || d->nb[1] % 4 || ldc < (uint64_t)c.N || ldc > INT32_MAX ||
+        (((uintptr_t)d->data | d->nb[2] | d->nb[3]) & 3))
+        return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: dst must be F32 rows (nb[0] = 4, nb[1] >= 4 ne[0])");
+    if ((c.ne2 > 1 && d->nb[2] < (uint64_t)c.M * d->nb[1]) || (c.ne3 > 1 && d->nb[3] < (uint64_t)c.ne2 * d->nb[2]))
+        return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: dst slices overlap");
+    // src1: element-aligned strides; fp16 rows the GEMM reads in place, or staging
+    const uint64_t es = s1->type == BF_GGML_F32 ? 4 : 2;
+    if (((uintptr_t)s1->data | s1->nb[0] | s1->nb[1] | s1->nb[2] | s1->nb[3]) & (es - 1))
+        return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: src1 strides must be multiples of its element size");
+    c.stage = !(s1->type == BF_GGML_F16 && s1->nb[0] == 2 &&
+                (((uintptr_t)s1->data | s1->nb[1] | s1->nb[2] | s1->nb[3]) & 15) == 0 &&
+                s1->nb[1] / 2 >= (uint64_t)c.K && s1->nb[1] / 2 <= INT32_MAX);
+    c.stage_bytes = c.stage ? align256((size_t)(c.M * c.ne2 * c.ne3) * (size_t)c.K * 2) : 0;
+    return BF_OK;
+}
+
+// The slices' GEMMs, src1 read from `staged` (fp16 rows of K, slice-major) or
+// in place, planned as bf_gemm_batched plans them.
+bf_status plan_ggml(const GgmlCall& c, const bf_ggml_tensor* s0, const bf_ggml_tensor* s1, const bf_ggml_tensor* d,
+                    const uint16_t* staged, BatchedPlan& bp) {
+    std::vector<bf_gemm_desc> descs;
+    descs.reserve((size_t)(c.ne2 * c.ne3));
+    for (int64_t i3 = 0; i3 < c.ne3; i3++)
+        for (int64_t i2 = 0; i2 < c.ne2; i2++) {
+            bf_gemm_desc g;
+            g.W = (const uint8_t*)s0->data + (i3 / c.r3) * s0->nb[3] + (i2 / c.r2) * s0->nb[2];
+            g.W_aux = nullptr;
+            if (c.stage) {
+                g.A = staged + (size_t)((i3 * c.ne2 + i2) * c.M) * (size_t)c.K;
+                g.lda = (int)c.K;
+            } else {
+                g.A = (const uint16_t*)((const uint8_t*)s1->data + i3 * s1->nb[3] + i2 * s1->nb[2]);
+                g.lda = (int)(s1->nb[1] / 2);
+            }
+            g.C = (uint8_t*)d->data + i3 * d->nb[3] + i2 * d->nb[2];
+            g.ldc = (int)(d->nb[1] / 4);
+            g.M = (int)c.M;
+            g.N = (int)c.N;
+            g.K = (int)c.K;
+            descs.push_back(g);
+        }
+    return plan_batched(c.qt, BF_OUT_F32, (int)descs.size(), descs.data(), bp);
+}
+
+// Any 256-byte aligned address: a plan's kernels depend on A's alignment only.
+const uint16_t* const kStagePlaceholder = (const uint16_t*)(uintptr_t)0x100000;
+
+bf_status enqueue_ggml(const GgmlCall& c, const bf_ggml_tensor* s1, uint16_t* staged, const BatchedPlan& bp,
+                       const bf::Scratch* scratch, hipStream_t hs) {
+    if (c.stage) {
+        const bf_status st = from_hip(bf::stage_rows_f16(s1->data, s1->type == BF_GGML_F32, s1->ne, s1->nb, staged, hs),
+                                      "ggml mul_mat: staging src1");
+        if (st != BF_OK) return st;
+    }
+    return launch_batched(bp, scratch, hs);
+}
 }  // namespace
 
 extern "C" {
@@ -694,6 +811,67 @@ bf_status bf_dequant_f16(bf_qtype qtype, const void* W, const void* W_aux, uint1
     return from_hip(bf::dequant_f16((int)qtype, (const uint8_t*)W, (const uint8_t*)W_aux, W_f16, N, K,
                                     (hipStream_t)stream),
                     "dequant launch");
+}
+
+
+bf_status bf_ggml_mul_mat(const bf_ggml_tensor* src0, const bf_ggml_tensor* src1, const bf_ggml_tensor* dst,
+                          void* stream) {
+    g_last_error[0] = '\0';
+    GgmlCall c;
+    bf_status st = check_ggml(src0, src1, dst, c);
+    if (st != BF_OK) return st;
+    hipStream_t hs = (hipStream_t)stream;
+    uint16_t* staged = nullptr;
+    if (c.stage) {
+        const hipError_t e = bf::staging_buffer(hs, c.stage_bytes, &staged);
+        if (e == hipErrorStreamCaptureUnsupported)
+            return fail(BF_ERR_UNSUPPORTED, "ggml mul_mat: the staging buffer for this stream is allocated on first "
+                                            "use, which cannot happen during stream capture; make one uncaptured call "
+                                            "of this size (or a larger one) on the stream first");
+        st = from_hip(e, "ggml mul_mat: staging buffer");
+        if (st != BF_OK) return st;
+    }
+    BatchedPlan bp;
+    st = plan_ggml(c, src0, src1, dst, staged, bp);
+    if (st != BF_OK) return st;
+    st = from_split(bf::reserve_workspace(hs, batched_ws_need(bp)), "bf_ggml_mul_mat");
+    if (st != BF_OK) return st;
+    return enqueue_ggml(c, src1, staged, bp, nullptr, hs);
+}
+
+size_t bf_ggml_mul_mat_workspace_bytes(const bf_ggml_tensor* src0, const bf_ggml_tensor* src1,
+                                       const bf_ggml_tensor* dst) {
+    g_last_error[0] = '\0';
+    GgmlCall c;
+    BatchedPlan bp;
+    if (check_ggml(src0, src1, dst, c) != BF_OK || plan_ggml(c, src0, src1, dst, kStagePlaceholder, bp) != BF_OK)
+        return 0;
+    const size_t need = batched_scratch_need(bp);
+    return need || c.stage_bytes ? align256(need) + c.stage_bytes : 0;
+}
+
+bf_status bf_ggml_mul_mat_ws(const bf_ggml_tensor* src0, const bf_ggml_tensor* src1, const bf_ggml_tensor* dst,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+    g_last_error[0] = '\0';
+    bf_status st = check_workspace(workspace, workspace_bytes);
+    if (st != BF_OK) return st;
+    GgmlCall c;
+    st = check_ggml(src0, src1, dst, c);
+    if (st != BF_OK) return st;
+    // the GEMMs' workspace first, the staging buffer behind it
+    BatchedPlan probe;
+    st = plan_ggml(c, src0, src1, dst, kStagePlaceholder, probe);
+    if (st != BF_OK) return st;
+    const size_t need = align256(batched_scratch_need(probe));
+    if (need + c.stage_bytes > workspace_bytes)
+        return fail(BF_ERR_INVALID, "bf_ggml_mul_mat_ws: the call needs %zu bytes of workspace, %zu given",
+                    need + c.stage_bytes, workspace_bytes);
+    uint16_t* staged = c.stage ? (uint16_t*)((uint8_t*)workspace + need) : nullptr;
+    BatchedPlan bp;
+    st = plan_ggml(c, src0, src1, dst, staged, bp);
+    if (st != BF_OK) return st;
+    const bf::Scratch sc{(uint8_t*)workspace, need};
+    return enqueue_ggml(c, src1, staged, bp, need ? &sc : nullptr, (hipStream_t)stream);
 }
 
 const char* bf_status_str(bf_status s) {

@@ -107,6 +107,17 @@ WsNeed dense_batched_ws_need(const GemmArgs* gs, int n);
 
 hipError_t dequant_f16(int qtype, const uint8_t* W, const uint8_t* Waux, uint16_t* out,
                        int N, int K, hipStream_t st);
+
+// ggml mul_mat hook: the rows of a strided fp32 (f32 = 1) or fp16 tensor
+// (ne[4] elements, nb[4] byte strides, as ggml's ne / nb) rounded to fp16
+// (nearest even) into dst[(i3 ne[2] + i2) ne[1] + i1][0:ne[0]] (ne[0] % 8 == 0,
+// dst 16-byte aligned); and the stream's staging buffer for them (the
+// library's, one per (device, stream) as its workspace; grown on demand, a
+// replaced one retired, never freed; hipErrorStreamCaptureUnsupported when it
+// would have to grow while the stream is capturing).
+hipError_t stage_rows_f16(const void* src, int f32, const int64_t ne[4], const uint64_t nb[4], uint16_t* dst,
+                          hipStream_t st);
+hipError_t staging_buffer(hipStream_t st, size_t bytes, uint16_t** out);
 // A = SiLU(A[:, 0:K]) * A[:, K:2K] formed while loading (batch 1-2 plans that
 // load A through the compute waves), and the standalone elementwise kernel.
 hipError_t gemm_lds_swiglu(const GemmArgs& g, hipStream_t st);

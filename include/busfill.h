@@ -359,6 +359,58 @@ bf_status bf_gguf_get_str(const bf_gguf* g, const char* key, const char** out, u
  * waits for the copy. */
 bf_status bf_gguf_upload(const bf_gguf* g, const bf_gguf_tensor* t, void* dst, void* stream);
 
+/* ggml mul_mat hook: the branch an engine built on ggml's HIP backend adds to
+ * its mul_mat dispatch (ggml-cuda.cu's ggml_cuda_mul_mat) for quantized
+ * weights.  No counterpart in the reference, whose end-to-end figures come
+ * from a patched llama.cpp that it does not ship (RESULTS.md:66-68).
+ *
+ * A tensor as ggml describes it: ggml's type code, the device address, and
+ * ggml_tensor's ne[4] (elements per dimension, ne[0] innermost) and nb[4]
+ * (byte strides), with the meaning those fields have in ggml. */
+typedef enum {
+    BF_GGML_F32 = 0,
+    BF_GGML_F16 = 1,
+    BF_GGML_Q4_0 = 2,    /* block_q4_0 rows: BF_Q4_0 */
+    BF_GGML_Q4_K = 12    /* block_q4_K rows: BF_Q4_K */
+} bf_ggml_type;
+
+typedef struct {
+    int32_t type;        /* a bf_ggml_type code */
+    void* data;          /* device address (read only for src0 and src1) */
+    int64_t ne[4];
+    uint64_t nb[4];
+} bf_ggml_tensor;
+
+/* dst = ggml_mul_mat(src0, src1) on `stream`, with ggml's semantics:
+ *   dst[i3][i2][i1][i0] = sum_k dequant(src0)[i3 / r3][i2 / r2][i0][k] * src1[i3][i2][i1][k],
+ * r2 = src1.ne[2] / src0.ne[2], r3 = src1.ne[3] / src0.ne[3] (src0 broadcast
+ * over src1's outer dimensions, as ggml_can_mul_mat allows), dst.ne =
+ * {src0.ne[1], src1.ne[1], src1.ne[2], src1.ne[3]}.  src1 is F32 or F16 with
+ * any strides: it is rounded to fp16 (round to nearest even, as ggml's own
+ * conversion) into a staging buffer unless it is already fp16 rows the GEMM
+ * can read in place (16-byte aligned, row stride a multiple of 16 bytes);
+ * each (i2, i3) slice is then one GEMM of bf_gemm_batched, with bf_gemm's
+ * bits for the fp16 activations.
+ * Serves src0 Q4_0 / Q4_K with whole rows (nb[0] the block size, nb[1] the
+ * row's bytes), dst F32 with nb[0] = 4 and slices that do not overlap; any
+ * other type or layout returns BF_ERR_UNSUPPORTED (the engine keeps its own
+ * kernels for it), shapes ggml_mul_mat would reject BF_ERR_INVALID; both
+ * before anything is enqueued.  The staging buffer is the library's, one per
+ * (device, stream) as for bf_gemm's workspace. */
+bf_status bf_ggml_mul_mat(const bf_ggml_tensor* src0, const bf_ggml_tensor* src1, const bf_ggml_tensor* dst,
+                          void* stream);
+
+/* Bytes of caller-owned workspace bf_ggml_mul_mat_ws needs (staging buffer
+ * and the GEMMs' workspace; 0: none, also for requests bf_ggml_mul_mat_ws
+ * rejects). */
+size_t bf_ggml_mul_mat_workspace_bytes(const bf_ggml_tensor* src0, const bf_ggml_tensor* src1,
+                                       const bf_ggml_tensor* dst);
+
+/* bf_ggml_mul_mat with a caller-owned workspace (an engine's memory pool), as
+ * bf_gemm_ws: allocates nothing, keeps no state, the same bits. */
+bf_status bf_ggml_mul_mat_ws(const bf_ggml_tensor* src0, const bf_ggml_tensor* src1, const bf_ggml_tensor* dst,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* Static text for a status code. */
 const char* bf_status_str(bf_status status);
 

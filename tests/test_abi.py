@@ -224,3 +224,69 @@ def test_workspace_entries_validate_before_any_launch():
     assert L.bf_gemm_batched_workspace_bytes(bf.Q4_K, bf.OUT_F32, -1, None) == 0
     assert L.bf_gemm_workspace_bytes(bf.Q4_K, bf.OUT_F32, 32, 5120, 5000) == 0      # K % 256 != 0
     assert L.bf_gemm_workspace_bytes(7, bf.OUT_F32, 32, 5120, 5120) == 0            # unknown format
+
+
+def test_ggml_tensor_layout_matches_header():
+    # type at 0, data at 8, ne[4] at 16, nb[4] at 48: 80 bytes
+    assert ctypes.sizeof(bf.GgmlTensor) == 80
+    assert bf.GgmlTensor.ne.offset == 16 and bf.GgmlTensor.nb.offset == 48
+    assert "bf_ggml_tensor" in HDR
+    for name, code in (("BF_GGML_F32", 0), ("BF_GGML_F16", 1), ("BF_GGML_Q4_0", 2), ("BF_GGML_Q4_K", 12)):
+        assert re.search(rf"\b{name} = {code}\b", HDR), name
+
+
+def _ggml_case(K=512, N=64, M=4, t0=bf.GGML_Q4_K, t1=bf.GGML_F32, ne2=(1, 1), nr=(1, 1)):
+    """Valid views (fake addresses) of a Q4 src0 [r2 r3 slices][N][K], an
+    src1 [ne2 x ne3][M][K] and an F32 dst."""
+    blk, bb = (256, 144) if t0 == bf.GGML_Q4_K else (32, 18)
+    rb = K // blk * bb
+    s0 = bf.ggml_tensor(t0, FAKE, [K, N, ne2[0] // nr[0], ne2[1] // nr[1]], [bb, rb])
+    es = 4 if t1 == bf.GGML_F32 else 2
+    s1 = bf.ggml_tensor(t1, FAKE, [K, M, ne2[0], ne2[1]], [es, es * K])
+    d = bf.ggml_tensor(bf.GGML_F32, FAKE, [N, M, ne2[0], ne2[1]], [4, 4 * N])
+    return s0, s1, d
+
+
+@pytest.mark.parametrize("edit,status,needle", [
+    (lambda s0, s1, d: setattr(s0, "type", bf.GGML_F32), bf.ERR_UNSUPPORTED, "src0 type"),
+    (lambda s0, s1, d: setattr(s1, "type", bf.GGML_Q4_0), bf.ERR_UNSUPPORTED, "src1 type"),
+    (lambda s0, s1, d: setattr(d, "type", bf.GGML_F16), bf.ERR_UNSUPPORTED, "dst type"),
+    (lambda s0, s1, d: s1.ne.__setitem__(0, 256), bf.ERR_INVALID, "ne[0]"),
+    (lambda s0, s1, d: (s0.ne.__setitem__(2, 2), s1.ne.__setitem__(2, 3)), bf.ERR_INVALID, "multiples"),
+    (lambda s0, s1, d: d.ne.__setitem__(1, 5), bf.ERR_INVALID, "dst ne"),
+    (lambda s0, s1, d: s0.ne.__setitem__(1, 0), bf.ERR_INVALID, "ne[1]=0"),
+    (lambda s0, s1, d: setattr(s1, "data", None), bf.ERR_INVALID, "NULL"),
+    (lambda s0, s1, d: s0.nb.__setitem__(1, 2 * 288), bf.ERR_UNSUPPORTED, "contiguous blocks"),
+    (lambda s0, s1, d: d.nb.__setitem__(0, 8), bf.ERR_UNSUPPORTED, "F32 rows"),
+    (lambda s0, s1, d: d.nb.__setitem__(1, 4 * 63), bf.ERR_UNSUPPORTED, "F32 rows"),
+    (lambda s0, s1, d: s1.nb.__setitem__(1, 4 * 512 + 2), bf.ERR_UNSUPPORTED, "element size"),
+])
+def test_ggml_mul_mat_rejects_before_any_launch(edit, status, needle):
+    s0, s1, d = _ggml_case()
+    edit(s0, s1, d)
+    L = bf.lib()
+    st = L.bf_ggml_mul_mat(ctypes.byref(s0), ctypes.byref(s1), ctypes.byref(d), None)
+    assert st == status, L.bf_last_error()
+    assert needle in L.bf_last_error().decode()
+    assert L.bf_ggml_mul_mat_workspace_bytes(ctypes.byref(s0), ctypes.byref(s1), ctypes.byref(d)) == 0
+
+
+def test_ggml_mul_mat_shape_rules():
+    """ggml_can_mul_mat: K must match and src1's outer dimensions be multiples
+    of src0's (broadcast); Q4_K rows are whole 256-weight blocks; overlapping
+    dst slices and a NULL tensor are refused."""
+    L = bf.lib()
+    s0, s1, d = _ggml_case(ne2=(6, 2), nr=(3, 2))
+    s1.ne[3] = 3   # 3 % 1 == 0 but dst ne[3] still 2
+    assert L.bf_ggml_mul_mat(ctypes.byref(s0), ctypes.byref(s1), ctypes.byref(d), None) == bf.ERR_INVALID
+    s0, s1, d = _ggml_case(K=288, t0=bf.GGML_Q4_K)
+    assert L.bf_ggml_mul_mat(ctypes.byref(s0), ctypes.byref(s1), ctypes.byref(d), None) == bf.ERR_INVALID
+    assert b"whole blocks" in L.bf_last_error()
+    s0, s1, d = _ggml_case(ne2=(2, 1))
+    d.nb[2] = 4 * 64 * 3   # slices 3 rows apart, 4 rows each
+    assert L.bf_ggml_mul_mat(ctypes.byref(s0), ctypes.byref(s1), ctypes.byref(d), None) == bf.ERR_UNSUPPORTED
+    assert b"overlap" in L.bf_last_error()
+    assert L.bf_ggml_mul_mat(None, ctypes.byref(s1), ctypes.byref(d), None) == bf.ERR_INVALID
+    s0, s1, d = _ggml_case()
+    st = L.bf_ggml_mul_mat_ws(ctypes.byref(s0), ctypes.byref(s1), ctypes.byref(d), None, 4096, None)
+    assert st == bf.ERR_INVALID and b"NULL" in L.bf_last_error()
