@@ -22,8 +22,8 @@ figures beside it (`*_events`); `cpu_baseline` is the oracle's CPU dequantize-th
 this host on a bounded sample of the same workload.
 
 Other workloads (--workload): q4_0 (18-byte blocks), planes (the reference
-layout), layer (one 27B-class decoder layer's Q4_K linears at M = 32) and sweep
-(M = 1..128 on 5120x17408 and 17408x5120).
+layout), layer (one 27B-class decoder layer's Q4_K linears at M = 32), sweep
+(M = 1..128 on 5120x17408 and 17408x5120) and ggml (the ggml mul_mat hook).
 """
 from __future__ import annotations
 
@@ -130,9 +130,10 @@ def bench_lib():
     L.bfb_copy.argtypes = [vp, vp, ctypes.c_size_t, i, vp, d]
     L.bfb_time_q8.argtypes = [i, vp, vp, i, vp, vp, vp, i, i, i, i, i, i, vp, d]
     L.bfb_time_ffn.argtypes = [i, vp, vp, vp, vp, vp, vp, i, vp, vp, vp, i, i, i, i, i, i, i, i, vp, d]
+    L.bfb_time_ggml.argtypes = [i, vp, i, vp, vp, vp, i, i, i, i, i, i, vp, d]
     L.bfb_last_error.restype = ctypes.c_char_p
     for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_time_sequence_batched", "bfb_read_peak", "bfb_read_slices",
-              "bfb_copy", "bfb_time_swiglu", "bfb_time_q8", "bfb_time_ffn"):
+              "bfb_copy", "bfb_time_swiglu", "bfb_time_q8", "bfb_time_ffn", "bfb_time_ggml"):
         getattr(L, f).restype = i
     return L
 
@@ -559,6 +560,36 @@ def run_q8(L, args, dev):
     return res
 
 
+def run_ggml(L, args, dev):
+    """The ggml mul_mat hook on the default GEMM (Q4_K 5120x5120 over the
+    rotation): bf_ggml_mul_mat with F32 src1 (staged to fp16, a second launch)
+    and with F16 src1 (read in place), against bf_gemm on the fp16 rows."""
+    import torch
+    N = K = 5120
+    rot = Rotation("q4_k", N, K, ROTATION_BYTES, seed=N, dev=dev)
+    W, _ = rot.ptr_arrays()
+    res = []
+    for M in [int(x) for x in (args.batches or "1,8,32").split(",")]:
+        A32 = torch.randn((M, K), device=dev)
+        A16 = A32.half()
+        C = torch.empty((M, N), device=dev, dtype=torch.float32)
+        r = {"M": M, "N": N, "K": K, "calls_per_pass": rot.count}
+        for mode, key in ((0, "bf_gemm_us"), (2, "ggml_f16_us"), (1, "ggml_f32_us")):
+            ms = ctypes.c_double()
+            torch.cuda.synchronize()
+            rc = L.bfb_time_ggml(QT["q4_k"], P(W), rot.count, A32.data_ptr(), A16.data_ptr(), C.data_ptr(), M, N, K,
+                                 mode, args.warmup * rot.count, args.steps * rot.count, stream_handle(),
+                                 ctypes.byref(ms))
+            torch.cuda.synchronize()
+            if rc != 0:
+                raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+            r[key] = round(ms.value * 1e3 / (args.steps * rot.count), 3)
+        log(f"[bench] ggml hook M={M:2d}: bf_gemm {r['bf_gemm_us']:.2f} us, F16 src1 {r['ggml_f16_us']:.2f} us, "
+            f"F32 src1 (staged) {r['ggml_f32_us']:.2f} us")
+        res.append(r)
+    return res
+
+
 SWEEP_SHAPES = "17408x5120,5120x17408"
 SWEEP_BATCHES = "1,2,3,4,6,8,16,32,64,128"
 
@@ -684,7 +715,7 @@ def main():
                     help="timed passes over the >= 1 GB weight rotation per configuration (one GEMM per matrix)")
     ap.add_argument("--warmup", type=int, default=3, help="untimed passes before the timed ones")
     ap.add_argument("--workload", default="q4_k",
-                    choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy", "swiglu", "q8", "ffn"])
+                    choices=["q4_k", "q4_0", "planes", "layer", "sweep", "copy", "swiglu", "q8", "ffn", "ggml"])
     ap.add_argument("--batches", default=None,
                     help="batch rows M to time (default 1,8,32; sweep: " + SWEEP_BATCHES + ")")
     ap.add_argument("--shapes", default=None,
@@ -822,6 +853,16 @@ def main():
                   "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
                   "data": "synthetic",
                   "config": {"workload": "q4_k N=5120 K=5120, M=1-16, value at M=8"}, "runs": recs}
+    elif args.workload == "ggml":
+        recs = run_ggml(L, args, dev)
+        head = recs[0]
+        record = {"metric": "ggml mul_mat hook, Q4_K 5120x5120, F32 src1: us per call",
+                  "value": head["ggml_f32_us"], "unit": "us", "n_gpus": 1, "steps": args.steps,
+                  "warmup": args.warmup, "ms_per_step": round(head["ggml_f32_us"] * head["calls_per_pass"] / 1e3, 6),
+                  "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+                  "data": "synthetic",
+                  "config": {"workload": f"q4_k N=5120 K=5120 through bf_ggml_mul_mat, value at M={head['M']}"},
+                  "runs": recs}
     else:
         recs = run_sweep(L, args, dev)
         record = {"metric": "Q4_K GEMM batch sweep: weight-stream GB/s and MFMA utilisation",

@@ -364,6 +364,57 @@ int bfb_time_q8(int qtype, const void* const* W, const void* const* W_aux, int c
     return 0;
 }
 
+// The ggml mul_mat hook over the rotation (src0 Q4_0 / Q4_K rows, one matrix
+// per call, dst [M][N] F32): mode 0 bf_gemm on fp16 activations A16 (the hook's
+// GEMM alone), 1 bf_ggml_mul_mat with F32 src1 A32 (staged to fp16 first),
+// 2 bf_ggml_mul_mat with F16 src1 A16 (read in place).
+int bfb_time_ggml(int qtype, const void* const* W, int count, const float* A32, const uint16_t* A16, float* C,
+                  int M, int N, int K, int mode, int warmup, int steps, void* stream, double* ms_out) {
+    hipStream_t st = (hipStream_t)stream;
+    const int blk = qtype == BF_Q4_K ? 256 : 32, bb = qtype == BF_Q4_K ? 144 : 18;
+    bf_ggml_tensor s0 = {}, s1 = {}, d = {};
+    s0.type = qtype == BF_Q4_K ? BF_GGML_Q4_K : BF_GGML_Q4_0;
+    s1.type = mode == 1 ? BF_GGML_F32 : BF_GGML_F16;
+    d.type = BF_GGML_F32;
+    const int64_t ne0[4] = {K, N, 1, 1}, ne1[4] = {K, M, 1, 1}, ned[4] = {N, M, 1, 1};
+    const uint64_t es = mode == 1 ? 4 : 2, rb = (uint64_t)K / blk * bb;
+    const uint64_t nb0[4] = {(uint64_t)bb, rb, rb * N, rb * N}, nb1[4] = {es, es * K, es * K * M, es * K * M},
+                   nbd[4] = {4, 4ull * N, 4ull * N * M, 4ull * N * M};
+    for (int i = 0; i < 4; i++) {
+        s0.ne[i] = ne0[i], s0.nb[i] = nb0[i];
+        s1.ne[i] = ne1[i], s1.nb[i] = nb1[i];
+        d.ne[i] = ned[i], d.nb[i] = nbd[i];
+    }
+    s1.data = mode == 1 ? (void*)A32 : (void*)A16;
+    d.data = C;
+    auto call = [&](int r) -> bf_status {
+        const void* w = W[r % count];
+        if (mode == 0) return bf_gemm((bf_qtype)qtype, w, nullptr, A16, K, C, N, BF_OUT_F32, M, N, K, st);
+        s0.data = (void*)w;
+        return bf_ggml_mul_mat(&s0, &s1, &d, st);
+    };
+    for (int r = 0; r < warmup; r++)
+        if ((g_bf = call(r)) != BF_OK) return -1;
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    HCK(hipEventRecord(e0, st));
+    for (int r = warmup; r < warmup + steps; r++)
+        if ((g_bf = call(r)) != BF_OK) {
+            (void)hipEventDestroy(e0);
+            (void)hipEventDestroy(e1);
+            return -1;
+        }
+    HCK(hipEventRecord(e1, st));
+    HCK(hipEventSynchronize(e1));
+    float ms;
+    HCK(hipEventElapsedTime(&ms, e0, e1));
+    *ms_out = ms;
+    HCK(hipEventDestroy(e0));
+    HCK(hipEventDestroy(e1));
+    return 0;
+}
+
 // Streaming reads of `bytes` per launch cycling through `count` buffers src[i]
 // (the weight rotation): the time one launch of that size takes to read its
 // bytes from HBM with nothing else to do.  Grid blocks x threads.
