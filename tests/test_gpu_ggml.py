@@ -163,3 +163,72 @@ def test_ggml_staging_rounding_bit_exact(dev):
     assert np.array_equal(got[rows], want[rows])
     for m, (k, v) in over.items():
         assert got[m, k] == np.float32(np.inf if v > 0 else -np.inf)
+
+
+@pytest.mark.parametrize("own_ws", [True, False], ids=["caller_ws", "library_ws"])
+def test_ggml_call_replays_in_a_graph(dev, own_ws):
+    """The hook captured in a HIP graph (F32 src1 staged, then a K-split GEMM
+    that uses the workspace): after one uncaptured call of the shape, every
+    replay -- src1 rewritten and other work on the stream between -- gives
+    the bits of the uncaptured call on the same src1."""
+    N = K = 5120
+    M = 16
+    w = O.gen_weights(O.Q4_K, N, K, seed=41)
+    Wd = torch.from_numpy(w.W).to(dev)
+    x = torch.randn((M, K), device=dev)
+    d = torch.full((M, N), float("nan"), device=dev)
+    args = (bf.ggml_view(Wd, QK), bf.ggml_view(x), bf.ggml_view(d))
+    nbytes = bf.ggml_mul_mat_workspace_bytes(*args)
+    assert nbytes > M * K * 2                            # staging and the K-split's slots
+    wsb = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    s = torch.cuda.Stream()
+
+    def call():
+        if own_ws:
+            bf.ggml_mul_mat_ws(*args, wsb, nbytes, stream=s)
+        else:
+            bf.ggml_mul_mat(*args, stream=s)
+
+    with torch.cuda.stream(s):
+        call()
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            call()
+        big = torch.zeros(16 << 20, dtype=torch.uint8, device=dev)
+        for r in range(4):
+            x.copy_(torch.randn((M, K), device=dev) * (r + 1))
+            big.add_(1)
+            d.fill_(float("nan"))
+            s.synchronize()
+            g.replay()
+            s.synchronize()
+            got = d.clone()
+            d.fill_(float("nan"))
+            call()
+            s.synchronize()
+            assert torch.isfinite(got).all() and torch.equal(got, d), r
+    torch.cuda.synchronize()
+
+
+def test_ggml_capture_on_a_new_stream_enqueues_nothing(dev):
+    """bf_ggml_mul_mat on a stream with no staging buffer yet, under capture:
+    BF_ERR_UNSUPPORTED and dst untouched; the same call uncaptured then works."""
+    w = O.gen_weights(O.Q4_K, 256, 512, seed=43)
+    Wd = torch.from_numpy(w.W).to(dev)
+    x = torch.randn((3, 512), device=dev)
+    d = torch.full((3, 256), 7.0, device=dev)
+    args = (bf.ggml_view(Wd, QK), bf.ggml_view(x), bf.ggml_view(d))
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        mark = torch.zeros(1, device=dev)
+        with pytest.raises(bf.BusfillError, match="capture"):
+            with torch.cuda.graph(g, stream=s):
+                mark.add_(1)
+                bf.ggml_mul_mat(*args, stream=s)
+        s.synchronize()
+        assert (d.cpu().numpy() == 7.0).all()
+        bf.ggml_mul_mat(*args, stream=s)
+        s.synchronize()
+    assert np.isfinite(d.cpu().numpy()).all()
