@@ -19,7 +19,11 @@ prices the algorithmic bytes (weights + A + C) per launch against the 8 TB/s
 HBM peak, over the per-launch time committed in profiles/kernel_time.json (the
 same event timing from a recorded run of this command), with this run's own
 figures beside it (`*_events`); `cpu_baseline` is the oracle's CPU dequantize-then-matmul timed on
-this host on a bounded sample of the same workload.
+this host on a bounded sample of the same workload.  Two floors measured in the
+same run stand beside them: `same_bytes_read_per_launch` (a plain streaming
+read of one matrix's bytes per launch over the rotation, best of a few grids)
+and `empty_kernel_per_launch` (back-to-back launches of a kernel that touches no
+memory: the stream's per-kernel dispatch-and-completion cost).
 
 Other workloads (--workload): q4_0 (18-byte blocks), planes (the reference
 layout), layer (one 27B-class decoder layer's Q4_K linears at M = 32), sweep
@@ -131,9 +135,11 @@ def bench_lib():
     L.bfb_time_q8.argtypes = [i, vp, vp, i, vp, vp, vp, i, i, i, i, i, i, vp, d]
     L.bfb_time_ffn.argtypes = [i, vp, vp, vp, vp, vp, vp, i, vp, vp, vp, i, i, i, i, i, i, i, i, vp, d]
     L.bfb_time_ggml.argtypes = [i, vp, i, vp, vp, vp, i, i, i, i, i, i, vp, d]
+    L.bfb_empty_launches.argtypes = [i, i, i, i, vp, vp, d]
     L.bfb_last_error.restype = ctypes.c_char_p
     for f in ("bfb_time_gemms", "bfb_time_sequence", "bfb_time_sequence_batched", "bfb_read_peak", "bfb_read_slices",
-              "bfb_copy", "bfb_time_swiglu", "bfb_time_q8", "bfb_time_ffn", "bfb_time_ggml"):
+              "bfb_copy", "bfb_time_swiglu", "bfb_time_q8", "bfb_time_ffn", "bfb_time_ggml",
+              "bfb_empty_launches"):
         getattr(L, f).restype = i
     return L
 
@@ -242,6 +248,19 @@ def read_floor(L, rot, steps, warmup):
             best_us, best_grid = us, (blocks, threads)
     return {"us_per_launch": round(best_us, 4), "GBps": round(rot.wbytes / (best_us / 1e6) / 1e9, 1),
             "bytes": rot.wbytes, "grid": list(best_grid)}
+
+
+def empty_launch(L, steps):
+    """Back-to-back launches of a kernel that touches no memory, with the
+    batch-1 GEMM's grid (256 x 1024): the per-launch floor of any kernel on
+    the stream (dispatch and completion), below which no GEMM launch goes."""
+    import torch
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ms = ctypes.c_double()
+    rc = L.bfb_empty_launches(256, 1024, 200, steps, sink.data_ptr(), stream_handle(), ctypes.byref(ms))
+    if rc != 0:
+        raise RuntimeError("bench host: " + L.bfb_last_error().decode())
+    return {"us_per_launch": round(ms.value * 1e3 / steps, 4), "grid": [256, 1024]}
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -791,6 +810,7 @@ def main():
             "all_runs": recs,
             "hbm_read_measured_GBps": round(peak, 1),
             "same_bytes_read_per_launch": rot.floor,
+            "empty_kernel_per_launch": empty_launch(L, 2000),
             "roofline": roofline_record(f"{fmt}_5120_m{head['M']}", alg_bytes, t),
         }
         if args.kernel_time_out:

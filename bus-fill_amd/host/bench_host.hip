@@ -198,6 +198,12 @@ __global__ __launch_bounds__(1024) void k_stream_read(const uint4* __restrict__ 
     if (acc == 0x9E3779B9u) sink[0] = acc;   // keeps the loads live; practically never taken
 }
 
+// No memory access at all (the condition is on an argument the host never
+// sets): back-to-back launches of it time a stream's per-kernel floor.
+__global__ __launch_bounds__(1024) void k_empty(unsigned* __restrict__ sink, int never) {
+    if (never == 0x5EED && threadIdx.x == 0) sink[0] = 1u;
+}
+
 __global__ __launch_bounds__(256) void k_stream_copy(const uint4* __restrict__ src, uint4* __restrict__ dst,
                                                      size_t n16) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
@@ -405,6 +411,34 @@ int bfb_time_ggml(int qtype, const void* const* W, int count, const float* A32, 
             (void)hipEventDestroy(e1);
             return -1;
         }
+    HCK(hipEventRecord(e1, st));
+    HCK(hipEventSynchronize(e1));
+    float ms;
+    HCK(hipEventElapsedTime(&ms, e0, e1));
+    *ms_out = ms;
+    HCK(hipEventDestroy(e0));
+    HCK(hipEventDestroy(e1));
+    return 0;
+}
+
+// `steps` back-to-back launches of k_empty (blocks x threads) after `warmup`:
+// the time per launch that any kernel of that grid takes on the stream.
+int bfb_empty_launches(int blocks, int threads, int warmup, int steps, void* sink, void* stream, double* ms_out) {
+    hipStream_t st = (hipStream_t)stream;
+    if (blocks < 1 || threads < 64 || threads > 1024 || threads % 64) {
+        g_err = hipErrorInvalidValue;
+        return -1;
+    }
+    for (int r = 0; r < warmup; r++)
+        hipLaunchKernelGGL(k_empty, dim3(blocks), dim3(threads), 0, st, (unsigned*)sink, 0);
+    HCK(hipGetLastError());
+    hipEvent_t e0, e1;
+    HCK(hipEventCreate(&e0));
+    HCK(hipEventCreate(&e1));
+    HCK(hipEventRecord(e0, st));
+    for (int r = 0; r < steps; r++)
+        hipLaunchKernelGGL(k_empty, dim3(blocks), dim3(threads), 0, st, (unsigned*)sink, 0);
+    HCK(hipGetLastError());
     HCK(hipEventRecord(e1, st));
     HCK(hipEventSynchronize(e1));
     float ms;
