@@ -495,7 +495,7 @@ bool plan_dense(const GemmArgs& g, DensePlan& p, int cus) {
     if ((g.M * 17 + 63) / 64 > kDnNLA * kDnAQS || (kDnRows * 9 + 63) / 64 > kDnNLW * kDnWQS) return false;
     // Eight compute waves (two per SIMD, on alternate units) where the
     // activation ring holds at least five half-slabs beside the hand-over
-    // area (M <= 64); otherwise four, one per SIMD.  5120 x 17408 at
+    // area (M <= 79); otherwise four, one per SIMD.  5120 x 17408 at
     // M = 24 / 32 / 64: 23.3-23.6 / 23.2 / 28.7-29.3 -> 21.7-21.9 / 22.1 /
     // 28.0-28.5 us, the 27B-class layer at M = 32 in one batched call
     // 88.0-91.8 -> 82.4-83.8 us; with four half-slabs (M = 96) eight waves were
@@ -598,10 +598,11 @@ template <int QT>
 hipError_t dispatch_dense_batched(const GemmArgs* gs, const DensePlan* ps, int n, const Scratch* scratch,
                                   hipStream_t st) {
     if (ps[0].nc == 8) {
+        // (the plan gives eight compute waves only where five half-slabs fit: M <= 79)
         if (ps[0].MT == 1) return launch_dense_batched<QT, 1, 8>(gs, ps, n, scratch, st);
         if (ps[0].MT == 2) return launch_dense_batched<QT, 2, 8>(gs, ps, n, scratch, st);
         if (ps[0].MT == 3) return launch_dense_batched<QT, 3, 8>(gs, ps, n, scratch, st);
-        return launch_dense_batched<QT, 4, 8>(gs, ps, n, scratch, st);
+        return hipErrorInvalidValue;
     }
     if (ps[0].MT == 1) return launch_dense_batched<QT, 1, 4>(gs, ps, n, scratch, st);
     if (ps[0].MT == 2) return launch_dense_batched<QT, 2, 4>(gs, ps, n, scratch, st);
@@ -612,10 +613,11 @@ hipError_t dispatch_dense_batched(const GemmArgs* gs, const DensePlan* ps, int n
 template <int QT>
 hipError_t dispatch_dense(const GemmArgs& g, const DensePlan& p, const Scratch* scratch, hipStream_t st) {
     if (p.nc == 8) {
+        // (the plan gives eight compute waves only where five half-slabs fit: M <= 79)
         if (p.MT == 1) return launch_dense<QT, 1, 8>(g, p, scratch, st);
         if (p.MT == 2) return launch_dense<QT, 2, 8>(g, p, scratch, st);
         if (p.MT == 3) return launch_dense<QT, 3, 8>(g, p, scratch, st);
-        return launch_dense<QT, 4, 8>(g, p, scratch, st);
+        return hipErrorInvalidValue;
     }
     if (p.MT == 1) return launch_dense<QT, 1, 4>(g, p, scratch, st);
     if (p.MT == 2) return launch_dense<QT, 2, 4>(g, p, scratch, st);
