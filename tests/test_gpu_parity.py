@@ -365,7 +365,8 @@ def test_dense_batch_parity(dev, qt, N, K):
     dw = upload(w, dev)
     A = O.gen_act(128, K, seed=K + 19)
     ref = Ref(w, A)
-    for M in (1, 9, 17, 32, 33, 48, 64, 65, 96, 100, 128):
+    # (79 / 80: the last batch with two compute waves per SIMD and the first with one)
+    for M in (1, 9, 17, 32, 33, 48, 64, 65, 79, 80, 96, 100, 128):
         C = gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DENSE, dw=dw)
         ref.check(C, f"dense {QT_NAME[qt]} N={N} K={K} M={M}", rows=M, form="f16")
         assert (gpu_gemm(w, A[:M], dev, algo=bf.ALGO_DENSE, dw=dw) == C).all()
