@@ -581,8 +581,9 @@ def run_q8(L, args, dev):
 
 def run_ggml(L, args, dev):
     """The ggml mul_mat hook on the default GEMM (Q4_K 5120x5120 over the
-    rotation): bf_ggml_mul_mat with F32 src1 (staged to fp16, a second launch)
-    and with F16 src1 (read in place), against bf_gemm on the fp16 rows."""
+    rotation): bf_ggml_mul_mat with F32 src1 (at M = 1 rounded by the batch-1
+    kernel as it loads the row, otherwise staged to fp16 by a launch of its
+    own) and with F16 src1 (read in place), against bf_gemm on the fp16 rows."""
     import torch
     N = K = 5120
     rot = Rotation("q4_k", N, K, ROTATION_BYTES, seed=N, dev=dev)
@@ -604,7 +605,7 @@ def run_ggml(L, args, dev):
                 raise RuntimeError("bench host: " + L.bfb_last_error().decode())
             r[key] = round(ms.value * 1e3 / (args.steps * rot.count), 3)
         log(f"[bench] ggml hook M={M:2d}: bf_gemm {r['bf_gemm_us']:.2f} us, F16 src1 {r['ggml_f16_us']:.2f} us, "
-            f"F32 src1 (staged) {r['ggml_f32_us']:.2f} us")
+            f"F32 src1 {r['ggml_f32_us']:.2f} us")
         res.append(r)
     return res
 

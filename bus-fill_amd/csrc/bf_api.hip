@@ -458,6 +458,8 @@ struct GgmlCall {
     int64_t K = 0, N = 0, M = 0, ne2 = 1, ne3 = 1, r2 = 1, r3 = 1;
     bool stage = false;            // src1 goes through the fp16 staging buffer
     size_t stage_bytes = 0;
+    bool fused = false;            // one fp32 row on the batch-1 LDS kernel, rounded as it loads (fg)
+    bf::GemmArgs fg;
 };
 
 constexpr size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -522,6 +524,28 @@ bf_status check_ggml(const bf_ggml_tensor* s0, const bf_ggml_tensor* s1, const b
                 (((uintptr_t)s1->data | s1->nb[1] | s1->nb[2] | s1->nb[3]) & 15) == 0 &&
                 s1->nb[1] / 2 >= (uint64_t)c.K && s1->nb[1] / 2 <= INT32_MAX);
     c.stage_bytes = c.stage ? align256((size_t)(c.M * c.ne2 * c.ne3) * (size_t)c.K * 2) : 0;
+    // One fp32 row (a decode step) where bf_gemm would run the batch-1 LDS
+    // kernel on its fp16 copy: that kernel rounds the row as its compute waves
+    // load it (the same rounding, so the same bits), and no staging launch runs.
+    if (s1->type == BF_GGML_F32 && c.M == 1 && c.ne2 * c.ne3 == 1 && s1->nb[0] == 4 &&
+        ((uintptr_t)s1->data & 15) == 0) {
+        const uint16_t* const fake = (const uint16_t*)(uintptr_t)0x100000;   // an aligned fp16 row (the plan's view)
+        std::vector<Planned> ls;
+        const bf_status st = plan_gemm(c.qt, s0->data, nullptr, fake, (int)c.K, d->data, (int)(d->nb[1] / 4),
+                                       BF_OUT_F32, 1, (int)c.N, (int)c.K, BF_ALGO_AUTO, ls);
+        if (st == BF_OK && ls.size() == 1 && ls[0].use == BF_ALGO_LDS) {
+            bf::GemmArgs g = ls[0].g;
+            g.A = (const uint16_t*)s1->data;
+            g.a_f32 = 1;
+            if (bf::lds_f32_supports(g)) {
+                c.fused = true;
+                c.fg = g;
+                c.stage = false;
+                c.stage_bytes = 0;
+            }
+        }
+        g_last_error[0] = '\0';
+    }
     return BF_OK;
 }
 
@@ -821,6 +845,7 @@ bf_status bf_ggml_mul_mat(const bf_ggml_tensor* src0, const bf_ggml_tensor* src1
     bf_status st = check_ggml(src0, src1, dst, c);
     if (st != BF_OK) return st;
     hipStream_t hs = (hipStream_t)stream;
+    if (c.fused) return from_hip(bf::gemm_lds(c.fg, hs), "ggml mul_mat: kernel launch");
     uint16_t* staged = nullptr;
     if (c.stage) {
         const hipError_t e = bf::staging_buffer(hs, c.stage_bytes, &staged);
@@ -844,7 +869,8 @@ size_t bf_ggml_mul_mat_workspace_bytes(const bf_ggml_tensor* src0, const bf_ggml
     g_last_error[0] = '\0';
     GgmlCall c;
     BatchedPlan bp;
-    if (check_ggml(src0, src1, dst, c) != BF_OK || plan_ggml(c, src0, src1, dst, kStagePlaceholder, bp) != BF_OK)
+    if (check_ggml(src0, src1, dst, c) != BF_OK || c.fused ||
+        plan_ggml(c, src0, src1, dst, kStagePlaceholder, bp) != BF_OK)
         return 0;
     const size_t need = batched_scratch_need(bp);
     return need || c.stage_bytes ? align256(need) + c.stage_bytes : 0;
@@ -858,6 +884,7 @@ bf_status bf_ggml_mul_mat_ws(const bf_ggml_tensor* src0, const bf_ggml_tensor* s
     GgmlCall c;
     st = check_ggml(src0, src1, dst, c);
     if (st != BF_OK) return st;
+    if (c.fused) return from_hip(bf::gemm_lds(c.fg, (hipStream_t)stream), "ggml mul_mat: kernel launch");
     // the GEMMs' workspace first, the staging buffer behind it
     BatchedPlan probe;
     st = plan_ggml(c, src0, src1, dst, kStagePlaceholder, probe);

@@ -224,4 +224,16 @@ __device__ __forceinline__ u4 swiglu8(const uint16_t* g, const uint16_t* u) {
     return swiglu8v(*(const u4*)g, *(const u4*)u);
 }
 
+// Eight fp32 activations (32 bytes, 16-byte aligned) rounded to fp16 (nearest
+// even: the conversion instruction's rounding, as an fp32 -> fp16 copy does).
+__device__ __forceinline__ u4 f32x8_to_f16(const float* x) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v a = *(const f4v*)x, b = *(const f4v*)(x + 4);
+    auto pk = [](float lo, float hi) {
+        return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+    };
+    return u4{pk(a[0], a[1]), pk(a[2], a[3]), pk(b[0], b[1]), pk(b[2], b[3])};
+}
+
 }  // namespace bf

@@ -86,15 +86,17 @@ namespace {
 // wait for the release flag, then load A with device-scope loads.  dep_users
 // workgroups wait; the last of them past its wait clears the words.  CO: C is
 // stored with device-scope stores (written through to the point of coherence:
-// the output is such a dependency's A).
+// the output is such a dependency's A).  AF (batch 1): A is one fp32 row,
+// rounded to fp16 as the compute waves load it.
 template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC, bool SW = false, bool DEP = false,
-          bool CO = false>
+          bool CO = false, bool AF = false>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                          const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
                                          int nslot, int na, int win, const uint8_t* __restrict__ Waux,
                                          void* __restrict__ C, int ldc, int out_f16, unsigned* dep = nullptr,
                                          unsigned dep_n = 0, unsigned dep_users = 0) {
     static_assert(!DEP || BD || AC, "a dependency needs A loaded by the compute waves");
+    static_assert(!AF || (BD && !SW && !DEP), "fp32 activations: the batch-1 form");
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     static_assert(!BD || G == 4, "sub-block rows: four K segments");
     // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
@@ -386,6 +388,10 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             } else if constexpr (SW) {
                 if (P < nsg * 33)
                     *(u4*)(lds + kFlagBytes + 1024 * i + 16 * lane) = swiglu8(A + 256 * sg + 8 * c, A + K + 256 * sg + 8 * c);
+            } else if constexpr (AF) {
+                if (P < nsg * 33)
+                    *(u4*)(lds + kFlagBytes + 1024 * i + 16 * lane) =
+                        f32x8_to_f16((const float*)(const void*)A + 256 * sg + 8 * c);
             } else {
                 if (P < nsg * 33) dma16(A + 256 * sg + 8 * c, lds0 + (uint32_t)(kFlagBytes + 1024 * i));
             }
@@ -781,12 +787,12 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
 // started, so the loaders' second group of steps and every step marker would
 // wait for it.  mo = M | out_f16 << 8 | nsub << 16 | win << 24, sl = nslot |
 // na << 16 (lds_packed_args).
-template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC = false, bool SW = false>
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC = false, bool SW = false, bool AF = false>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, const uint8_t* __restrict__ Waux,
                 void* __restrict__ C, int lda, int ldc, int N, int K, uint32_t mo, uint32_t sl) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    lds_body<QT, G, MT, NC, NL, BD, RG, AC, SW>((int)blockIdx.x, lds, W, A, lda, (int)(mo & 0xFFu), N, K,
+    lds_body<QT, G, MT, NC, NL, BD, RG, AC, SW, false, false, AF>((int)blockIdx.x, lds, W, A, lda, (int)(mo & 0xFFu), N, K,
                                                 (int)((mo >> 16) & 0xFFu), (int)(sl & 0xFFFFu), (int)(sl >> 16),
                                                 (int)(mo >> 24), Waux, C, ldc, (int)((mo >> 8) & 1u));
 }
@@ -836,9 +842,9 @@ bool lds_packed_args(const GemmArgs& g, const LdsPlan& p, uint32_t& mo, uint32_t
     return true;
 }
 
-template <int QT, int G, int MT, bool BD = false, bool RG = false, bool AC = false, bool SW = false>
+template <int QT, int G, int MT, bool BD = false, bool RG = false, bool AC = false, bool SW = false, bool AF = false>
 hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
-    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG, AC, SW>;
+    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG, AC, SW, AF>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -858,6 +864,7 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
 
 template <int QT>
 hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
+    if (g.a_f32) return p.BD ? launch_lds<QT, 4, 1, true, false, false, false, true>(g, p, st) : hipErrorInvalidValue;
     if (p.BD) return launch_lds<QT, 4, 1, true>(g, p, st);
     if (p.RG) {
         if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1, false, true>(g, p, st);
@@ -1102,6 +1109,12 @@ bool lds_supports(const GemmArgs& g) {
     LdsPlan p;
     if (g.qtype == QT_PLANES && ((uintptr_t)g.Waux & 15)) return false;
     return choose_lds(lds_shape(g), p);
+}
+
+bool lds_f32_supports(const GemmArgs& g) {
+    LdsPlan p;
+    if (g.M != 1 || ((uintptr_t)g.A & 15) || (g.qtype == QT_PLANES && ((uintptr_t)g.Waux & 15))) return false;
+    return choose_lds(lds_shape(g), p) && p.BD;
 }
 
 hipError_t gemm_lds(const GemmArgs& g, hipStream_t st) {

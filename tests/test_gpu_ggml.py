@@ -232,3 +232,68 @@ def test_ggml_capture_on_a_new_stream_enqueues_nothing(dev):
         bf.ggml_mul_mat(*args, stream=s)
         s.synchronize()
     assert np.isfinite(d.cpu().numpy()).all()
+
+
+def halfway_row(K, seed):
+    """fp32 activations with every seventh value on an fp16 rounding midpoint
+    (ties to even decide it) and the rest random."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(K).astype(np.float32)
+    h = x.astype(np.float16)
+    up = np.nextafter(h, np.float16(np.inf))
+    mid = ((h.astype(np.float64) + up.astype(np.float64)) / 2).astype(np.float32)   # exact in fp32
+    x[::7] = mid[::7]
+    return x
+
+
+@pytest.mark.parametrize("t0", [QK, Q0], ids=["q4_k", "q4_0"])
+@pytest.mark.parametrize("N,K", [(5120, 5120), (17408, 5120), (5120, 17408)])
+def test_ggml_f32_decode_row_fused(dev, t0, N, K):
+    """One fp32 activation row (a decode step) on the batch-1 kernel: no
+    workspace and no staging launch (the kernel rounds the row as it loads
+    it), and bf_gemm's bits on the row rounded by the oracle, rounding
+    midpoints included."""
+    w = O.gen_weights(OQT[t0], N, K, seed=N + K + t0)
+    Wd = torch.from_numpy(w.W).to(dev)
+    x = halfway_row(K, N + t0)
+    s1 = torch.from_numpy(x).reshape(1, K).to(dev)
+    d = torch.full((1, N), float("nan"), device=dev)
+    args = (bf.ggml_view(Wd, t0), bf.ggml_view(s1), bf.ggml_view(d))
+    assert bf.ggml_mul_mat_workspace_bytes(*args) == 0
+    bf.ggml_mul_mat(*args)
+    A16 = O.f32_to_f16_bits(x).reshape(1, K)
+    C = torch.full((1, N), float("nan"), device=dev)
+    bf.gemm(BQT[t0], Wd, None, torch.from_numpy(A16.view(np.int16)).to(dev), C, 1, N, K)
+    torch.cuda.synchronize()
+    got, ref = d.cpu().numpy(), C.cpu().numpy()
+    assert np.isfinite(got).all() and np.array_equal(got, ref)
+    ok, mae, rfe, nf = O.gate(got.astype(np.float64), O.gemm_f64(w, A16))
+    assert ok, (mae, rfe, nf)
+
+
+def test_ggml_f32_decode_row_captures_on_a_new_stream(dev):
+    """The fused decode-row call needs no buffer, so it captures into a graph
+    on a stream that has run nothing; every replay gives the eager bits."""
+    N = K = 5120
+    w = O.gen_weights(O.Q4_K, N, K, seed=51)
+    Wd = torch.from_numpy(w.W).to(dev)
+    x = torch.from_numpy(halfway_row(K, 52)).reshape(1, K).to(dev)
+    d = torch.full((1, N), float("nan"), device=dev)
+    args = (bf.ggml_view(Wd, QK), bf.ggml_view(x), bf.ggml_view(d))
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            bf.ggml_mul_mat(*args, stream=s)
+        for r in range(3):
+            x.mul_(-1.5)
+            d.fill_(float("nan"))
+            s.synchronize()
+            g.replay()
+            s.synchronize()
+            got = d.clone()
+            d.fill_(float("nan"))
+            bf.ggml_mul_mat(*args, stream=s)
+            s.synchronize()
+            assert torch.isfinite(got).all() and torch.equal(got, d), r
+    torch.cuda.synchronize()
