@@ -524,18 +524,21 @@ bf_status check_ggml(const bf_ggml_tensor* s0, const bf_ggml_tensor* s1, const b
                 (((uintptr_t)s1->data | s1->nb[1] | s1->nb[2] | s1->nb[3]) & 15) == 0 &&
                 s1->nb[1] / 2 >= (uint64_t)c.K && s1->nb[1] / 2 <= INT32_MAX);
     c.stage_bytes = c.stage ? align256((size_t)(c.M * c.ne2 * c.ne3) * (size_t)c.K * 2) : 0;
-    // One fp32 row (a decode step) where bf_gemm would run the batch-1 LDS
-    // kernel on its fp16 copy: that kernel rounds the row as its compute waves
-    // load it (the same rounding, so the same bits), and no staging launch runs.
-    if (s1->type == BF_GGML_F32 && c.M == 1 && c.ne2 * c.ne3 == 1 && s1->nb[0] == 4 &&
-        ((uintptr_t)s1->data & 15) == 0) {
-        const uint16_t* const fake = (const uint16_t*)(uintptr_t)0x100000;   // an aligned fp16 row (the plan's view)
+    // One or two fp32 rows (decode steps) where bf_gemm would run the LDS
+    // kernel on their fp16 copy in a form whose compute waves load all of A:
+    // that kernel rounds the rows as it loads them (the same rounding, so the
+    // same bits), and no staging launch runs.
+    if (s1->type == BF_GGML_F32 && c.M <= 2 && c.ne2 * c.ne3 == 1 && s1->nb[0] == 4 &&
+        (((uintptr_t)s1->data | s1->nb[1]) & 15) == 0 && s1->nb[1] / 4 >= (uint64_t)c.K &&
+        s1->nb[1] / 4 <= INT32_MAX) {
+        const uint16_t* const fake = (const uint16_t*)(uintptr_t)0x100000;   // aligned fp16 rows (the plan's view)
         std::vector<Planned> ls;
         const bf_status st = plan_gemm(c.qt, s0->data, nullptr, fake, (int)c.K, d->data, (int)(d->nb[1] / 4),
-                                       BF_OUT_F32, 1, (int)c.N, (int)c.K, BF_ALGO_AUTO, ls);
+                                       BF_OUT_F32, (int)c.M, (int)c.N, (int)c.K, BF_ALGO_AUTO, ls);
         if (st == BF_OK && ls.size() == 1 && ls[0].use == BF_ALGO_LDS) {
             bf::GemmArgs g = ls[0].g;
             g.A = (const uint16_t*)s1->data;
+            g.lda = (int)(s1->nb[1] / 4);
             g.a_f32 = 1;
             if (bf::lds_f32_supports(g)) {
                 c.fused = true;

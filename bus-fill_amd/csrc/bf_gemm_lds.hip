@@ -86,8 +86,8 @@ namespace {
 // wait for the release flag, then load A with device-scope loads.  dep_users
 // workgroups wait; the last of them past its wait clears the words.  CO: C is
 // stored with device-scope stores (written through to the point of coherence:
-// the output is such a dependency's A).  AF (batch 1): A is one fp32 row,
-// rounded to fp16 as the compute waves load it.
+// the output is such a dependency's A).  AF (with BD or AC): A is fp32 rows
+// (lda in floats), rounded to fp16 as the compute waves load them.
 template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC, bool SW = false, bool DEP = false,
           bool CO = false, bool AF = false>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
@@ -96,7 +96,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                                          void* __restrict__ C, int ldc, int out_f16, unsigned* dep = nullptr,
                                          unsigned dep_n = 0, unsigned dep_users = 0) {
     static_assert(!DEP || BD || AC, "a dependency needs A loaded by the compute waves");
-    static_assert(!AF || (BD && !SW && !DEP), "fp32 activations: the batch-1 form");
+    static_assert(!AF || ((BD || AC) && !SW && !DEP), "fp32 activations: loaded by the compute waves");
     constexpr int R = 16 / G;                          // weight rows (and batch rows) per segment
     static_assert(!BD || G == 4, "sub-block rows: four K segments");
     // floats of one parked partial: batch rows x weight rows (BD: one batch row per m-tile)
@@ -421,6 +421,10 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
             } else if constexpr (SW) {
                 if (P < (uint32_t)PA && c < 32)
                     *(u4*)(lds + kFlagBytes + sg * seg_bytes + (i << 10) + 16 * lane) = swiglu8(src, src + K);
+            } else if constexpr (AF) {
+                if (P < (uint32_t)PA && c < 32)
+                    *(u4*)(lds + kFlagBytes + sg * seg_bytes + (i << 10) + 16 * lane) =
+                        f32x8_to_f16((const float*)(const void*)A + elem);
             } else {
                 if (P < (uint32_t)PA && c < 32) dma16(src, lds0 + (uint32_t)(kFlagBytes + sg * seg_bytes + (i << 10)));
             }
@@ -864,7 +868,11 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
 
 template <int QT>
 hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
-    if (g.a_f32) return p.BD ? launch_lds<QT, 4, 1, true, false, false, false, true>(g, p, st) : hipErrorInvalidValue;
+    if (g.a_f32) {
+        if (p.BD) return launch_lds<QT, 4, 1, true, false, false, false, true>(g, p, st);
+        if (p.AC) return launch_lds<QT, 4, 1, false, false, true, false, true>(g, p, st);
+        return hipErrorInvalidValue;
+    }
     if (p.BD) return launch_lds<QT, 4, 1, true>(g, p, st);
     if (p.RG) {
         if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1, false, true>(g, p, st);
@@ -1113,8 +1121,8 @@ bool lds_supports(const GemmArgs& g) {
 
 bool lds_f32_supports(const GemmArgs& g) {
     LdsPlan p;
-    if (g.M != 1 || ((uintptr_t)g.A & 15) || (g.qtype == QT_PLANES && ((uintptr_t)g.Waux & 15))) return false;
-    return choose_lds(lds_shape(g), p) && p.BD;
+    if (((uintptr_t)g.A & 15) || (g.lda & 3) || (g.qtype == QT_PLANES && ((uintptr_t)g.Waux & 15))) return false;
+    return choose_lds(lds_shape(g), p) && (p.BD || p.AC);
 }
 
 hipError_t gemm_lds(const GemmArgs& g, hipStream_t st) {

@@ -19,7 +19,7 @@ struct GemmArgs {
     int ldc;
     int out_f16;
     int M, N, K;               // M <= 128 per launch (the front end slices larger M)
-    int a_f32 = 0;             // A is fp32 rows (rounded to fp16 as loaded; the batch-1 LDS kernel only)
+    int a_f32 = 0;             // A is fp32 rows, lda in floats (rounded to fp16 as loaded: lds_f32_supports)
 };
 
 // Device memory a call may use for the K-split kernel's workspace instead of
@@ -34,8 +34,9 @@ hipError_t gemm_mfma(const GemmArgs& g, hipStream_t st);
 hipError_t gemm_dot2(const GemmArgs& g, hipStream_t st);
 hipError_t gemm_simple(const GemmArgs& g, hipStream_t st);
 hipError_t gemm_lds(const GemmArgs& g, hipStream_t st);
-// g with a_f32 set: the batch-1 LDS kernel (the one bf_gemm gives g with fp16
-// rows) whose compute waves round the fp32 row to fp16 as they load it.
+// g with a_f32 set: the LDS kernel of bf_gemm's plan for g's shape in a form
+// whose compute waves load all of A (batch 1, and batch 2 where A fits), then
+// rounding the fp32 rows to fp16 as they load them.
 bool lds_f32_supports(const GemmArgs& g);
 bool lds_supports(const GemmArgs& g);
 // Independent GEMMs that all take the same LDS-staged kernel shape (batch 1,

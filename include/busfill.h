@@ -389,9 +389,10 @@ typedef struct {
  * any strides: it is rounded to fp16 (round to nearest even, as ggml's own
  * conversion) into a staging buffer unless it is already fp16 rows the GEMM
  * can read in place (16-byte aligned, row stride a multiple of 16 bytes), or
- * one 16-byte aligned F32 row on the batch-1 kernel, which rounds it as it
- * loads it (no staging launch); each (i2, i3) slice is then one GEMM of
- * bf_gemm_batched, with bf_gemm's bits for the fp16 activations.
+ * one or two 16-byte aligned F32 rows on the small-batch kernel whose compute
+ * waves load all of A, which rounds them as it loads them (no staging launch);
+ * each (i2, i3) slice is then one GEMM of bf_gemm_batched, with bf_gemm's bits
+ * for the fp16 activations.
  * Serves src0 Q4_0 / Q4_K with whole rows (nb[0] the block size, nb[1] the
  * row's bytes), dst F32 with nb[0] = 4 and slices that do not overlap; any
  * other type or layout returns BF_ERR_UNSUPPORTED (the engine keeps its own

@@ -247,23 +247,27 @@ def halfway_row(K, seed):
 
 
 @pytest.mark.parametrize("t0", [QK, Q0], ids=["q4_k", "q4_0"])
-@pytest.mark.parametrize("N,K", [(5120, 5120), (17408, 5120), (5120, 17408)])
-def test_ggml_f32_decode_row_fused(dev, t0, N, K):
-    """One fp32 activation row (a decode step) on the batch-1 kernel: no
-    workspace and no staging launch (the kernel rounds the row as it loads
-    it), and bf_gemm's bits on the row rounded by the oracle, rounding
-    midpoints included."""
+@pytest.mark.parametrize("M,N,K,pad", [(1, 5120, 5120, 0), (1, 17408, 5120, 0), (1, 5120, 17408, 0),
+                                       (2, 5120, 5120, 0), (2, 5120, 5120, 8), (2, 17408, 5120, 0)])
+def test_ggml_f32_decode_row_fused(dev, t0, M, N, K, pad):
+    """One or two fp32 activation rows (decode steps) on the LDS kernel's forms
+    that load all of A through the compute waves: no workspace and no staging
+    launch (the kernel rounds the rows as it loads them; rows pad floats
+    apart beyond K), and bf_gemm's bits on the rows rounded by the oracle,
+    rounding midpoints included."""
     w = O.gen_weights(OQT[t0], N, K, seed=N + K + t0)
     Wd = torch.from_numpy(w.W).to(dev)
-    x = halfway_row(K, N + t0)
-    s1 = torch.from_numpy(x).reshape(1, K).to(dev)
-    d = torch.full((1, N), float("nan"), device=dev)
+    x = np.stack([halfway_row(K, N + t0 + 7 * m) for m in range(M)])
+    base = torch.zeros((M, K + pad), device=dev)
+    base[:, :K] = torch.from_numpy(x).to(dev)
+    s1 = base[:, :K]
+    d = torch.full((M, N), float("nan"), device=dev)
     args = (bf.ggml_view(Wd, t0), bf.ggml_view(s1), bf.ggml_view(d))
     assert bf.ggml_mul_mat_workspace_bytes(*args) == 0
     bf.ggml_mul_mat(*args)
-    A16 = O.f32_to_f16_bits(x).reshape(1, K)
-    C = torch.full((1, N), float("nan"), device=dev)
-    bf.gemm(BQT[t0], Wd, None, torch.from_numpy(A16.view(np.int16)).to(dev), C, 1, N, K)
+    A16 = O.f32_to_f16_bits(x)
+    C = torch.full((M, N), float("nan"), device=dev)
+    bf.gemm(BQT[t0], Wd, None, torch.from_numpy(A16.view(np.int16)).to(dev), C, M, N, K)
     torch.cuda.synchronize()
     got, ref = d.cpu().numpy(), C.cpu().numpy()
     assert np.isfinite(got).all() and np.array_equal(got, ref)
