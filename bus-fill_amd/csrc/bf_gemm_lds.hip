@@ -583,24 +583,39 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         if constexpr (BD) {
             // the step's marker with the step's weight and activation reads right
             // behind it: a wave's LDS reads complete in order, so a nonzero marker
-            // means the reads behind it saw the landed step (one round trip)
-            for (int it = 0;; it++) {
-                int mark;
-                asm volatile("ds_read_b32 %0, %1" : "=v"(mark) : "v"(lds_addr(&flags[kStepMark + e])) : "memory");
-                lds_raw<QT>(raw, w_lds + (e - (int)(((uint32_t)e * inv_nslot) >> 16) * nslot) * kStep + r * 144, kg);
+            // means the reads behind it saw the landed step (one round trip).  Only
+            // the first poll carries the data reads: a wave that finds the step not
+            // landed polls the marker alone and reads the step once it is set (each
+            // poll's data reads would take LDS bandwidth from the loaders' stream)
+            const uint8_t* const wstep = w_lds + (e - (int)(((uint32_t)e * inv_nslot) >> 16) * nslot) * kStep + r * 144;
+            auto read_step = [&]() __attribute__((always_inline)) {
+                lds_raw<QT>(raw, wstep, kg);
                 if (bd_on) {
 #pragma unroll
                     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
                         for (int t = 0; t < 8; t++) abd[mt][t] = *(const h8*)(aseg + arow[mt] + 16 * t);
                 }
+            };
+            bool first = true;
+            for (int it = 0;; it++) {
+                int mark;
+                asm volatile("ds_read_b32 %0, %1" : "=v"(mark) : "v"(lds_addr(&flags[kStepMark + e])) : "memory");
+                if (it == 0) read_step();
                 asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(mark) :: "memory");
-                if (__builtin_amdgcn_readfirstlane(mark) != 0) break;
+                if (__builtin_amdgcn_readfirstlane(mark) != 0) {
+                    first = it == 0;
+                    break;
+                }
                 if (it >= kWaitBound) {
                     mark_poison(flags + kPoison);
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
+            }
+            if (!first) {
+                read_step();
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             }
             // the step's slot is free again (its reads have completed)
             if (lane == 0) asm volatile("ds_write_b32 %0, %1" :: "v"(lds_addr(&flags[kStepMark + e])), "v"(2) : "memory");
