@@ -8,6 +8,10 @@
 #include <cstring>
 #include <algorithm>
 #include <map>
+#include <memory>
+#include <mutex>
+#include <thread>
+#include <tuple>
 #include <vector>
 
 #include "bf_device.h"
@@ -31,6 +35,31 @@ bf_status from_hip(hipError_t e, const char* what) {
 }
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// Held while a call plans, secures its workspace and enqueues its launches:
+// one lock per (device, stream; per host thread for hipStreamPerThread), so
+// the launches of one call stay together on the stream when several host
+// threads call on it.  A call of two or more launches (a kernel and its
+// second-launch sum, a slot fill and its kernel, the ggml hook's staging and
+// its GEMMs) shares the stream's workspace between them; another call's
+// launches in between would overwrite it.  Recursive: an entry point that
+// calls another takes it again.
+std::unique_lock<std::recursive_mutex> stream_lock(void* stream) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, uintptr_t, std::thread::id>, std::unique_ptr<std::recursive_mutex>> locks;
+    const hipStream_t st = (hipStream_t)stream;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    const std::thread::id tid = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+    std::recursive_mutex* m = nullptr;
+    {
+        std::lock_guard<std::mutex> g(mu);
+        std::unique_ptr<std::recursive_mutex>& slot = locks[{dev, (uintptr_t)st, tid}];
+        if (!slot) slot.reset(new std::recursive_mutex);
+        m = slot.get();
+    }
+    return std::unique_lock<std::recursive_mutex>(*m);
+}
 
 // A K-split launch: the one error of its own is a first use of a stream's
 // workspace while the stream is being captured.
@@ -279,6 +308,12 @@ bf_status run_gemm(bf_qtype qtype, const void* W, const void* W_aux, const uint1
     st = plan_gemm(qtype, W, W_aux, A, lda, C, ldc, otype, M, N, K, algo, ls);
     if (st != BF_OK) return st;
     hipStream_t hs = (hipStream_t)stream;
+    // calls on the LDS-staged and other single-launch kernels share nothing
+    // between launches: no lock on the batch 1-8 path
+    bool shares = scratch != nullptr;
+    for (const Planned& l : ls) shares = shares || l.use == BF_ALGO_SPLIT || l.use == BF_ALGO_DENSE;
+    std::unique_lock<std::recursive_mutex> held;
+    if (shares) held = stream_lock(stream);
     st = secure_workspace(ls, scratch, hs, who, holder);
     if (st != BF_OK) return st;
     for (const Planned& l : ls) {
@@ -642,6 +677,7 @@ bf_status bf_gemm_batched(bf_qtype qtype, bf_otype otype, int count, const bf_ge
     bf_status st = plan_batched(qtype, otype, count, descs, bp);
     if (st != BF_OK) return st;
     hipStream_t hs = (hipStream_t)stream;
+    const auto held = stream_lock(stream);
     st = from_split(bf::reserve_workspace(hs, batched_ws_need(bp)), "bf_gemm_batched");
     if (st != BF_OK) return st;
     return launch_batched(bp, nullptr, hs);
@@ -667,6 +703,7 @@ bf_status bf_gemm_batched_ws(bf_qtype qtype, bf_otype otype, int count, const bf
         return fail(BF_ERR_INVALID, "bf_gemm_batched_ws: the call needs %zu bytes of workspace, %zu given", need,
                     workspace_bytes);
     const bf::Scratch sc{(uint8_t*)workspace, workspace_bytes};
+    const auto held = stream_lock(stream);
     return launch_batched(bp, need ? &sc : nullptr, (hipStream_t)stream);
 }
 
@@ -726,6 +763,7 @@ bf_status bf_ffn_swiglu_ex(bf_qtype qtype, bf_qweights gate, bf_qweights up, bf_
         g.K = i < 2 ? K : F;
     }
     const bool fast = fast_eligible(gs[0]) && fast_eligible(gs[1]) && fast_eligible(gs[2]);
+    const auto held = stream_lock(stream);
     if (form == BF_FFN_ONE_LAUNCH) {
         if (!fast || !bf::ffn_lds_supports(gs))
             return fail(BF_ERR_UNSUPPORTED, "one-launch feed-forward block: batch 1-2 with every GEMM on the LDS-staged "
@@ -849,6 +887,7 @@ bf_status bf_ggml_mul_mat(const bf_ggml_tensor* src0, const bf_ggml_tensor* src1
     if (st != BF_OK) return st;
     hipStream_t hs = (hipStream_t)stream;
     if (c.fused) return from_hip(bf::gemm_lds(c.fg, hs), "ggml mul_mat: kernel launch");
+    const auto held = stream_lock(stream);
     uint16_t* staged = nullptr;
     if (c.stage) {
         const hipError_t e = bf::staging_buffer(hs, c.stage_bytes, &staged);
@@ -901,6 +940,7 @@ bf_status bf_ggml_mul_mat_ws(const bf_ggml_tensor* src0, const bf_ggml_tensor* s
     st = plan_ggml(c, src0, src1, dst, staged, bp);
     if (st != BF_OK) return st;
     const bf::Scratch sc{(uint8_t*)workspace, need};
+    const auto held = stream_lock(stream);
     return enqueue_ggml(c, src1, staged, bp, need ? &sc : nullptr, (hipStream_t)stream);
 }
 

@@ -40,7 +40,11 @@
  *         that uses that buffer runs (on another stream, or another replay)
  *         races.
  *     Every call plans all its launches and secures their workspace before
- *     it enqueues the first, so a call that fails enqueues nothing.
+ *     it enqueues the first, so a call that fails enqueues nothing.  A call
+ *     whose launches share workspace (a kernel and its second-launch sum, a
+ *     slot fill and its kernel, the ggml hook's staging and its GEMMs)
+ *     enqueues them under a lock per (device, stream), so calls from several
+ *     host threads on one stream never interleave their launches.
  *   - fp16 values travel as uint16_t bit patterns.
  *   - A is [M][lda] row-major fp16, C is [M][ldc] row-major (fp32 or fp16),
  *     W is [N][K] in the chosen block format: C = A . dequant(W)^T.
@@ -50,8 +54,9 @@
  *     enqueued; a rejected call returns BF_ERR_INVALID and touches nothing.
  *   - Global state: the thread-local text of the last error (bf_last_error),
  *     per-device records that a kernel's LDS limit has been raised and of the
- *     device's XCD and CU counts, the workspaces above, and the per-GPU
- *     address of bf_gemm_noalloc's scratch array.
+ *     device's XCD and CU counts, the workspaces above, the per-stream
+ *     enqueue locks, and the per-GPU address of bf_gemm_noalloc's scratch
+ *     array.
  */
 #ifndef BUSFILL_H
 #define BUSFILL_H

@@ -12,7 +12,9 @@
   nothing and returns BF_ERR_UNSUPPORTED (bf_gemm_batched included, which
   plans all its launches first).
 * Host threads that share one stream while another grows its workspace get
-  the bits of the single-threaded calls.
+  the bits of the single-threaded calls, also when both issue calls of two
+  launches (dense GEMMs and their second-launch sums, the ggml hook's
+  staging and GEMM) that share the stream's workspace.
 All calls go through the C-ABI."""
 import threading
 
@@ -260,3 +262,62 @@ def test_threads_share_a_stream_while_it_grows(dev):
         assert (bits(C) == bits(ref)).all()
     for C in outs_b:
         assert (bits(C) == bits(ref2)).all()
+
+
+def test_threads_interleave_two_launch_calls_on_one_stream(dev):
+    """Two host threads issue calls of two launches each on one stream: dense
+    GEMMs (the kernel, then the second-launch sum of its partial pieces) and
+    ggml mul_mat calls with fp32 activations (a staging launch, then the
+    GEMM), with different operands per thread.  The launches of one call stay
+    together on the stream, so no thread's partials or staged activations are
+    overwritten by the other's between its two launches: every output equals
+    the single-threaded call's bits."""
+    s = new_stream()
+    N, K, M, MG = 5120, 5120, 64, 4
+    ops = []
+    for t in range(2):
+        _, W, aux, _, Ad = case(O.Q4_K, N, K, M, 200 + 10 * t, dev)
+        x = torch.from_numpy(np.random.default_rng(300 + t).standard_normal((MG, K)).astype(np.float32)).to(dev)
+        ops.append((W, Ad, x))
+
+    def gemm_call(t, C):
+        W, Ad, _ = ops[t]
+        bf.gemm(O.Q4_K, W, None, Ad, C, M, N, K, stream=s)
+
+    def ggml_call(t, D):
+        W, _, x = ops[t]
+        bf.ggml_mul_mat(bf.ggml_view(W, bf.GGML_Q4_K), bf.ggml_view(x, bf.GGML_F32), bf.ggml_view(D), stream=s)
+
+    refs = []
+    for t in range(2):
+        C = torch.full((M, N), float("nan"), device=dev)
+        D = torch.full((MG, N), float("nan"), device=dev)
+        gemm_call(t, C)
+        ggml_call(t, D)
+        s.synchronize()
+        assert np.isfinite(C.cpu().numpy()).all() and np.isfinite(D.cpu().numpy()).all()
+        refs.append((bits(C), bits(D)))
+    assert not (refs[0][0] == refs[1][0]).all() and not (refs[0][1] == refs[1][1]).all()
+    outs = [[(torch.full((M, N), float("nan"), device=dev), torch.full((MG, N), float("nan"), device=dev))
+             for _ in range(24)] for _ in range(2)]
+    errors = []
+
+    def run(t):
+        try:
+            for C, D in outs[t]:
+                gemm_call(t, C)
+                ggml_call(t, D)
+        except Exception as e:          # noqa: BLE001 -- reported by the main thread
+            errors.append(e)
+
+    ts = [threading.Thread(target=run, args=(t,)) for t in range(2)]
+    for th in ts:
+        th.start()
+    for th in ts:
+        th.join()
+    s.synchronize()
+    assert not errors, errors
+    for t in range(2):
+        for C, D in outs[t]:
+            assert (bits(C) == refs[t][0]).all()
+            assert (bits(D) == refs[t][1]).all()
