@@ -87,9 +87,11 @@ namespace {
 // workgroups wait; the last of them past its wait clears the words.  CO: C is
 // stored with device-scope stores (written through to the point of coherence:
 // the output is such a dependency's A).  AF (with BD or AC): A is fp32 rows
-// (lda in floats), rounded to fp16 as the compute waves load them.
+// (lda in floats), rounded to fp16 as the compute waves load them.  EA (plans
+// whose steps all have a slot of their own, no step ring): each loader issues
+// the first group's step before the rest of its setup.
 template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC, bool SW = false, bool DEP = false,
-          bool CO = false, bool AF = false>
+          bool CO = false, bool AF = false, bool EA = false>
 __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* __restrict__ W,
                                          const uint16_t* __restrict__ A, int lda, int M, int N, int K, int nsub,
                                          int nslot, int na, int win, const uint8_t* __restrict__ Waux,
@@ -215,6 +217,35 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
         __builtin_amdgcn_s_setprio(3);
         static_assert(NL == 4, "one step of each group per loader");
         const int j = wave;
+        // EA: the first group's step goes out before anything else is computed
+        // (the setup below is a few hundred cycles of instruction issue that
+        // would delay the start of the stream), from the same address pattern
+        // as the loop, which then skips it; not in the last workgroup (rows
+        // past N) nor in step-ring plans (kernels of their own: the added code
+        // measured slower there even where it did not run)
+        bool early = false;
+        if constexpr (EA) {
+            early = (int64_t)(tile0 + nsub) * R <= N && j < S;
+            if (early) {
+                int te0 = 0, se0 = j;
+                if (RG) step_ts(j, te0, se0);
+                else
+                    while (se0 >= nsteps) { se0 -= nsteps; te0++; }
+                const StepBase<QT> base0 = step_base<QT>((int64_t)(tile0 + te0) * R, G * se0, K);
+                const uint32_t m00 = lds0 + (uint32_t)(kFlagBytes + a_bytes);
+                const int b0 = (9 * j) / 4, b1 = (9 * j + 8) / 4;
+#pragma unroll
+                for (int q = 0; q < 3; q++) {
+                    const int b = b0 + q;
+                    if (b > b1) break;
+                    const uint32_t P = 64u * b + lane, d = __umul24(P, 7282u) >> 20, r9 = P - 144u * d;
+                    const uint32_t nn = __umul24(r9, 7282u) >> 16, c = r9 - 9u * nn;
+                    if (d == (uint32_t)j && (int)P < S * 144)
+                        dma16(piece_addr<QT>(W, Waux, base0, step_piece_offset<QT>(nn / G, nn % G, c, K)),
+                              m00 + (uint32_t)(b << 10));
+                }
+            }
+        }
         // touch the workgroup's first weight line before computing any address, so
         // that its translation and DRAM page are under way early (the value is
         // unused; its register stays reserved until the final wait)
@@ -276,7 +307,7 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
                 s_hi = s_next;
                 step_ts(e, te, se);
             }
-            if (e < S) {
+            if (e < S && !(EA && g4 == 0 && early)) {
                 // the slot's previous step must be consumed (its marker set to 2
                 // by the compute wave that read it) before it is overwritten
                 if (e >= nslot) wait_flag_value(&flags[kStepMark + e - nslot], 2, flags + kPoison);
@@ -806,12 +837,13 @@ __device__ __forceinline__ void lds_body(int bid, uint8_t* lds, const uint8_t* _
 // started, so the loaders' second group of steps and every step marker would
 // wait for it.  mo = M | out_f16 << 8 | nsub << 16 | win << 24, sl = nslot |
 // na << 16 (lds_packed_args).
-template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC = false, bool SW = false, bool AF = false>
+template <int QT, int G, int MT, int NC, int NL, bool BD, bool RG, bool AC = false, bool SW = false, bool AF = false,
+          bool EA = false>
 __global__ __launch_bounds__(64 * (NC + NL))
 void k_gemm_lds(const uint8_t* __restrict__ W, const uint16_t* __restrict__ A, const uint8_t* __restrict__ Waux,
                 void* __restrict__ C, int lda, int ldc, int N, int K, uint32_t mo, uint32_t sl) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-    lds_body<QT, G, MT, NC, NL, BD, RG, AC, SW, false, false, AF>((int)blockIdx.x, lds, W, A, lda, (int)(mo & 0xFFu), N, K,
+    lds_body<QT, G, MT, NC, NL, BD, RG, AC, SW, false, false, AF, EA>((int)blockIdx.x, lds, W, A, lda, (int)(mo & 0xFFu), N, K,
                                                 (int)((mo >> 16) & 0xFFu), (int)(sl & 0xFFFFu), (int)(sl >> 16),
                                                 (int)(mo >> 24), Waux, C, ldc, (int)((mo >> 8) & 1u));
 }
@@ -861,9 +893,10 @@ bool lds_packed_args(const GemmArgs& g, const LdsPlan& p, uint32_t& mo, uint32_t
     return true;
 }
 
-template <int QT, int G, int MT, bool BD = false, bool RG = false, bool AC = false, bool SW = false, bool AF = false>
+template <int QT, int G, int MT, bool BD = false, bool RG = false, bool AC = false, bool SW = false, bool AF = false,
+          bool EA = false>
 hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
-    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG, AC, SW, AF>;
+    auto k = k_gemm_lds<QT, G, MT, kNC, kNL, BD, RG, AC, SW, AF, EA>;
     static std::atomic<uint64_t> attr_set{0};          // one bit per device: LDS limit raised
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -888,16 +921,22 @@ hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
         if (p.AC) return launch_lds<QT, 4, 1, false, false, true, false, true>(g, p, st);
         return hipErrorInvalidValue;
     }
-    if (p.BD) return launch_lds<QT, 4, 1, true>(g, p, st);
+    // every step in a slot of its own (no step ring): the loaders' first group early
+    const bool ea = p.nslot >= p.nsub * (g.K / (256 * p.G));
+    if (p.BD) return ea ? launch_lds<QT, 4, 1, true, false, false, false, false, true>(g, p, st)
+                        : launch_lds<QT, 4, 1, true>(g, p, st);
     if (p.RG) {
         if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1, false, true>(g, p, st);
         if (p.G == 4 && p.MT == 2) return launch_lds<QT, 4, 2, false, true>(g, p, st);
         if (p.G == 2 && p.MT == 1) return launch_lds<QT, 2, 1, false, true>(g, p, st);
         return hipErrorInvalidValue;                    // no ring kernel of this shape
     }
-    if (p.AC) return launch_lds<QT, 4, 1, false, false, true>(g, p, st);
-    if (p.G == 4 && p.MT == 1) return launch_lds<QT, 4, 1>(g, p, st);
-    if (p.G == 4 && p.MT == 2) return launch_lds<QT, 4, 2>(g, p, st);
+    if (p.AC) return ea ? launch_lds<QT, 4, 1, false, false, true, false, false, true>(g, p, st)
+                        : launch_lds<QT, 4, 1, false, false, true>(g, p, st);
+    if (p.G == 4 && p.MT == 1) return ea ? launch_lds<QT, 4, 1, false, false, false, false, false, true>(g, p, st)
+                                         : launch_lds<QT, 4, 1>(g, p, st);
+    if (p.G == 4 && p.MT == 2) return ea ? launch_lds<QT, 4, 2, false, false, false, false, false, true>(g, p, st)
+                                         : launch_lds<QT, 4, 2>(g, p, st);
     if (p.G == 2 && p.MT == 1) return launch_lds<QT, 2, 1>(g, p, st);
     return launch_lds<QT, 1, 1>(g, p, st);
 }
