@@ -287,7 +287,9 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
         __builtin_amdgcn_s_setprio(3);
         const int j = wave;
         // instruction q = j + 4 * slot covers pieces 64 q + lane of every unit;
-        // the piece's address in unit i is src + i * step (step 0: lane idle)
+        // the piece's address in unit i is src + i * step (step 0: lane idle).
+        // Unit 0's load of each slot goes out as soon as its address is known
+        // (all slots' addresses take a few hundred cycles of instruction issue).
         const uint8_t* src[kSpQS];
         uint32_t step[kSpQS];
 #pragma unroll
@@ -310,13 +312,15 @@ __device__ __forceinline__ void split_body(int bid, uint8_t* lds, const uint8_t*
                 src[q2] = w_piece<QT>(W, Waux, row, sg0, (int)c, K);
                 step[q2] = QT == QT_PLANES ? (c == 0 ? 16u : 128u) : 144u;
             }
+            const int q = j + 4 * q2;
+            if (q < I && step[q2]) dma16(src[q2], lds0 + (uint32_t)(kSpFlags + (q << 10)));
         }
         for (int i = 0; i < nsgS; i++) {
             const uint32_t ub = lds0 + (uint32_t)(kSpFlags + i * unit_bytes);
 #pragma unroll
             for (int q2 = 0; q2 < kSpQS; q2++) {
                 const int q = j + 4 * q2;
-                if (q >= I) break;
+                if (i == 0 || q >= I) break;
                 if (step[q2]) dma16(src[q2] + (uint32_t)i * step[q2], ub + (uint32_t)(q << 10));
             }
             if (i == 0) clear_flags_and_meet();
