@@ -916,16 +916,18 @@ hipError_t launch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
 
 template <int QT>
 hipError_t dispatch_lds(const GemmArgs& g, const LdsPlan& p, hipStream_t st) {
-    if (g.a_f32) {
-        if (p.BD) return launch_lds<QT, 4, 1, true, false, false, false, true>(g, p, st);
-        if (p.AC) return launch_lds<QT, 4, 1, false, false, true, false, true>(g, p, st);
-        return hipErrorInvalidValue;
-    }
     // Q4_K, every step in a slot of its own (no step ring): the loaders' first
     // group early (the Q4_0 formats measured slower with it: 5120^2 at M = 1 /
     // 8 planes 6.23 / 7.95 -> 6.41 / 8.05-8.48 us, Q4_0 blocks at M = 8 7.84 ->
     // 8.16 us)
     const bool ea = QT == QT_Q4_K && p.nslot >= p.nsub * (g.K / (256 * p.G));
+    if (g.a_f32) {
+        if (p.BD) return ea ? launch_lds<QT, 4, 1, true, false, false, false, true, true>(g, p, st)
+                            : launch_lds<QT, 4, 1, true, false, false, false, true>(g, p, st);
+        if (p.AC) return ea ? launch_lds<QT, 4, 1, false, false, true, false, true, true>(g, p, st)
+                            : launch_lds<QT, 4, 1, false, false, true, false, true>(g, p, st);
+        return hipErrorInvalidValue;
+    }
     if (p.BD) return ea ? launch_lds<QT, 4, 1, true, false, false, false, false, true>(g, p, st)
                         : launch_lds<QT, 4, 1, true>(g, p, st);
     if (p.RG) {
