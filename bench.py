@@ -344,20 +344,40 @@ def kernel_time_from_profiles(key):
     return e if isinstance(e, dict) and e.get("us_per_launch", 0) > 0 else None
 
 
+def library_digest():
+    """The first 16 hex digits of the SHA-256 of the loaded libbusfill.so."""
+    import hashlib
+    import busfill
+    with open(busfill.LIB_PATH, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
 def write_kernel_time(path, fmt, N, K, recs, batches, argv):
     """Merges this run's per-launch times (the best launch mode of each batch
     size: HIP events around the timed passes, divided by the GEMMs timed) into
-    the JSON file at path, one entry per configuration."""
+    the JSON file at path, one entry per configuration.  An entry written by a
+    run of the same library build (the same SHA-256 of libbusfill.so) keeps
+    the best of the runs and counts them (boxes differ by a few percent from
+    one run to the next); a new build starts the entry over."""
     try:
         data = json.load(open(path))
     except (OSError, ValueError):
         data = {}
+    lib = library_digest()
     for M in batches:
         r = best(recs, M)
-        data[f"{fmt}_{N}_m{M}" if N == K else f"{fmt}_{N}x{K}_m{M}"] = {
+        key = f"{fmt}_{N}_m{M}" if N == K else f"{fmt}_{N}x{K}_m{M}"
+        old = data.get(key)
+        same = isinstance(old, dict) and old.get("lib_sha16") == lib
+        runs = old.get("runs", 1) + 1 if same else 1
+        if same and old.get("us_per_launch", 1e30) <= r["us_per_gemm"]:
+            old["runs"] = runs
+            continue
+        data[key] = {
             "us_per_launch": r["us_per_gemm"], "launch": r["launch"], "gemms_timed": r["gemms_timed"],
-            "ms_per_pass": r["ms_per_pass"],
-            "how": "HIP events on the launch stream around the timed passes, / GEMMs timed",
+            "ms_per_pass": r["ms_per_pass"], "lib_sha16": lib, "runs": runs,
+            "how": "HIP events on the launch stream around the timed passes, / GEMMs timed; the best of the "
+                   "runs of this library build",
             "command": "python3 bench.py " + " ".join(argv)}
     with open(path, "w") as f:
         json.dump(data, f, indent=1, sort_keys=True)
