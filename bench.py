@@ -345,11 +345,15 @@ def kernel_time_from_profiles(key):
 
 
 def library_digest():
-    """The first 16 hex digits of the SHA-256 of the loaded libbusfill.so."""
+    """The first 16 hex digits of the SHA-256 of libbusfill.so ("" if it
+    cannot be read: every entry then starts over)."""
     import hashlib
     import busfill
-    with open(busfill.LIB_PATH, "rb") as f:
-        return hashlib.sha256(f.read()).hexdigest()[:16]
+    try:
+        with open(busfill.LIB_PATH, "rb") as f:
+            return hashlib.sha256(f.read()).hexdigest()[:16]
+    except OSError:
+        return ""
 
 
 def write_kernel_time(path, fmt, N, K, recs, batches, argv):
@@ -368,7 +372,7 @@ def write_kernel_time(path, fmt, N, K, recs, batches, argv):
         r = best(recs, M)
         key = f"{fmt}_{N}_m{M}" if N == K else f"{fmt}_{N}x{K}_m{M}"
         old = data.get(key)
-        same = isinstance(old, dict) and old.get("lib_sha16") == lib
+        same = bool(lib) and isinstance(old, dict) and old.get("lib_sha16") == lib
         runs = old.get("runs", 1) + 1 if same else 1
         if same and old.get("us_per_launch", 1e30) <= r["us_per_gemm"]:
             old["runs"] = runs

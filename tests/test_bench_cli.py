@@ -97,6 +97,17 @@ def test_roofline_basis_is_the_committed_kernel_time(tmp_path, monkeypatch):
     d = json.loads(path.read_text())
     assert d["other"]["us_per_launch"] == 1.0
     assert d["q4_k_5120_m1"]["us_per_launch"] == 6.1 and d["q4_k_5120_m1"]["launch"] == "graph"
+    # runs of one library build keep the best time and count the runs; a new build starts over
+    monkeypatch.setattr(bench, "library_digest", lambda: "aaaa")
+    path.write_text("{}")
+    for us in (6.3, 6.1, 6.2):
+        bench.write_kernel_time(str(path), "q4_k", 5120, 5120, [dict(recs[0], us_per_gemm=us)], [1], ["--no-cpu"])
+    e = json.loads(path.read_text())["q4_k_5120_m1"]
+    assert e["us_per_launch"] == 6.1 and e["runs"] == 3 and e["lib_sha16"] == "aaaa"
+    monkeypatch.setattr(bench, "library_digest", lambda: "bbbb")
+    bench.write_kernel_time(str(path), "q4_k", 5120, 5120, [dict(recs[0], us_per_gemm=6.4)], [1], ["--no-cpu"])
+    e = json.loads(path.read_text())["q4_k_5120_m1"]
+    assert e["us_per_launch"] == 6.4 and e["runs"] == 1 and e["lib_sha16"] == "bbbb"
 
 
 def test_counter_summary_means_per_dispatch(tmp_path):
